@@ -1,0 +1,1237 @@
+// C-ABI of the MI355X LoRA-SFT backward: handle, bindings, the per-cycle
+// kernel sequence (captured once as a hipGraph), and single-op entry points.
+//
+// The cycle follows LoraSftTrainerService.process_backward
+// (deltaserve-plugin/deltaserve/bwd_services/common/trainer.py:503-678):
+//   head_backward (common/head.py:42-100)
+//   for i in reversed(range(L)):  layer_forward (llama3.py:62-146 / qwen3.py:68-130)
+//                                 layer_backward (llama3.py:149-219 / qwen3.py:147-204)
+//   per-layer clip (trainer.py:624-636), AdamW step (trainer.py:668)
+// extended to LoRA on all seven projections (q, k, v, o, gate, up, down).
+//
+// Everything the kernels need per cycle (n, tile tables, positions, label
+// flags, optimizer scalars) lives in one device block refreshed by a single
+// host→device copy before the graph launch, so one captured graph serves any
+// n <= s_max and any packing.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/dsb.h"
+#include "gemm_nt.h"
+#include "kernels.h"
+
+namespace dsb {
+
+static thread_local char g_err[2048];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+const char* get_error() { return g_err; }
+
+// ------------------------------------------------------------ small kernels
+
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restrict__ in,
+                                                             long ldi, bf16* __restrict__ out,
+                                                             long ldo, int R, int C) {
+  __shared__ bf16 t[64][66];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + i * 4;
+    if (r0 + r < R && c0 + tx < C) t[r][tx] = in[(long)(r0 + r) * ldi + c0 + tx];
+  }
+  __syncthreads();
+  for (int i = 0; i < 16; ++i) {
+    const int c = ty + i * 4;
+    if (c0 + c < C && r0 + tx < R) out[(long)(c0 + c) * ldo + r0 + tx] = t[tx][c];
+  }
+}
+
+static hipError_t transpose_bf16(const bf16* in, long ldi, bf16* out, long ldo, int R, int C,
+                                 hipStream_t s) {
+  if (R <= 0 || C <= 0) return hipSuccess;
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((C + 63) / 64, (R + 63) / 64), dim3(256), 0, s,
+                     in, ldi, out, ldo, R, C);
+  return hipGetLastError();
+}
+
+// labels[t] = pred[t] ? ids[t + 1] : -1; out-of-range ids raise err bit 1.
+__global__ void labels_kernel(const int64_t* __restrict__ ids, const int* __restrict__ pred,
+                              int* __restrict__ labels, int n, const int* n_dev, int V,
+                              int* err) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N) return;
+  int lab = -1;
+  if (pred[t]) {
+    const int64_t id = ids[t + 1];
+    if (id < 0 || id >= V) {
+      atomicOr(err, 1);
+    } else {
+      lab = (int)id;
+    }
+  }
+  labels[t] = lab;
+}
+
+hipError_t build_labels(const int64_t* ids, const int* pred, int* labels, int n,
+                        const int* n_dev, int V, int* err, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(labels_kernel, dim3((n + 255) / 256), dim3(256), 0, s, ids, pred, labels, n,
+                     n_dev, V, err);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------ host helpers
+
+// Integer packing of a cycle (trainer.py:510-518, head.py:63-72).
+static int pack_cycle(const int32_t* seq_lens, int nseq, int n, int32_t* pos, int32_t* pred,
+                      std::vector<int4>* tiles) {
+  long acc = 0;
+  for (int i = 0; i < nseq; ++i) {
+    if (seq_lens[i] < 0) return -1;
+    acc += seq_lens[i];
+  }
+  if (acc != n) return -1;
+  int st = 0, n_valid = 0;
+  for (int i = 0; i < nseq; ++i) {
+    const int L = seq_lens[i];
+    for (int p = 0; p < L; ++p) {
+      if (pos) pos[st + p] = p;
+      if (pred) pred[st + p] = (p < L - 1) ? 1 : 0;
+    }
+    if (L >= 2) n_valid += L - 1;
+    if (tiles)
+      for (int t0 = 0; t0 < L; t0 += 128) tiles->push_back(int4{st, L, t0, 0});
+    st += L;
+  }
+  return n_valid;
+}
+
+static int max_tiles_for(int s_max, int max_seqs) { return (s_max + 127) / 128 + max_seqs; }
+
+static void rope_inv_freq_host(int hd, float theta, int type, float factor, float low,
+                               float high, float orig, float* out) {
+  const int half = hd / 2;
+  for (int i = 0; i < half; ++i) {
+    const float ex = (float)(2 * i) / (float)hd;
+    float inv = 1.0f / powf(theta, ex);
+    if (type == DSB_ROPE_LINEAR) {
+      inv = inv / factor;
+    } else if (type == DSB_ROPE_LLAMA3) {
+      const double low_wl = (double)orig / low, high_wl = (double)orig / high;
+      const float wl = (float)(2.0 * M_PI) / inv;
+      if (wl < high_wl) {
+        // keep inv
+      } else if (wl > low_wl) {
+        inv = inv / factor;
+      } else {
+        const float smooth = (low != high) ? (orig / wl - low) / (high - low) : 0.f;
+        inv = (1.f - smooth) * inv / factor + smooth * inv;
+      }
+    }
+    out[i] = inv;
+  }
+}
+
+}  // namespace dsb
+
+using namespace dsb;
+
+// ------------------------------------------------------------ the handle
+
+namespace {
+
+struct StepHdr {  // device-resident per-cycle scalars (64 bytes)
+  int n;
+  int ntiles;
+  int n_valid;
+  int err;
+  float inv_nvalid;
+  float loss;
+  int pad[2];
+  OptHyper hyper;
+};
+static_assert(sizeof(StepHdr) == 64, "StepHdr layout");
+
+struct LayerState {
+  dsb_layer_weights w{};
+  bool bound = false;
+  bf16 *qkvT = nullptr, *oT = nullptr, *guT = nullptr, *downT = nullptr;
+  dsb_lora_tensors lora[DSB_NUM_PROJ]{};
+  bool has[DSB_NUM_PROJ]{};
+  bf16 *Aqkv, *AqkvT, *B2qkv, *BTq, *BTk, *BTv;
+  bf16 *Ao, *AoT, *Bo, *BTo;
+  bf16 *Agu, *AguT, *B2gu, *BTg, *BTu;
+  bf16 *Ad, *AdT, *Bd, *BTd;
+};
+
+}  // namespace
+
+struct dsb_handle {
+  dsb_desc d{};
+  int D, Hq, Hkv, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk;
+  float s;
+  bool qwen = false;
+  hipStream_t hs = nullptr;
+  hipEvent_t ev_in = nullptr, ev_out = nullptr, ev_t0 = nullptr, ev_t1 = nullptr;
+  std::vector<LayerState> layers;
+  const bf16* lm_w = nullptr;
+  const bf16* norm_w = nullptr;
+  bf16* lm_wT = nullptr;
+  std::vector<const bf16*> layer_in;
+  const bf16* final_in = nullptr;
+  const int64_t* ids = nullptr;
+  long act_ld = 0;
+  bool finalized = false;
+  std::vector<void*> allocs;
+  // workspace
+  bf16 *xn1, *qkv_pre, *qk, *ctx, *resid, *xn2, *gu, *hb;
+  float *o32, *lse, *dsum;
+  bf16 *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
+  float *Pqkv, *Po, *Pgu, *Pd;
+  bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
+  float *gZd_f, *gZgu_f, *gZo_f, *gZqkv_f;
+  bf16 *g0, *g1, *Ggu, *grm, *gctx, *gqkv;
+  float *gxn2, *gxn1;
+  bf16 *normed, *dlog;
+  float2* stats;
+  float *tgt_logit, *lse_h, *loss_row, *dH;
+  float* tn_work;
+  long tn_work_elems;
+  float *cosb, *sinb, *inv_freq;
+  int* labels;
+  // step staging
+  void* h_stage = nullptr;  // pinned
+  void* d_stage = nullptr;
+  size_t stage_bytes = 0;
+  StepHdr* d_hdr = nullptr;
+  int* d_pos = nullptr;
+  int* d_pred = nullptr;
+  int4* d_tiles = nullptr;
+  // optimizer
+  CastJob* d_jobs = nullptr;
+  int2* d_cast_chunks = nullptr;
+  int ncast_chunks = 0;
+  OptTensor* d_opt = nullptr;
+  int2* d_opt_chunks = nullptr;
+  int nopt_chunks = 0;
+  int nopt_tensors = 0;
+  int2* d_layer_chunks = nullptr;
+  float *d_opt_partial = nullptr, *d_sq = nullptr;
+  // graph
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  bool graph_failed = false;
+  std::mutex mu;
+  std::string err;
+};
+
+namespace {
+
+int fail(dsb_handle* h, const char* msg) {
+  set_error("%s", msg);
+  if (h) h->err = get_error();
+  return -1;
+}
+
+template <class T>
+int dalloc(dsb_handle* h, T** p, size_t count) {
+  void* v = nullptr;
+  const size_t bytes = count * sizeof(T) + 256;
+  hipError_t e = hipMalloc(&v, bytes);
+  if (e != hipSuccess) {
+    set_error("hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    h->err = get_error();
+    return -1;
+  }
+  h->allocs.push_back(v);
+  *p = reinterpret_cast<T*>(v);
+  return 0;
+}
+
+#define CK(expr)                                                                     \
+  do {                                                                               \
+    hipError_t _e = (expr);                                                          \
+    if (_e != hipSuccess) {                                                          \
+      set_error("%s: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, __LINE__); \
+      h->err = get_error();                                                          \
+      return -1;                                                                     \
+    }                                                                                \
+  } while (0)
+
+#define CKR(expr)            \
+  do {                       \
+    if ((expr) != 0) return -1; \
+  } while (0)
+
+int finalize(dsb_handle* h) {
+  if (h->finalized) return 0;
+  for (int i = 0; i < h->L; ++i)
+    if (!h->layers[i].bound) {
+      set_error("layer %d weights not bound", i);
+      h->err = get_error();
+      return -1;
+    }
+  if (!h->lm_w || !h->norm_w) return fail(h, "LM head / final norm not bound");
+  if (!h->final_in || !h->ids || (int)h->layer_in.size() != h->L)
+    return fail(h, "activations not bound");
+  for (int i = 0; i < h->L; ++i) {
+    LayerState& ls = h->layers[i];
+    const bool q = ls.has[DSB_PROJ_Q], k = ls.has[DSB_PROJ_K], v = ls.has[DSB_PROJ_V];
+    if (q != k || q != v) {
+      set_error("layer %d: q/k/v LoRA must be bound together", i);
+      h->err = get_error();
+      return -1;
+    }
+    if (ls.has[DSB_PROJ_GATE] != ls.has[DSB_PROJ_UP]) {
+      set_error("layer %d: gate/up LoRA must be bound together", i);
+      h->err = get_error();
+      return -1;
+    }
+  }
+  const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
+  const long NN = N + 1;
+  CKR(dalloc(h, &h->xn1, NN * D));
+  CKR(dalloc(h, &h->qkv_pre, NN * W3));
+  CKR(dalloc(h, &h->qk, NN * (q + kv)));
+  CKR(dalloc(h, &h->ctx, NN * q));
+  CKR(dalloc(h, &h->o32, NN * q));
+  CKR(dalloc(h, &h->lse, (long)h->Hq * NN));
+  CKR(dalloc(h, &h->dsum, (long)h->Hq * NN));
+  CKR(dalloc(h, &h->resid, NN * D));
+  CKR(dalloc(h, &h->xn2, NN * D));
+  CKR(dalloc(h, &h->gu, NN * 2 * I));
+  CKR(dalloc(h, &h->hb, NN * I));
+  CKR(dalloc(h, &h->Zqkv_b, NN * 3 * r));
+  CKR(dalloc(h, &h->Zo_b, NN * r));
+  CKR(dalloc(h, &h->Zgu_b, NN * 2 * r));
+  CKR(dalloc(h, &h->Zd_b, NN * r));
+  CKR(dalloc(h, &h->Pqkv, NN * 3 * r));
+  CKR(dalloc(h, &h->Po, NN * r));
+  CKR(dalloc(h, &h->Pgu, NN * 2 * r));
+  CKR(dalloc(h, &h->Pd, NN * r));
+  CKR(dalloc(h, &h->gZd_b, NN * r));
+  CKR(dalloc(h, &h->gZgu_b, NN * 2 * r));
+  CKR(dalloc(h, &h->gZo_b, NN * r));
+  CKR(dalloc(h, &h->gZqkv_b, NN * 3 * r));
+  CKR(dalloc(h, &h->gZd_f, NN * r));
+  CKR(dalloc(h, &h->gZgu_f, NN * 2 * r));
+  CKR(dalloc(h, &h->gZo_f, NN * r));
+  CKR(dalloc(h, &h->gZqkv_f, NN * 3 * r));
+  CKR(dalloc(h, &h->g0, NN * D));
+  CKR(dalloc(h, &h->g1, NN * D));
+  CKR(dalloc(h, &h->Ggu, NN * 2 * I));
+  CKR(dalloc(h, &h->grm, NN * D));
+  CKR(dalloc(h, &h->gctx, NN * q));
+  CKR(dalloc(h, &h->gqkv, NN * W3));
+  CKR(dalloc(h, &h->gxn2, NN * D));
+  CKR(dalloc(h, &h->gxn1, NN * D));
+  CKR(dalloc(h, &h->normed, NN * D));
+  CKR(dalloc(h, &h->stats, NN * h->ntn));
+  CKR(dalloc(h, &h->tgt_logit, NN));
+  CKR(dalloc(h, &h->lse_h, NN));
+  CKR(dalloc(h, &h->loss_row, NN));
+  CKR(dalloc(h, &h->dlog, NN * h->vchunk));
+  CKR(dalloc(h, &h->dH, NN * D));
+  h->tn_work_elems = 32L << 20;
+  CKR(dalloc(h, &h->tn_work, h->tn_work_elems));
+  CKR(dalloc(h, &h->cosb, NN * 64));
+  CKR(dalloc(h, &h->sinb, NN * 64));
+  CKR(dalloc(h, &h->inv_freq, 64));
+  CKR(dalloc(h, &h->labels, NN));
+  {
+    float inv[64];
+    rope_inv_freq_host(128, h->d.rope_theta, h->d.rope_type, h->d.rope_factor,
+                       h->d.rope_low_freq_factor, h->d.rope_high_freq_factor,
+                       h->d.rope_orig_max_pos, inv);
+    CK(hipMemcpy(h->inv_freq, inv, sizeof(inv), hipMemcpyHostToDevice));
+  }
+  // step staging: header | positions | pred | tiles
+  const size_t off_pos = 64, off_pred = off_pos + ((size_t)N * 4 + 63) / 64 * 64;
+  const size_t off_tiles = off_pred + ((size_t)N * 4 + 63) / 64 * 64;
+  h->stage_bytes = off_tiles + (size_t)h->max_tiles * sizeof(int4);
+  CK(hipHostMalloc(&h->h_stage, h->stage_bytes, hipHostMallocDefault));
+  memset(h->h_stage, 0, h->stage_bytes);
+  char* ds = nullptr;
+  CKR(dalloc(h, &ds, h->stage_bytes));
+  h->d_stage = ds;
+  h->d_hdr = reinterpret_cast<StepHdr*>(ds);
+  h->d_pos = reinterpret_cast<int*>(ds + off_pos);
+  h->d_pred = reinterpret_cast<int*>(ds + off_pred);
+  h->d_tiles = reinterpret_cast<int4*>(ds + off_tiles);
+
+  // LoRA bf16 operand copies + cast jobs + optimizer tensor table.
+  std::vector<CastJob> jobs;
+  std::vector<OptTensor> opt;
+  std::vector<int2> layer_chunks;
+  std::vector<int2> opt_chunks;
+  const float s = h->s;
+  auto job = [&](const float* src, int rows, int cols, int lds, bf16* dst, int ldd, int tr,
+                 float sc) { jobs.push_back(CastJob{src, dst, rows, cols, lds, ldd, tr, sc}); };
+  for (int i = 0; i < h->L; ++i) {
+    LayerState& ls = h->layers[i];
+    if (ls.has[DSB_PROJ_Q]) {
+      CKR(dalloc(h, &ls.Aqkv, 3L * r * D));
+      CKR(dalloc(h, &ls.AqkvT, (long)D * 3 * r));
+      CKR(dalloc(h, &ls.B2qkv, (long)W3 * 3 * r));
+      CK(hipMemset(ls.B2qkv, 0, (size_t)W3 * 3 * r * 2));
+      CKR(dalloc(h, &ls.BTq, (long)r * q));
+      CKR(dalloc(h, &ls.BTk, (long)r * kv));
+      CKR(dalloc(h, &ls.BTv, (long)r * kv));
+      const int outs[3] = {q, kv, kv}, rowoff[3] = {0, q, q + kv};
+      bf16* bts[3] = {ls.BTq, ls.BTk, ls.BTv};
+      for (int p = 0; p < 3; ++p) {
+        const dsb_lora_tensors& t = ls.lora[p];
+        job(t.A, r, D, D, ls.Aqkv + (long)p * r * D, D, 0, 1.f);
+        job(t.A, r, D, D, ls.AqkvT + p * r, 3 * r, 1, 1.f);
+        job(t.B, outs[p], r, r, ls.B2qkv + (long)rowoff[p] * 3 * r + p * r, 3 * r, 0, s);
+        job(t.B, outs[p], r, r, bts[p], outs[p], 1, s);
+      }
+    }
+    if (ls.has[DSB_PROJ_O]) {
+      CKR(dalloc(h, &ls.Ao, (long)r * q));
+      CKR(dalloc(h, &ls.AoT, (long)q * r));
+      CKR(dalloc(h, &ls.Bo, (long)D * r));
+      CKR(dalloc(h, &ls.BTo, (long)r * D));
+      const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
+      job(t.A, r, q, q, ls.Ao, q, 0, 1.f);
+      job(t.A, r, q, q, ls.AoT, r, 1, 1.f);
+      job(t.B, D, r, r, ls.Bo, r, 0, s);
+      job(t.B, D, r, r, ls.BTo, D, 1, s);
+    }
+    if (ls.has[DSB_PROJ_GATE]) {
+      CKR(dalloc(h, &ls.Agu, 2L * r * D));
+      CKR(dalloc(h, &ls.AguT, (long)D * 2 * r));
+      CKR(dalloc(h, &ls.B2gu, 2L * I * 2 * r));
+      CK(hipMemset(ls.B2gu, 0, (size_t)2 * I * 2 * r * 2));
+      CKR(dalloc(h, &ls.BTg, (long)r * I));
+      CKR(dalloc(h, &ls.BTu, (long)r * I));
+      const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
+      const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
+      job(tg.A, r, D, D, ls.Agu, D, 0, 1.f);
+      job(tg.A, r, D, D, ls.AguT, 2 * r, 1, 1.f);
+      job(tu.A, r, D, D, ls.Agu + (long)r * D, D, 0, 1.f);
+      job(tu.A, r, D, D, ls.AguT + r, 2 * r, 1, 1.f);
+      job(tg.B, I, r, r, ls.B2gu, 2 * r, 0, s);
+      job(tg.B, I, r, r, ls.BTg, I, 1, s);
+      job(tu.B, I, r, r, ls.B2gu + (long)I * 2 * r + r, 2 * r, 0, s);
+      job(tu.B, I, r, r, ls.BTu, I, 1, s);
+    }
+    if (ls.has[DSB_PROJ_DOWN]) {
+      CKR(dalloc(h, &ls.Ad, (long)r * I));
+      CKR(dalloc(h, &ls.AdT, (long)I * r));
+      CKR(dalloc(h, &ls.Bd, (long)D * r));
+      CKR(dalloc(h, &ls.BTd, (long)r * D));
+      const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
+      job(t.A, r, I, I, ls.Ad, I, 0, 1.f);
+      job(t.A, r, I, I, ls.AdT, r, 1, 1.f);
+      job(t.B, D, r, r, ls.Bd, r, 0, s);
+      job(t.B, D, r, r, ls.BTd, D, 1, s);
+    }
+    // optimizer tensors of this layer (A then B per projection, q..down)
+    const int first_chunk = (int)opt_chunks.size();
+    const int ins[7] = {D, D, D, q, D, D, I}, outsz[7] = {q, kv, kv, D, I, I, D};
+    for (int p = 0; p < DSB_NUM_PROJ; ++p) {
+      if (!ls.has[p]) continue;
+      const dsb_lora_tensors& t = ls.lora[p];
+      const int na = r * ins[p], nb = outsz[p] * r;
+      float *mA, *vA, *mB, *vB;
+      CKR(dalloc(h, &mA, na));
+      CKR(dalloc(h, &vA, na));
+      CKR(dalloc(h, &mB, nb));
+      CKR(dalloc(h, &vB, nb));
+      CK(hipMemset(mA, 0, (size_t)na * 4));
+      CK(hipMemset(vA, 0, (size_t)na * 4));
+      CK(hipMemset(mB, 0, (size_t)nb * 4));
+      CK(hipMemset(vB, 0, (size_t)nb * 4));
+      const int ia = (int)opt.size();
+      opt.push_back(OptTensor{t.A, t.gA, mA, vA, na, i});
+      opt.push_back(OptTensor{t.B, t.gB, mB, vB, nb, i});
+      for (int st = 0; st < na; st += 4096) opt_chunks.push_back(int2{ia, st});
+      for (int st = 0; st < nb; st += 4096) opt_chunks.push_back(int2{ia + 1, st});
+    }
+    layer_chunks.push_back(int2{first_chunk, (int)opt_chunks.size() - first_chunk});
+  }
+  std::vector<int2> cast_chunks;
+  for (int j = 0; j < (int)jobs.size(); ++j) {
+    const long tot = (long)jobs[j].rows * jobs[j].cols;
+    for (long st = 0; st < tot; st += 1024) cast_chunks.push_back(int2{j, (int)st});
+  }
+  h->ncast_chunks = (int)cast_chunks.size();
+  h->nopt_chunks = (int)opt_chunks.size();
+  h->nopt_tensors = (int)opt.size();
+  if (!jobs.empty()) {
+    CKR(dalloc(h, &h->d_jobs, jobs.size()));
+    CK(hipMemcpy(h->d_jobs, jobs.data(), jobs.size() * sizeof(CastJob), hipMemcpyHostToDevice));
+    CKR(dalloc(h, &h->d_cast_chunks, cast_chunks.size()));
+    CK(hipMemcpy(h->d_cast_chunks, cast_chunks.data(), cast_chunks.size() * sizeof(int2),
+                 hipMemcpyHostToDevice));
+  }
+  if (!opt.empty()) {
+    CKR(dalloc(h, &h->d_opt, opt.size()));
+    CK(hipMemcpy(h->d_opt, opt.data(), opt.size() * sizeof(OptTensor), hipMemcpyHostToDevice));
+    CKR(dalloc(h, &h->d_opt_chunks, opt_chunks.size()));
+    CK(hipMemcpy(h->d_opt_chunks, opt_chunks.data(), opt_chunks.size() * sizeof(int2),
+                 hipMemcpyHostToDevice));
+    CKR(dalloc(h, &h->d_opt_partial, opt_chunks.size()));
+  }
+  CKR(dalloc(h, &h->d_layer_chunks, layer_chunks.size()));
+  CK(hipMemcpy(h->d_layer_chunks, layer_chunks.data(), layer_chunks.size() * sizeof(int2),
+               hipMemcpyHostToDevice));
+  CKR(dalloc(h, &h->d_sq, h->L));
+  CK(hipDeviceSynchronize());
+  h->finalized = true;
+  return 0;
+}
+
+#define LK(expr)                                                                 \
+  do {                                                                           \
+    hipError_t _e = (expr);                                                      \
+    if (_e != hipSuccess) {                                                      \
+      set_error("%s: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, __LINE__); \
+      h->err = get_error();                                                      \
+      return -1;                                                                 \
+    }                                                                            \
+  } while (0)
+
+// Z-type skinny product: Zb = bf16(sb·(A·Bᵀ)), Zf = sf·(A·Bᵀ).
+int skinny(dsb_handle* h, const bf16* A, long lda, const bf16* B, int Nout, int K, float* Zf,
+           long ldzf, float sf, bf16* Zb, long ldzb, float sb, hipStream_t s) {
+  GemmProblem p{A, lda, B, (long)K, nullptr, 0, nullptr, 0, h->N, Nout, K, 0, &h->d_hdr->n};
+  EpiLoraZ e{Zf, ldzf, sf, Zb, ldzb, sb, Nout};
+  LK(launch_gemm(p, e, s, GEMM_SKINNY));
+  return 0;
+}
+
+int tn(dsb_handle* h, const float* P, long ldp, const bf16* X, long ldx, int R, int C,
+       float* o0, float* o1, float* o2, int rg, int transpose, hipStream_t s) {
+  TnArgs a{};
+  a.P = P; a.ldp = ldp; a.X = X; a.ldx = ldx; a.R = R; a.C = C;
+  a.n = h->N; a.n_dev = &h->d_hdr->n; a.work = h->tn_work;
+  const int cb = (C + 1023) / 1024, rb = (R + 15) / 16;
+  int ns = (512 + cb * rb - 1) / (cb * rb);
+  ns = std::min(ns, 64);
+  ns = std::min<long>(ns, h->tn_work_elems / ((long)R * C));
+  ns = std::min(ns, std::max(1, h->N / 32));
+  a.nsplit = std::max(ns, 1);
+  a.outs[0] = o0; a.outs[1] = o1; a.outs[2] = o2;
+  a.rg = rg; a.transpose_out = transpose;
+  LK(lora_tn(a, s));
+  return 0;
+}
+
+// The whole cycle on stream s (captured once into a graph).
+int enqueue(dsb_handle* h, hipStream_t st) {
+  const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
+  const int* nd = &h->d_hdr->n;
+  const float eps = h->d.rms_eps;
+  const bf16* qn = nullptr;
+  (void)qn;
+  LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
+  LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
+
+  // ---- head: loss and grad wrt final_in (head.py:42-100)
+  LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
+  LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
+  {
+    HeadArgs a{};
+    a.normed = h->normed; a.ldh = D; a.W = h->lm_w; a.WT = h->lm_wT; a.labels = h->labels;
+    a.n = N; a.n_dev = nd; a.D = D; a.V = h->V; a.stats = h->stats; a.ntn = h->ntn;
+    a.tgt_logit = h->tgt_logit; a.lse = h->lse_h; a.loss_row = h->loss_row;
+    a.loss_out = &h->d_hdr->loss; a.inv_nvalid = &h->d_hdr->inv_nvalid;
+    a.dlog = h->dlog; a.vchunk = h->vchunk; a.dH = h->dH;
+    LK(head_fwd_bwd(a, st));
+  }
+  bf16* g = h->g0;
+  bf16* gnext = h->g1;
+  LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, g, D, N, nd, D,
+                 eps, st));
+
+  AttnArgs at{};
+  at.q = h->qk; at.ldq = q + kv;
+  at.k = h->qk + q; at.ldk = q + kv;
+  at.v = h->qkv_pre + q + kv; at.ldv = W3;
+  at.ctx = h->ctx; at.ldc = q; at.o32 = h->o32; at.ldo32 = q;
+  at.lse = h->lse; at.dsum = h->dsum; at.ld_stat = N + 1;
+  at.dout = h->gctx; at.lddo = q;
+  at.dq = h->gqkv; at.lddq = W3;
+  at.dk = h->gqkv + q; at.lddk = W3;
+  at.dv = h->gqkv + q + kv; at.lddv = W3;
+  at.tiles = h->d_tiles; at.ntiles_dev = &h->d_hdr->ntiles; at.max_tiles = h->max_tiles;
+  at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
+
+  for (int li = h->L - 1; li >= 0; --li) {
+    LayerState& ls = h->layers[li];
+    const bf16* x = h->layer_in[li];
+    const long ldx = h->act_ld;
+    const bool hq = ls.has[DSB_PROJ_Q], ho = ls.has[DSB_PROJ_O], hg = ls.has[DSB_PROJ_GATE],
+               hd = ls.has[DSB_PROJ_DOWN];
+    const bf16* wqkv = (const bf16*)ls.w.qkv;
+    const bf16* wo = (const bf16*)ls.w.o;
+    const bf16* wgu = (const bf16*)ls.w.gate_up;
+    const bf16* qnw = (const bf16*)ls.w.q_norm;
+    const bf16* knw = (const bf16*)ls.w.k_norm;
+
+    // ================= forward recompute (llama3.py:62-146, qwen3.py:68-130)
+    LK(rmsnorm_fwd(x, ldx, (const bf16*)ls.w.in_ln, h->xn1, D, N, nd, D, eps, st));
+    if (hq) CKR(skinny(h, h->xn1, D, ls.Aqkv, 3 * r, D, h->Pqkv, 3 * r, h->s, h->Zqkv_b, 3 * r, 1.f, st));
+    {
+      GemmProblem p{h->xn1, (long)D, wqkv, (long)D, hq ? h->Zqkv_b : nullptr, 3L * r,
+                    hq ? ls.B2qkv : nullptr, 3L * r, N, W3, D, hq ? 3 * r : 0, nd};
+      EpiBF16 e{h->qkv_pre, (long)W3, W3, nullptr, 0};
+      LK(launch_gemm(p, e, st));
+    }
+    LK(rope_fwd(h->qkv_pre, W3, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
+                h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+    LK(attn_fwd(at, st));
+    if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Po, r, h->s, h->Zo_b, r, 1.f, st));
+    {
+      GemmProblem p{h->ctx, (long)q, wo, (long)q, ho ? h->Zo_b : nullptr, (long)r,
+                    ho ? ls.Bo : nullptr, (long)r, N, D, q, ho ? r : 0, nd};
+      EpiBF16 e{h->resid, (long)D, D, x, ldx};
+      LK(launch_gemm(p, e, st));
+    }
+    LK(rmsnorm_fwd(h->resid, D, (const bf16*)ls.w.post_ln, h->xn2, D, N, nd, D, eps, st));
+    if (hg) CKR(skinny(h, h->xn2, D, ls.Agu, 2 * r, D, h->Pgu, 2 * r, h->s, h->Zgu_b, 2 * r, 1.f, st));
+    {
+      GemmProblem p{h->xn2, (long)D, wgu, (long)D, hg ? h->Zgu_b : nullptr, 2L * r,
+                    hg ? ls.B2gu : nullptr, 2L * r, N, 2 * I, D, hg ? 2 * r : 0, nd};
+      EpiBF16 e{h->gu, 2L * I, 2 * I, nullptr, 0};
+      LK(launch_gemm(p, e, st));
+    }
+    if (hd) {
+      LK(swiglu_h(h->gu, 2L * I, h->hb, I, N, nd, I, st));
+      CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Pd, r, h->s, h->Zd_b, r, 1.f, st));
+    }
+
+    // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
+    if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_f, r, 1.f, h->gZd_b, r, 1.f, st));
+    {
+      GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
+                    hd ? ls.AdT : nullptr, (long)r, N, I, D, hd ? r : 0, nd};
+      EpiSwiGLUBwd e{h->gu, 2L * I, h->Ggu, 2L * I, I};
+      LK(launch_gemm(p, e, st));
+    }
+    if (hd) {
+      const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
+      CKR(tn(h, h->gZd_f, r, h->hb, I, r, I, t.gA, nullptr, nullptr, r, 0, st));
+      CKR(tn(h, h->Pd, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, st));
+    }
+    if (hg) {
+      CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_f, 2 * r, 1.f, h->gZgu_b, 2 * r, 1.f, st));
+      CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_f + r, 2 * r, 1.f, h->gZgu_b + r,
+                 2 * r, 1.f, st));
+    }
+    {
+      GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
+                    hg ? ls.AguT : nullptr, 2L * r, N, D, 2 * I, hg ? 2 * r : 0, nd};
+      EpiF32 e{h->gxn2, (long)D, D, 0};
+      LK(launch_gemm(p, e, st));
+    }
+    if (hg) {
+      const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
+      const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
+      CKR(tn(h, h->gZgu_f, 2 * r, h->xn2, D, 2 * r, D, tg.gA, tu.gA, nullptr, r, 0, st));
+      CKR(tn(h, h->Pgu, 2 * r, h->Ggu, 2L * I, r, I, tg.gB, nullptr, nullptr, r, 1, st));
+      CKR(tn(h, h->Pgu + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1, st));
+    }
+    LK(rmsnorm_bwd(h->resid, D, h->gxn2, true, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
+                   nd, D, eps, st));
+    if (ho) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_f, r, 1.f, h->gZo_b, r, 1.f, st));
+    {
+      GemmProblem p{h->grm, (long)D, ls.oT, (long)D, ho ? h->gZo_b : nullptr, (long)r,
+                    ho ? ls.AoT : nullptr, (long)r, N, q, D, ho ? r : 0, nd};
+      EpiBF16 e{h->gctx, (long)q, q, nullptr, 0};
+      LK(launch_gemm(p, e, st));
+    }
+    if (ho) {
+      const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
+      CKR(tn(h, h->gZo_f, r, h->ctx, q, r, q, t.gA, nullptr, nullptr, r, 0, st));
+      CKR(tn(h, h->Po, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, st));
+    }
+    LK(attn_bwd(at, st));
+    LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
+                h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+    if (hq) {
+      CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_f, 3 * r, 1.f, h->gZqkv_b, 3 * r, 1.f, st));
+      CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_f + r, 3 * r, 1.f, h->gZqkv_b + r,
+                 3 * r, 1.f, st));
+      CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_f + 2 * r, 3 * r, 1.f,
+                 h->gZqkv_b + 2 * r, 3 * r, 1.f, st));
+    }
+    {
+      GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
+                    hq ? ls.AqkvT : nullptr, 3L * r, N, D, W3, hq ? 3 * r : 0, nd};
+      EpiF32 e{h->gxn1, (long)D, D, 0};
+      LK(launch_gemm(p, e, st));
+    }
+    if (hq) {
+      const dsb_lora_tensors& tq = ls.lora[DSB_PROJ_Q];
+      const dsb_lora_tensors& tk = ls.lora[DSB_PROJ_K];
+      const dsb_lora_tensors& tv = ls.lora[DSB_PROJ_V];
+      CKR(tn(h, h->gZqkv_f, 3 * r, h->xn1, D, 3 * r, D, tq.gA, tk.gA, tv.gA, r, 0, st));
+      CKR(tn(h, h->Pqkv, 3 * r, h->gqkv, W3, r, q, tq.gB, nullptr, nullptr, r, 1, st));
+      CKR(tn(h, h->Pqkv + r, 3 * r, h->gqkv + q, W3, r, kv, tk.gB, nullptr, nullptr, r, 1, st));
+      CKR(tn(h, h->Pqkv + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, tv.gB, nullptr, nullptr, r, 1,
+             st));
+    }
+    LK(rmsnorm_bwd(x, ldx, h->gxn1, true, D, (const bf16*)ls.w.in_ln, h->grm, D, gnext, D, N, nd,
+                   D, eps, st));
+    std::swap(g, gnext);
+  }
+
+  // ---- per-layer clip + AdamW (trainer.py:624-636, :668)
+  LK(clip_adamw(h->d_opt, h->d_opt_chunks, h->nopt_chunks, h->d_layer_chunks, h->L,
+                h->d_opt_partial, h->d_sq, &h->d_hdr->hyper,
+                (h->d.flags & DSB_FLAG_NO_CLIP) ? 0 : 1, st));
+  return 0;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ C-ABI
+
+extern "C" {
+
+const char* dsb_last_error(const dsb_handle* h) {
+  if (h && !h->err.empty()) return h->err.c_str();
+  return get_error();
+}
+
+int dsb_create(const dsb_desc* d, dsb_handle** out) {
+  if (!d || !out) return fail(nullptr, "dsb_create: null argument");
+  if (d->abi_version != DSB_ABI_VERSION) return fail(nullptr, "dsb_create: ABI version mismatch");
+  if (d->head_dim != 128) return fail(nullptr, "dsb_create: head_dim must be 128");
+  if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->n_heads % d->n_kv_heads)
+    return fail(nullptr, "dsb_create: n_heads must be a positive multiple of n_kv_heads");
+  if (d->lora_rank <= 0 || d->lora_rank % 8 || d->lora_rank > 64)
+    return fail(nullptr, "dsb_create: lora_rank must be a multiple of 8 in [8, 64]");
+  if (d->hidden % 8 || d->hidden > 8192 || d->intermediate % 8 || d->vocab % 8)
+    return fail(nullptr, "dsb_create: hidden (<= 8192), intermediate and vocab must be multiples of 8");
+  if (d->s_max <= 0 || d->max_seqs <= 0 || d->n_layers <= 0)
+    return fail(nullptr, "dsb_create: s_max, max_seqs, n_layers must be positive");
+  if (d->family != DSB_FAMILY_LLAMA3 && d->family != DSB_FAMILY_QWEN3)
+    return fail(nullptr, "dsb_create: unknown family");
+  auto* h = new dsb_handle();
+  h->d = *d;
+  h->D = d->hidden; h->Hq = d->n_heads; h->Hkv = d->n_kv_heads;
+  h->q = h->Hq * 128; h->kv = h->Hkv * 128; h->W3 = h->q + 2 * h->kv;
+  h->I = d->intermediate; h->V = d->vocab; h->r = d->lora_rank; h->L = d->n_layers;
+  h->N = d->s_max; h->s = d->lora_scaling; h->qwen = d->family == DSB_FAMILY_QWEN3;
+  h->max_tiles = max_tiles_for(d->s_max, d->max_seqs);
+  h->ntn = (h->V + 255) / 256;
+  {  // bf16 dlogits chunk: at most 2^28 elements (512 MiB), multiple of 256 columns
+    long vc = (1L << 28) / std::max(1, h->N);
+    vc = std::max<long>(256, vc / 256 * 256);
+    h->vchunk = (int)std::min<long>(vc, ((long)h->V + 255) / 256 * 256);
+  }
+  h->layers.resize(h->L);
+  hipError_t e = hipStreamCreateWithFlags(&h->hs, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_in, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_out, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreate(&h->ev_t0);
+  if (e == hipSuccess) e = hipEventCreate(&h->ev_t1);
+  if (e != hipSuccess) {
+    set_error("dsb_create: %s", hipGetErrorString(e));
+    dsb_destroy(h);
+    return -1;
+  }
+  *out = h;
+  return 0;
+}
+
+void dsb_destroy(dsb_handle* h) {
+  if (!h) return;
+  if (h->hs) (void)hipStreamSynchronize(h->hs);
+  if (h->gexec) (void)hipGraphExecDestroy(h->gexec);
+  if (h->graph) (void)hipGraphDestroy(h->graph);
+  for (void* p : h->allocs) (void)hipFree(p);
+  for (auto& ls : h->layers) {
+    if (ls.qkvT) (void)hipFree(ls.qkvT);
+    if (ls.oT) (void)hipFree(ls.oT);
+    if (ls.guT) (void)hipFree(ls.guT);
+    if (ls.downT) (void)hipFree(ls.downT);
+  }
+  if (h->lm_wT) (void)hipFree(h->lm_wT);
+  if (h->h_stage) (void)hipHostFree(h->h_stage);
+  if (h->ev_in) (void)hipEventDestroy(h->ev_in);
+  if (h->ev_out) (void)hipEventDestroy(h->ev_out);
+  if (h->ev_t0) (void)hipEventDestroy(h->ev_t0);
+  if (h->ev_t1) (void)hipEventDestroy(h->ev_t1);
+  if (h->hs) (void)hipStreamDestroy(h->hs);
+  delete h;
+}
+
+int dsb_bind_weights(dsb_handle* h, int layer, const dsb_layer_weights* w) {
+  if (!h || !w) return fail(h, "dsb_bind_weights: null argument");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (layer < 0 || layer >= h->L) return fail(h, "dsb_bind_weights: layer out of range");
+  if (h->finalized) return fail(h, "dsb_bind_weights: state already finalized");
+  if (!w->qkv || !w->o || !w->gate_up || !w->down || !w->in_ln || !w->post_ln)
+    return fail(h, "dsb_bind_weights: missing base weight");
+  if (h->qwen && (!w->q_norm || !w->k_norm))
+    return fail(h, "dsb_bind_weights: qwen3 needs q_norm and k_norm");
+  LayerState& ls = h->layers[layer];
+  ls.w = *w;
+  const int D = h->D, W3 = h->W3, q = h->q, I = h->I;
+  if (!ls.qkvT) {
+    CK(hipMalloc(&ls.qkvT, (size_t)D * W3 * 2));
+    CK(hipMalloc(&ls.oT, (size_t)q * D * 2));
+    CK(hipMalloc(&ls.guT, (size_t)D * 2 * I * 2));
+    CK(hipMalloc(&ls.downT, (size_t)I * D * 2));
+  }
+  CK(transpose_bf16((const bf16*)w->qkv, D, ls.qkvT, W3, W3, D, h->hs));
+  CK(transpose_bf16((const bf16*)w->o, q, ls.oT, D, D, q, h->hs));
+  CK(transpose_bf16((const bf16*)w->gate_up, D, ls.guT, 2L * I, 2 * I, D, h->hs));
+  CK(transpose_bf16((const bf16*)w->down, I, ls.downT, D, D, I, h->hs));
+  CK(hipStreamSynchronize(h->hs));
+  ls.bound = true;
+  return 0;
+}
+
+int dsb_bind_head(dsb_handle* h, const void* lm_head, const void* final_norm) {
+  if (!h || !lm_head || !final_norm) return fail(h, "dsb_bind_head: null argument");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (h->finalized) return fail(h, "dsb_bind_head: state already finalized");
+  h->lm_w = (const bf16*)lm_head;
+  h->norm_w = (const bf16*)final_norm;
+  if (!h->lm_wT) CK(hipMalloc(&h->lm_wT, (size_t)h->V * h->D * 2));
+  CK(transpose_bf16(h->lm_w, h->D, h->lm_wT, h->V, h->V, h->D, h->hs));
+  CK(hipStreamSynchronize(h->hs));
+  return 0;
+}
+
+int dsb_bind_lora(dsb_handle* h, int layer, int proj, const dsb_lora_tensors* t) {
+  if (!h || !t) return fail(h, "dsb_bind_lora: null argument");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (layer < 0 || layer >= h->L || proj < 0 || proj >= DSB_NUM_PROJ)
+    return fail(h, "dsb_bind_lora: layer/proj out of range");
+  if (h->finalized) return fail(h, "dsb_bind_lora: state already finalized");
+  if (!t->A || !t->B || !t->gA || !t->gB) return fail(h, "dsb_bind_lora: null tensor");
+  h->layers[layer].lora[proj] = *t;
+  h->layers[layer].has[proj] = true;
+  return 0;
+}
+
+int dsb_bind_activations(dsb_handle* h, const dsb_activations* a) {
+  if (!h || !a || !a->layer_in || !a->final_in || !a->input_ids)
+    return fail(h, "dsb_bind_activations: null argument");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (a->ld < h->D || a->ld % 8) return fail(h, "dsb_bind_activations: bad row stride");
+  h->layer_in.assign(h->L, nullptr);
+  for (int i = 0; i < h->L; ++i) {
+    if (!a->layer_in[i]) return fail(h, "dsb_bind_activations: null layer_in");
+    h->layer_in[i] = (const bf16*)a->layer_in[i];
+  }
+  h->final_in = (const bf16*)a->final_in;
+  h->ids = a->input_ids;
+  h->act_ld = a->ld;
+  // Rebinding activations after capture changes baked pointers: drop the graph.
+  if (h->gexec) {
+    (void)hipGraphExecDestroy(h->gexec);
+    h->gexec = nullptr;
+  }
+  if (h->graph) {
+    (void)hipGraphDestroy(h->graph);
+    h->graph = nullptr;
+  }
+  return 0;
+}
+
+int dsb_reset_optimizer(dsb_handle* h, float weight_decay) {
+  if (!h) return fail(nullptr, "dsb_reset_optimizer: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  h->d.weight_decay = weight_decay;
+  if (!h->finalized) return 0;  // moments are created zeroed at finalize
+  std::vector<OptTensor> T(h->nopt_tensors);
+  if (!T.empty()) {
+    CK(hipMemcpy(T.data(), h->d_opt, T.size() * sizeof(OptTensor), hipMemcpyDeviceToHost));
+    for (const OptTensor& t : T) {
+      CK(hipMemsetAsync(t.m, 0, (size_t)t.numel * 4, h->hs));
+      CK(hipMemsetAsync(t.v, 0, (size_t)t.numel * 4, h->hs));
+    }
+  }
+  CK(hipStreamSynchronize(h->hs));
+  return 0;
+}
+
+int dsb_pack(const int32_t* seq_lens, int nseq, int n, int32_t* positions, int32_t* pred) {
+  if (nseq < 0 || n < 0 || (nseq > 0 && !seq_lens)) return -1;
+  return pack_cycle(seq_lens, nseq, n, positions, pred, nullptr);
+}
+
+int dsb_rope_inv_freq(int head_dim, float theta, int rope_type, float factor, float low,
+                      float high, float orig_max, float* out) {
+  if (head_dim <= 0 || head_dim % 2 || !out) return -1;
+  rope_inv_freq_host(head_dim, theta, rope_type, factor, low, high, orig_max, out);
+  return 0;
+}
+
+int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, int64_t step,
+             void* stream, float* loss, int* n_valid, dsb_cycle_info* info) {
+  if (!h) return fail(nullptr, "dsb_step: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  h->err.clear();
+  if (n <= 0 || n > h->N) return fail(h, "dsb_step: n must be in [1, s_max]");
+  if (nseq <= 0 || nseq > h->d.max_seqs) return fail(h, "dsb_step: nseq out of range");
+  if (step < 1) return fail(h, "dsb_step: step must be >= 1");
+  if (finalize(h)) return -1;
+  const size_t off_pos = 64, off_pred = off_pos + ((size_t)h->N * 4 + 63) / 64 * 64;
+  const size_t off_tiles = off_pred + ((size_t)h->N * 4 + 63) / 64 * 64;
+  char* hs = (char*)h->h_stage;
+  std::vector<int4> tiles;
+  const int nv = pack_cycle(seq_lens, nseq, n, (int32_t*)(hs + off_pos), (int32_t*)(hs + off_pred),
+                            &tiles);
+  if (nv < 0) return fail(h, "dsb_step: seq_lens must be non-negative and sum to n");
+  if ((int)tiles.size() > h->max_tiles) return fail(h, "dsb_step: too many attention tiles");
+  memcpy(hs + off_tiles, tiles.data(), tiles.size() * sizeof(int4));
+  StepHdr hdr{};
+  hdr.n = n;
+  hdr.ntiles = (int)tiles.size();
+  hdr.n_valid = nv;
+  hdr.inv_nvalid = nv > 0 ? 1.f / (float)nv : 0.f;
+  hdr.hyper.lr = lr;
+  hdr.hyper.beta1 = h->d.beta1;
+  hdr.hyper.beta2 = h->d.beta2;
+  hdr.hyper.eps = h->d.adam_eps;
+  hdr.hyper.wd = h->d.weight_decay;
+  hdr.hyper.bc1 = (float)(1.0 - pow((double)h->d.beta1, (double)step));
+  hdr.hyper.bc2 = (float)(1.0 - pow((double)h->d.beta2, (double)step));
+  hdr.hyper.max_norm = h->d.max_grad_norm;
+  memcpy(hs, &hdr, sizeof(hdr));
+  hipStream_t cs = (hipStream_t)stream;
+  CK(hipEventRecord(h->ev_in, cs));
+  CK(hipStreamWaitEvent(h->hs, h->ev_in, 0));
+  CK(hipMemcpyAsync(h->d_stage, h->h_stage, h->stage_bytes, hipMemcpyHostToDevice, h->hs));
+  CK(hipEventRecord(h->ev_t0, h->hs));
+  bool used_graph = false;
+  if ((h->d.flags & DSB_FLAG_GRAPH) && !h->graph_failed) {
+    if (!h->gexec) {
+      hipError_t e = hipStreamBeginCapture(h->hs, hipStreamCaptureModeThreadLocal);
+      if (e == hipSuccess) {
+        const int rc = enqueue(h, h->hs);
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(h->hs, &g);
+        if (rc != 0) {
+          if (g) (void)hipGraphDestroy(g);
+          return -1;
+        }
+        if (e == hipSuccess) {
+          e = hipGraphInstantiate(&h->gexec, g, nullptr, nullptr, 0);
+          h->graph = g;
+        }
+      }
+      if (e != hipSuccess) {
+        h->graph_failed = true;
+        (void)hipGetLastError();
+        fprintf(stderr, "[dsb] hipGraph capture failed (%s); running the cycle eagerly\n",
+                hipGetErrorString(e));
+      }
+    }
+    if (h->gexec) {
+      CK(hipGraphLaunch(h->gexec, h->hs));
+      used_graph = true;
+    }
+  }
+  if (!used_graph && enqueue(h, h->hs)) return -1;
+  CK(hipEventRecord(h->ev_t1, h->hs));
+  CK(hipMemcpyAsync(h->h_stage, h->d_stage, sizeof(StepHdr), hipMemcpyDeviceToHost, h->hs));
+  CK(hipEventRecord(h->ev_out, h->hs));
+  CK(hipStreamWaitEvent(cs, h->ev_out, 0));
+  CK(hipEventSynchronize(h->ev_out));
+  StepHdr back;
+  memcpy(&back, hs, sizeof(back));
+  if (back.err & 1) return fail(h, "dsb_step: a target token id is outside [0, vocab)");
+  if (loss) *loss = back.loss;
+  if (n_valid) *n_valid = nv;
+  if (info) {
+    float ms = 0.f;
+    CK(hipEventElapsedTime(&ms, h->ev_t0, h->ev_t1));
+    info->gpu_ms = ms;
+    info->graph = used_graph ? 1 : 0;
+    info->n_valid = nv;
+  }
+  return 0;
+}
+
+// ------------------------------------------------------------ single ops
+
+#define OPCK(expr)                                                                   \
+  do {                                                                               \
+    hipError_t _e = (expr);                                                          \
+    if (_e != hipSuccess) {                                                          \
+      set_error("%s: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, __LINE__); \
+      return -1;                                                                     \
+    }                                                                                \
+  } while (0)
+
+int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
+                int64_t lda2, const void* B2, int64_t ldb2, int M, int N, int K1, int K2, void* C,
+                int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr, int cfg,
+                void* stream) {
+  if (K1 % 8 || K2 % 8 || lda % 8 || ldb % 8 || (K2 && (lda2 % 8 || ldb2 % 8)) || ldc % 4)
+    return fail(nullptr, "dsb_op_gemm: K and leading dims must be multiples of 8 (ldc of 4)");
+  hipStream_t s = (hipStream_t)stream;
+  GemmProblem p{(const bf16*)A, lda, (const bf16*)B, ldb, (const bf16*)A2, lda2,
+                (const bf16*)B2, ldb2, M, N, K1, K2, nullptr};
+  if (out_f32) {
+    EpiF32 e{(float*)C, ldc, N, accumulate};
+    OPCK(launch_gemm(p, e, s, cfg));
+  } else {
+    EpiBF16 e{(bf16*)C, ldc, N, (const bf16*)R, ldr};
+    OPCK(launch_gemm(p, e, s, cfg));
+  }
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_rmsnorm(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int rows,
+                   int D, float eps, void* stream) {
+  if (D % 8 || D > 8192) return fail(nullptr, "dsb_op_rmsnorm: D must be a multiple of 8, <= 8192");
+  hipStream_t s = (hipStream_t)stream;
+  OPCK(rmsnorm_fwd((const bf16*)x, ldx, (const bf16*)w, (bf16*)y, ldy, rows, nullptr, D, eps, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_rmsnorm_bwd(const void* x, int64_t ldx, const void* g, int g_f32, int64_t ldg,
+                       const void* w, const void* resid, int64_t ldr, void* out, int64_t ldo,
+                       int rows, int D, float eps, void* stream) {
+  if (D % 8 || D > 8192) return fail(nullptr, "dsb_op_rmsnorm_bwd: D must be a multiple of 8, <= 8192");
+  hipStream_t s = (hipStream_t)stream;
+  OPCK(rmsnorm_bwd((const bf16*)x, ldx, g, g_f32 != 0, ldg, (const bf16*)w, (const bf16*)resid,
+                   ldr, (bf16*)out, ldo, rows, nullptr, D, eps, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_rope_table(const int32_t* pos, int n, const float* inv_freq, int half, float* cos_out,
+                      float* sin_out, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  OPCK(rope_table(pos, n, nullptr, inv_freq, half, cos_out, sin_out, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_rope(const void* qkv_pre, int64_t ldin, void* qk_out, int64_t ldout, const float* cos_t,
+                const float* sin_t, int n, int Hq, int Hkv, const void* q_norm, const void* k_norm,
+                float eps, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  OPCK(rope_fwd((const bf16*)qkv_pre, ldin, (bf16*)qk_out, ldout, cos_t, sin_t, n, nullptr, Hq,
+                Hkv, (const bf16*)q_norm, (const bf16*)k_norm, eps, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_rope_bwd(void* g, int64_t ldg, const void* qkv_pre, int64_t ldp, const float* cos_t,
+                    const float* sin_t, int n, int Hq, int Hkv, const void* q_norm,
+                    const void* k_norm, float eps, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  OPCK(rope_bwd((bf16*)g, ldg, (const bf16*)qkv_pre, ldp, cos_t, sin_t, n, nullptr, Hq, Hkv,
+                (const bf16*)q_norm, (const bf16*)k_norm, eps, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+}  // extern "C"
+
+namespace {
+struct TmpDev {
+  std::vector<void*> ptrs;
+  ~TmpDev() {
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+  template <class T>
+  T* alloc(size_t count) {
+    void* p = nullptr;
+    if (hipMalloc(&p, count * sizeof(T) + 256) != hipSuccess) return nullptr;
+    ptrs.push_back(p);
+    return (T*)p;
+  }
+};
+
+int attn_setup(const int32_t* seq_lens, int nseq, TmpDev& tmp, AttnArgs& a, int* n_out) {
+  std::vector<int4> tiles;
+  long n = 0;
+  for (int i = 0; i < nseq; ++i) n += seq_lens[i];
+  if (pack_cycle(seq_lens, nseq, (int)n, nullptr, nullptr, &tiles) < 0)
+    return fail(nullptr, "attention: bad seq_lens");
+  int4* dt = tmp.alloc<int4>(tiles.size() + 1);
+  int* dn = tmp.alloc<int>(2);
+  if (!dt || !dn) return fail(nullptr, "attention: hipMalloc failed");
+  int hv[2] = {(int)tiles.size(), (int)n};
+  if (!tiles.empty() &&
+      hipMemcpy(dt, tiles.data(), tiles.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess)
+    return fail(nullptr, "attention: copy failed");
+  if (hipMemcpy(dn, hv, sizeof(hv), hipMemcpyHostToDevice) != hipSuccess)
+    return fail(nullptr, "attention: copy failed");
+  a.tiles = dt;
+  a.ntiles_dev = dn;
+  a.max_tiles = (int)tiles.size();
+  a.n_dev = dn + 1;
+  a.n = (int)n;
+  *n_out = (int)n;
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int dsb_op_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                    int64_t ldv, void* ctx, int64_t ldc, float* o32, float* lse,
+                    const int32_t* seq_lens, int nseq, int Hq, int Hkv, void* stream) {
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(nullptr, "attn: bad head counts");
+  hipStream_t s = (hipStream_t)stream;
+  TmpDev tmp;
+  AttnArgs a{};
+  int n = 0;
+  if (attn_setup(seq_lens, nseq, tmp, a, &n)) return -1;
+  a.q = (const bf16*)q; a.ldq = ldq; a.k = (const bf16*)k; a.ldk = ldk;
+  a.v = (const bf16*)v; a.ldv = ldv; a.ctx = (bf16*)ctx; a.ldc = ldc;
+  a.o32 = o32; a.ldo32 = (long)Hq * 128; a.lse = lse; a.ld_stat = n; a.Hq = Hq; a.Hkv = Hkv;
+  OPCK(attn_fwd(a, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                    int64_t ldv, const float* o32, const float* lse, const void* dout,
+                    int64_t lddo, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
+                    int64_t lddv, const int32_t* seq_lens, int nseq, int Hq, int Hkv,
+                    void* stream) {
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(nullptr, "attn: bad head counts");
+  hipStream_t s = (hipStream_t)stream;
+  TmpDev tmp;
+  AttnArgs a{};
+  int n = 0;
+  if (attn_setup(seq_lens, nseq, tmp, a, &n)) return -1;
+  float* dsum = tmp.alloc<float>((size_t)Hq * (n + 1));
+  if (!dsum) return fail(nullptr, "attn: hipMalloc failed");
+  a.q = (const bf16*)q; a.ldq = ldq; a.k = (const bf16*)k; a.ldk = ldk;
+  a.v = (const bf16*)v; a.ldv = ldv; a.o32 = (float*)o32; a.ldo32 = (long)Hq * 128;
+  a.lse = (float*)lse; a.dsum = dsum; a.ld_stat = n; a.dout = (const bf16*)dout; a.lddo = lddo;
+  a.dq = (bf16*)dq; a.lddq = lddq; a.dk = (bf16*)dk; a.lddk = lddk; a.dv = (bf16*)dv;
+  a.lddv = lddv; a.Hq = Hq; a.Hkv = Hkv;
+  OPCK(attn_bwd(a, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t* ids,
+                const int32_t* seq_lens, int nseq, int n, int D, int V, float* dH, float* loss,
+                int* n_valid, void* stream) {
+  if (D % 8 || V % 8 || ldh % 8) return fail(nullptr, "dsb_op_head: D, V, ldh must be multiples of 8");
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<int32_t> pred(n > 0 ? n : 1);
+  const int nv = pack_cycle(seq_lens, nseq, n, nullptr, pred.data(), nullptr);
+  if (nv < 0) return fail(nullptr, "dsb_op_head: seq_lens must sum to n");
+  TmpDev tmp;
+  const int ntn = (V + 255) / 256;
+  const int vchunk = std::min(((V + 255) / 256) * 256, 4096);
+  bf16* WT = tmp.alloc<bf16>((size_t)V * D);
+  int* dpred = tmp.alloc<int>(n + 1);
+  int* labels = tmp.alloc<int>(n + 1);
+  float2* stats = tmp.alloc<float2>((size_t)(n + 1) * ntn);
+  float* tl = tmp.alloc<float>(n + 1);
+  float* lse = tmp.alloc<float>(n + 1);
+  float* lr = tmp.alloc<float>(n + 1);
+  float* scal = tmp.alloc<float>(4);
+  int* err = tmp.alloc<int>(1);
+  bf16* dlog = tmp.alloc<bf16>((size_t)(n + 1) * vchunk);
+  if (!WT || !dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog)
+    return fail(nullptr, "dsb_op_head: hipMalloc failed");
+  float hsc[4] = {nv > 0 ? 1.f / nv : 0.f, 0.f, 0.f, 0.f};
+  OPCK(hipMemcpy(scal, hsc, sizeof(hsc), hipMemcpyHostToDevice));
+  OPCK(hipMemcpy(dpred, pred.data(), n * sizeof(int32_t), hipMemcpyHostToDevice));
+  OPCK(hipMemset(err, 0, sizeof(int)));
+  OPCK(transpose_bf16((const bf16*)lm_w, D, WT, V, V, D, s));
+  OPCK(build_labels(ids, dpred, labels, n, nullptr, V, err, s));
+  HeadArgs a{};
+  a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w; a.WT = WT;
+  a.labels = labels; a.n = n; a.n_dev = nullptr; a.D = D; a.V = V; a.stats = stats; a.ntn = ntn;
+  a.tgt_logit = tl; a.lse = lse; a.loss_row = lr; a.loss_out = scal + 1; a.inv_nvalid = scal;
+  a.dlog = dlog; a.vchunk = vchunk; a.dH = dH;
+  OPCK(head_fwd_bwd(a, s));
+  OPCK(hipStreamSynchronize(s));
+  int herr = 0;
+  OPCK(hipMemcpy(&herr, err, sizeof(int), hipMemcpyDeviceToHost));
+  if (herr) return fail(nullptr, "dsb_op_head: a target token id is outside [0, vocab)");
+  OPCK(hipMemcpy(hsc, scal, sizeof(hsc), hipMemcpyDeviceToHost));
+  if (loss) *loss = hsc[1];
+  if (n_valid) *n_valid = nv;
+  return 0;
+}
+
+int dsb_op_lora_tn(const float* P, int64_t ldp, const void* X, int64_t ldx, int n, int R, int C,
+                   float* out0, float* out1, float* out2, int rg, int transpose_out,
+                   void* stream) {
+  if (C % 4 || ldx % 4 || rg <= 0 || (R + rg - 1) / rg > 3)
+    return fail(nullptr, "dsb_op_lora_tn: C and ldx must be multiples of 4, at most 3 groups");
+  hipStream_t s = (hipStream_t)stream;
+  TmpDev tmp;
+  const int ns = 8;
+  float* work = tmp.alloc<float>((size_t)ns * R * C);
+  if (!work) return fail(nullptr, "dsb_op_lora_tn: hipMalloc failed");
+  TnArgs a{};
+  a.P = P; a.ldp = ldp; a.X = (const bf16*)X; a.ldx = ldx; a.R = R; a.C = C; a.n = n;
+  a.n_dev = nullptr; a.work = work; a.nsplit = ns; a.outs[0] = out0; a.outs[1] = out1;
+  a.outs[2] = out2; a.rg = rg; a.transpose_out = transpose_out;
+  OPCK(lora_tn(a, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_clip_adamw(float* const* w, float* const* g, float* const* m, float* const* v,
+                      const int32_t* numel, const int32_t* group, int ntensors, int ngroups,
+                      float lr, float beta1, float beta2, float eps, float wd, int64_t step,
+                      float max_norm, int do_clip, void* stream) {
+  if (ntensors <= 0 || ngroups <= 0 || step < 1) return fail(nullptr, "dsb_op_clip_adamw: bad sizes");
+  std::vector<OptTensor> T;
+  std::vector<int2> chunks, lchunks(ngroups, int2{0, 0});
+  int prev = -1;
+  for (int i = 0; i < ntensors; ++i) {
+    if (group[i] < prev || group[i] >= ngroups)
+      return fail(nullptr, "dsb_op_clip_adamw: groups must be non-decreasing and < ngroups");
+    if (group[i] != prev) {
+      for (int gidx = prev + 1; gidx <= group[i]; ++gidx) lchunks[gidx] = int2{(int)chunks.size(), 0};
+      prev = group[i];
+    }
+    T.push_back(OptTensor{w[i], g[i], m[i], v[i], numel[i], group[i]});
+    for (int st = 0; st < numel[i]; st += 4096) chunks.push_back(int2{i, st});
+    lchunks[group[i]].y = (int)chunks.size() - lchunks[group[i]].x;
+  }
+  for (int gidx = prev + 1; gidx < ngroups; ++gidx) lchunks[gidx] = int2{(int)chunks.size(), 0};
+  hipStream_t s = (hipStream_t)stream;
+  TmpDev tmp;
+  OptTensor* dT = tmp.alloc<OptTensor>(T.size());
+  int2* dc = tmp.alloc<int2>(chunks.size() + 1);
+  int2* dl = tmp.alloc<int2>(lchunks.size());
+  float* part = tmp.alloc<float>(chunks.size() + 1);
+  float* sq = tmp.alloc<float>(ngroups);
+  OptHyper* hp = tmp.alloc<OptHyper>(1);
+  if (!dT || !dc || !dl || !part || !sq || !hp) return fail(nullptr, "dsb_op_clip_adamw: hipMalloc failed");
+  OptHyper hh{lr, beta1, beta2, eps, wd, (float)(1.0 - pow((double)beta1, (double)step)),
+              (float)(1.0 - pow((double)beta2, (double)step)), max_norm};
+  OPCK(hipMemcpy(dT, T.data(), T.size() * sizeof(OptTensor), hipMemcpyHostToDevice));
+  if (!chunks.empty())
+    OPCK(hipMemcpy(dc, chunks.data(), chunks.size() * sizeof(int2), hipMemcpyHostToDevice));
+  OPCK(hipMemcpy(dl, lchunks.data(), lchunks.size() * sizeof(int2), hipMemcpyHostToDevice));
+  OPCK(hipMemcpy(hp, &hh, sizeof(hh), hipMemcpyHostToDevice));
+  OPCK(hipMemset(sq, 0, ngroups * sizeof(float)));
+  OPCK(clip_adamw(dT, dc, (int)chunks.size(), dl, ngroups, part, sq, hp, do_clip, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+}  // extern "C"

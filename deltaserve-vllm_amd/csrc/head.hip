@@ -1,0 +1,201 @@
+// Final-norm output → LM head → shifted cross-entropy → dH, without the
+// [rows, vocab] fp32 logits or probabilities of the reference.
+//
+// Semantics: deltaserve-plugin/deltaserve/bwd_services/common/head.py:42-100
+//   loss = sum_rows CE(logits, target) / n_valid, dlogits = (softmax - onehot)/n_valid,
+//   grad_rows = dlogits · W. Rows that predict nothing (the last token of each
+//   sequence) carry label -1 and contribute neither loss nor gradient.
+//
+// Pass 1 (LSE): one vocab-tiled MFMA GEMM whose epilogue reduces each 256-wide
+//   vocab tile to (max, sum exp) per row and picks out the target logit.
+// Reduce: combine the per-tile statistics into the row LSE and the row loss;
+//   a single-block deterministic sum gives the cycle loss.
+// Pass 2, per vocab chunk: recompute the logits with an epilogue writing
+//   bf16 dlogits for the chunk only, then dH += dlogits_chunk · W_chunk with
+//   the transposed head copy (fp32 accumulate in the epilogue).
+#include "gemm_nt.h"
+#include "kernels.h"
+
+namespace dsb {
+
+namespace {
+constexpr int CE_BN = 256;
+
+struct EpiCEStats {
+  const int* labels;
+  float2* stats;
+  int ntn;
+  float* tgt_logit;
+  int V;
+  template <int FM, int FN, int WM, int WN>
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
+    constexpr int TM = FM * 32, TN = FN * 32, BMl = WM * TM;
+    const int wn = wave % WN, wm = wave / WN;
+    const int n0 = nw - wn * TN;
+    const int pn = n0 / (WN * TN);
+    const int lr = lane & 31, lh = lane >> 5;
+    float* red = reinterpret_cast<float*>(smem);  // [WN][BMl]
+    float mx[FM];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int m = mw + fm * 32 + lr;
+      const int t = (m < M) ? labels[m] : -1;
+      float v = -INFINITY;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int n = nw + fn * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          const float x = acc[fm][fn][r];
+          if (n < V) v = fmaxf(v, x);
+          if (n == t) tgt_logit[m] = x;
+        }
+      mx[fm] = fmaxf(v, __shfl_xor(v, 32, 64));
+    }
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+      if (lh == 0) red[wn * BMl + wm * TM + fm * 32 + lr] = mx[fm];
+    __syncthreads();
+    float sm[FM];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int row = wm * TM + fm * 32 + lr;
+      float b = red[row];
+#pragma unroll
+      for (int j = 1; j < WN; ++j) b = fmaxf(b, red[j * BMl + row]);
+      mx[fm] = b;
+      float s = 0.f;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int n = nw + fn * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (n < V) s += __expf(acc[fm][fn][r] - b);
+        }
+      sm[fm] = s + __shfl_xor(s, 32, 64);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+      if (lh == 0) red[wn * BMl + wm * TM + fm * 32 + lr] = sm[fm];
+    __syncthreads();
+    if (wn == 0 && lh == 0) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int row = wm * TM + fm * 32 + lr;
+        const int m = mw + fm * 32 + lr;
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < WN; ++j) s += red[j * BMl + row];
+        if (m < M) stats[(long)m * ntn + pn] = make_float2(mx[fm], s);
+      }
+    }
+  }
+};
+
+struct EpiCEGrad {
+  const int* labels;
+  const float* lse;
+  const float* inv_nvalid;
+  bf16* D;
+  long ldd;
+  int c0;
+  int Nc;
+  template <int FM, int FN, int WM, int WN>
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int,
+                   void*) const {
+    const float sc = *inv_nvalid;
+    for_each_quad(acc, mw, nw, M, lane, [&](int m, int n, float* v) {
+      if (n >= Nc) return;
+      const int t = labels[m];
+      const float l = lse[m];
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __expf(v[i] - l) - ((c0 + n + i) == t ? 1.f : 0.f);
+        p[i] = t >= 0 ? e * sc : 0.f;
+      }
+      bf16* d = D + (long)m * ldd + n;
+      if (n + 3 < Nc) {
+        bf16x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (bf16)p[i];
+        *reinterpret_cast<bf16x4*>(d) = o;
+      } else {
+        for (int i = 0; i < 4 && n + i < Nc; ++i) d[i] = (bf16)p[i];
+      }
+    });
+  }
+};
+}  // namespace
+
+// One wave per row: combine the per-tile (max, sumexp) pairs.
+__global__ __launch_bounds__(256) void ce_reduce_kernel(const float2* __restrict__ stats,
+                                                        int ntn, const int* __restrict__ labels,
+                                                        const float* __restrict__ tgt_logit,
+                                                        float* __restrict__ lse,
+                                                        float* __restrict__ loss_row, int n,
+                                                        const int* n_dev) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (m >= N) return;
+  const float2* st = stats + (long)m * ntn;
+  float mx = -INFINITY;
+  for (int j = l; j < ntn; j += 64) mx = fmaxf(mx, st[j].x);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int j = l; j < ntn; j += 64) s += st[j].y * __expf(st[j].x - mx);
+  s = wave_sum(s);
+  if (l == 0) {
+    const float v = mx + __logf(s);
+    lse[m] = v;
+    loss_row[m] = labels[m] >= 0 ? v - tgt_logit[m] : 0.f;
+  }
+}
+
+// Deterministic single-block sum of loss_row[0:n) times 1/n_valid.
+__global__ __launch_bounds__(1024) void ce_loss_kernel(const float* __restrict__ loss_row,
+                                                       int n, const int* n_dev,
+                                                       const float* inv_nvalid,
+                                                       float* __restrict__ out) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  __shared__ float red[16];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < N; i += 1024) s += loss_row[i];
+  s = block_sum<1024>(s, red);
+  if (threadIdx.x == 0) out[0] = s * (*inv_nvalid);
+}
+
+hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s) {
+  hipError_t e;
+  if (a.n <= 0) return hipSuccess;
+  {
+    GemmProblem p{a.normed, a.ldh, a.W, (long)a.D, nullptr, 0, nullptr, 0,
+                  a.n, a.V, a.D, 0, a.n_dev};
+    EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.V};
+    if ((e = launch_gemm_cfg<256, CE_BN, 2, 2>(p, epi, s)) != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(ce_reduce_kernel, dim3((a.n + 3) / 4), dim3(256), 0, s, a.stats, a.ntn,
+                     a.labels, a.tgt_logit, a.lse, a.loss_row, a.n, a.n_dev);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(ce_loss_kernel, dim3(1), dim3(1024), 0, s, a.loss_row, a.n, a.n_dev,
+                     a.inv_nvalid, a.loss_out);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  for (int c0 = 0; c0 < a.V; c0 += a.vchunk) {
+    const int Nc = min(a.vchunk, a.V - c0);
+    GemmProblem p{a.normed, a.ldh, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
+                  a.n, Nc, a.D, 0, a.n_dev};
+    EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Nc};
+    if ((e = launch_gemm(p, epi, s)) != hipSuccess) return e;
+    GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, (long)a.V, nullptr, 0, nullptr, 0,
+                  a.n, a.D, Nc, 0, a.n_dev};
+    EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
+    if ((e = launch_gemm(q, ef, s)) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace dsb

@@ -1,0 +1,119 @@
+// Internal launch API of the backward's HIP kernels (not part of the C-ABI).
+#pragma once
+
+#include "dsb_common.h"
+
+namespace dsb {
+
+// ---- norm_rope.hip
+hipError_t rmsnorm_fwd(const bf16* x, long ldx, const bf16* w, bf16* y, long ldy, int rows,
+                       const int* rows_dev, int D, float eps, hipStream_t s);
+hipError_t rmsnorm_bwd(const bf16* x, long ldx, const void* g, bool g_f32, long ldg,
+                       const bf16* w, const bf16* resid, long ldr, bf16* out, long ldo,
+                       int rows, const int* rows_dev, int D, float eps, hipStream_t s);
+hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_freq,
+                      int half, float* cosb, float* sinb, hipStream_t s);
+hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s);
+hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* cosb,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s);
+hipError_t swiglu_h(const bf16* gu, long ldgu, bf16* h, long ldh, int n, const int* n_dev,
+                    int I, hipStream_t s);
+
+// ---- attention.hip
+// Packed varlen causal GQA attention, head_dim 128. `tiles` holds one int4
+// (seq_start, seq_len, tile_start, 0) per 128-token tile of every sequence;
+// `ntiles_dev` is the live tile count (grid is sized for `max_tiles`).
+struct AttnArgs {
+  const bf16* q; long ldq;   // [n, Hq*128] (post-RoPE)
+  const bf16* k; long ldk;   // [n, Hkv*128] (post-RoPE)
+  const bf16* v; long ldv;   // [n, Hkv*128]
+  bf16* ctx; long ldc;       // fwd out [n, Hq*128]
+  float* o32;                // fwd out fp32 copy of ctx, ld = ldo32
+  long ldo32;
+  float* lse;                // [Hq, ld_stat] log2-domain row log-sum-exp
+  float* dsum;               // [Hq, ld_stat] rowsum(dO ∘ O)
+  long ld_stat;
+  const bf16* dout; long lddo;  // bwd in: grad of ctx
+  bf16* dq; long lddq;       // bwd out
+  bf16* dk; long lddk;
+  bf16* dv; long lddv;
+  const int4* tiles;
+  const int* ntiles_dev;
+  int max_tiles;
+  int Hq, Hkv;
+  const int* n_dev;  // live token count (for the dsum prep)
+  int n;
+};
+hipError_t attn_fwd(const AttnArgs& a, hipStream_t s);
+hipError_t attn_bwd(const AttnArgs& a, hipStream_t s);
+
+// ---- lora.hip
+struct CastJob {
+  const float* src;
+  bf16* dst;
+  int rows, cols;   // source shape
+  int ld_src, ld_dst;
+  int transpose;    // dst[c, r] = src[r, c]
+  float scale;
+};
+hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunks,
+                     hipStream_t s);
+// out[j, c] (or out[c, j] when transposed) = sum_t P[t, j] * X[t, c], t < n.
+// Output rows j are split into groups of `rg` rows written to outs[j / rg].
+struct TnArgs {
+  const float* P; long ldp;
+  const bf16* X; long ldx;
+  int R, C;
+  int n; const int* n_dev;
+  float* work;     // [nsplit, R, C]
+  int nsplit;
+  float* outs[3];
+  int rg;
+  int transpose_out;
+};
+hipError_t lora_tn(const TnArgs& a, hipStream_t s);
+
+// ---- head.hip
+struct HeadArgs {
+  const bf16* normed; long ldh;   // [n, D]
+  const bf16* W;                  // [V, D]
+  const bf16* WT;                 // [D, V]
+  const int* labels;              // [n] target id or -1
+  int n; const int* n_dev;
+  int D, V;
+  float2* stats;                  // [n_cap, ntn]
+  int ntn;
+  float* tgt_logit;               // [n_cap]
+  float* lse;                     // [n_cap]
+  float* loss_row;                // [n_cap]
+  float* loss_out;                // scalar: sum(loss_row)/n_valid
+  const float* inv_nvalid;        // device scalar 1/n_valid (0 when none)
+  bf16* dlog; int vchunk;         // [n_cap, vchunk] bf16 scratch
+  float* dH;                      // [n, D] fp32
+};
+hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s);
+
+// ---- optim.hip
+struct OptTensor {
+  float* w;
+  float* g;
+  float* m;
+  float* v;
+  int numel;
+  int layer;
+};
+struct OptHyper {
+  float lr, beta1, beta2, eps, wd, bc1, bc2, max_norm;
+};
+hipError_t clip_adamw(const OptTensor* tensors_dev, const int2* chunks_dev, int nchunks,
+                      const int2* layer_chunks_dev, int nlayers, float* partial,
+                      float* sq_layer, const OptHyper* hyper_dev, int do_clip, hipStream_t s);
+
+// ---- misc (dsb_api.hip)
+hipError_t build_labels(const int64_t* ids, const int* pred_flag, int* labels, int n,
+                        const int* n_dev, int V, int* err, hipStream_t s);
+
+}  // namespace dsb

@@ -1,0 +1,286 @@
+// Bandwidth-bound per-row kernels of the backward: RMSNorm forward/backward,
+// RoPE (NeoX rotate-half) forward/backward with the optional per-head q/k
+// RMSNorm of Qwen3, the RoPE cos/sin table, and h = silu(gate)·up.
+//
+// Semantics follow deltaserve-plugin/deltaserve/bwd_services/common/ops.py:
+//   rmsnorm            ops.py:84-88   (fp32 internals, output in the input dtype)
+//   rmsnorm_backward   ops.py:91-100
+//   rope_cos_sin       ops.py:60-65
+//   apply_rope         ops.py:68-73
+//   rope_backward      ops.py:76-81
+//   q/k-norm fwd/bwd   bwd_services/qwen3.py:96-107, :133-144
+// All arithmetic is fp32 with one rounding to bf16 at the store.
+#include "kernels.h"
+
+namespace dsb {
+
+// One 256-thread block per row; each thread keeps up to RPT 8-wide chunks.
+constexpr int NORM_NT = 256;
+constexpr int NORM_RPT = 4;  // D <= 256 * 8 * 4 = 8192
+
+__global__ __launch_bounds__(NORM_NT) void rmsnorm_fwd_kernel(
+    const bf16* __restrict__ x, long ldx, const bf16* __restrict__ w,
+    bf16* __restrict__ y, long ldy, int rows, const int* rows_dev, int D, float eps) {
+  int R = rows;
+  if (rows_dev) R = min(R, *rows_dev);
+  const int row = blockIdx.x;
+  if (row >= R) return;
+  __shared__ float red[NORM_NT / 64];
+  const bf16* xr = x + (long)row * ldx;
+  const int nch = D >> 3;
+  float v[NORM_RPT][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_RPT; ++i) {
+    const int c = threadIdx.x + i * NORM_NT;
+    if (c < nch) {
+      unpack8(ldg128(xr + c * 8), v[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+    }
+  }
+  ss = block_sum<NORM_NT>(ss, red);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  bf16* yr = y + (long)row * ldy;
+#pragma unroll
+  for (int i = 0; i < NORM_RPT; ++i) {
+    const int c = threadIdx.x + i * NORM_NT;
+    if (c < nch) {
+      float wf[8], o[8];
+      unpack8(ldg128(w + c * 8), wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (v[i][e] * inv) * wf[e];
+      stg128(yr + c * 8, pack8(o));
+    }
+  }
+}
+
+// out = bf16( rmsnorm_backward(x, g, w) + resid ), g fp32 or bf16.
+template <typename GT>
+__global__ __launch_bounds__(NORM_NT) void rmsnorm_bwd_kernel(
+    const bf16* __restrict__ x, long ldx, const GT* __restrict__ g, long ldg,
+    const bf16* __restrict__ w, const bf16* __restrict__ resid, long ldr,
+    bf16* __restrict__ out, long ldo, int rows, const int* rows_dev, int D, float eps) {
+  int R = rows;
+  if (rows_dev) R = min(R, *rows_dev);
+  const int row = blockIdx.x;
+  if (row >= R) return;
+  __shared__ float red[NORM_NT / 64];
+  const bf16* xr = x + (long)row * ldx;
+  const GT* gr = g + (long)row * ldg;
+  const int nch = D >> 3;
+  float xv[NORM_RPT][8], gw[NORM_RPT][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_RPT; ++i) {
+    const int c = threadIdx.x + i * NORM_NT;
+    if (c < nch) {
+      unpack8(ldg128(xr + c * 8), xv[i]);
+      float wf[8];
+      unpack8(ldg128(w + c * 8), wf);
+      if constexpr (sizeof(GT) == 4) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(gr + c * 8);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(gr + c * 8 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { gw[i][e] = a[e] * wf[e]; gw[i][e + 4] = b[e] * wf[e + 4]; }
+      } else {
+        float gf[8];
+        unpack8(ldg128(gr + c * 8), gf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gw[i][e] = gf[e] * wf[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += xv[i][e] * xv[i][e];
+    }
+  }
+  ss = block_sum<NORM_NT>(ss, red);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_RPT; ++i) {
+    const int c = threadIdx.x + i * NORM_NT;
+    if (c < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot += gw[i][e] * (xv[i][e] * inv);
+    }
+  }
+  dot = block_sum<NORM_NT>(dot, red);
+  const float k = dot / (float)D;
+  bf16* orow = out + (long)row * ldo;
+#pragma unroll
+  for (int i = 0; i < NORM_RPT; ++i) {
+    const int c = threadIdx.x + i * NORM_NT;
+    if (c < nch) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (gw[i][e] - (xv[i][e] * inv) * k) * inv;
+      if (resid) {
+        float rf[8];
+        unpack8(ldg128(resid + (long)row * ldr + c * 8), rf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += rf[e];
+      }
+      stg128(orow + c * 8, pack8(o));
+    }
+  }
+}
+
+// cos/sin[t, i] = cos/sin(float(pos[t]) * inv_freq[i]), i < half.
+__global__ void rope_table_kernel(const int* __restrict__ pos, int n, const int* n_dev,
+                                  const float* __restrict__ inv_freq, int half,
+                                  float* __restrict__ cosb, float* __restrict__ sinb) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)N * half) return;
+  const int t = (int)(idx / half), i = (int)(idx % half);
+  const float a = (float)pos[t] * inv_freq[i];
+  float s, c;
+  sincosf(a, &s, &c);
+  cosb[idx] = c;
+  sinb[idx] = s;
+}
+
+// One wave per (token, head) over the q heads then the k heads; head_dim 128:
+// lane l owns the rotate-half pair (l, l + 64).
+//   in : qkv_pre row [q | k | v] (pre-norm, pre-RoPE projection output)
+//   out: qk row [q | k] after (optional per-head RMSNorm, rounded to bf16) + RoPE
+__global__ __launch_bounds__(256) void rope_fwd_kernel(
+    const bf16* __restrict__ in, long ldin, bf16* __restrict__ out, long ldout,
+    const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
+    const int* n_dev, int Hq, int Hkv, const bf16* __restrict__ qn_w,
+    const bf16* __restrict__ kn_w, float eps) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  const int H = Hq + Hkv;
+  const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= (long)N * H) return;
+  const int t = (int)(item / H), hh = (int)(item % H), l = threadIdx.x & 63;
+  const bf16* src = in + (long)t * ldin + hh * 128;
+  float x1 = (float)src[l], x2 = (float)src[l + 64];
+  const bf16* nw = hh < Hq ? qn_w : kn_w;
+  if (nw) {
+    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    const float inv = rsqrtf(ss / 128.f + eps);
+    x1 = (float)(bf16)((x1 * inv) * (float)nw[l]);
+    x2 = (float)(bf16)((x2 * inv) * (float)nw[l + 64]);
+  }
+  const float c = cosb[(long)t * 64 + l], s = sinb[(long)t * 64 + l];
+  bf16* dst = out + (long)t * ldout + hh * 128;
+  dst[l] = (bf16)(x1 * c - x2 * s);
+  dst[l + 64] = (bf16)(x2 * c + x1 * s);
+}
+
+// In-place RoPE backward on g[:, :(Hq+Hkv)*128] (then the per-head RMSNorm
+// backward against the pre-norm projection output when norm weights are given).
+__global__ __launch_bounds__(256) void rope_bwd_kernel(
+    bf16* __restrict__ g, long ldg, const bf16* __restrict__ pre, long ldp,
+    const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
+    const int* n_dev, int Hq, int Hkv, const bf16* __restrict__ qn_w,
+    const bf16* __restrict__ kn_w, float eps) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  const int H = Hq + Hkv;
+  const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= (long)N * H) return;
+  const int t = (int)(item / H), hh = (int)(item % H), l = threadIdx.x & 63;
+  bf16* gp = g + (long)t * ldg + hh * 128;
+  const float g1 = (float)gp[l], g2 = (float)gp[l + 64];
+  const float c = cosb[(long)t * 64 + l], s = sinb[(long)t * 64 + l];
+  float r1 = g1 * c + g2 * s;
+  float r2 = -g1 * s + g2 * c;
+  const bf16* nw = hh < Hq ? qn_w : kn_w;
+  if (nw) {
+    const bf16* xp = pre + (long)t * ldp + hh * 128;
+    const float x1 = (float)xp[l], x2 = (float)xp[l + 64];
+    const float inv = rsqrtf(wave_sum(x1 * x1 + x2 * x2) / 128.f + eps);
+    const float a1 = r1 * (float)nw[l], a2 = r2 * (float)nw[l + 64];
+    const float dot = wave_sum(a1 * (x1 * inv) + a2 * (x2 * inv));
+    const float k = dot / 128.f;
+    r1 = (a1 - (x1 * inv) * k) * inv;
+    r2 = (a2 - (x2 * inv) * k) * inv;
+  }
+  gp[l] = (bf16)r1;
+  gp[l + 64] = (bf16)r2;
+}
+
+// h[m, j] = bf16(silu(gate) * up) with gate = GU[m, j], up = GU[m, I + j].
+__global__ __launch_bounds__(256) void swiglu_h_kernel(const bf16* __restrict__ gu, long ldgu,
+                                                       bf16* __restrict__ h, long ldh, int n,
+                                                       const int* n_dev, int I) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  const int cpr = I >> 3;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)N * cpr) return;
+  const int m = (int)(idx / cpr), c = (int)(idx % cpr);
+  float g[8], u[8], o[8];
+  unpack8(ldg128(gu + (long)m * ldgu + c * 8), g);
+  unpack8(ldg128(gu + (long)m * ldgu + I + c * 8), u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = g[e] / (1.f + __expf(-g[e])) * u[e];
+  stg128(h + (long)m * ldh + c * 8, pack8(o));
+}
+
+// ------------------------------------------------------------------ launchers
+
+hipError_t rmsnorm_fwd(const bf16* x, long ldx, const bf16* w, bf16* y, long ldy, int rows,
+                       const int* rows_dev, int D, float eps, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3(rows), dim3(NORM_NT), 0, s, x, ldx, w, y, ldy,
+                     rows, rows_dev, D, eps);
+  return hipGetLastError();
+}
+
+hipError_t rmsnorm_bwd(const bf16* x, long ldx, const void* g, bool g_f32, long ldg,
+                       const bf16* w, const bf16* resid, long ldr, bf16* out, long ldo,
+                       int rows, const int* rows_dev, int D, float eps, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (g_f32)
+    hipLaunchKernelGGL(rmsnorm_bwd_kernel<float>, dim3(rows), dim3(NORM_NT), 0, s, x, ldx,
+                       (const float*)g, ldg, w, resid, ldr, out, ldo, rows, rows_dev, D, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_bwd_kernel<bf16>, dim3(rows), dim3(NORM_NT), 0, s, x, ldx,
+                       (const bf16*)g, ldg, w, resid, ldr, out, ldo, rows, rows_dev, D, eps);
+  return hipGetLastError();
+}
+
+hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_freq,
+                      int half, float* cosb, float* sinb, hipStream_t s) {
+  const long tot = (long)n * half;
+  if (tot <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
+                     pos, n, n_dev, inv_freq, half, cosb, sinb);
+  return hipGetLastError();
+}
+
+hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s) {
+  const long items = (long)n * (Hq + Hkv);
+  if (items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_fwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, in,
+                     ldin, out, ldout, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+  return hipGetLastError();
+}
+
+hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* cosb,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s) {
+  const long items = (long)n * (Hq + Hkv);
+  if (items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_bwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, g,
+                     ldg, pre, ldp, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+  return hipGetLastError();
+}
+
+hipError_t swiglu_h(const bf16* gu, long ldgu, bf16* h, long ldh, int n, const int* n_dev,
+                    int I, hipStream_t s) {
+  const long tot = (long)n * (I >> 3);
+  if (tot <= 0) return hipSuccess;
+  hipLaunchKernelGGL(swiglu_h_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, gu,
+                     ldgu, h, ldh, n, n_dev, I);
+  return hipGetLastError();
+}
+
+}  // namespace dsb

@@ -1,0 +1,153 @@
+"""ctypes binding of ``libdsb.so`` (the C-ABI declared in ``include/dsb.h``).
+
+The library is built in-tree by ``make -C deltaserve-vllm_amd/csrc`` (or
+``__graft_entry__.build()``) into ``deltaserve_amd/_lib/libdsb.so``. There is
+no fallback: every entry point raises when the library is missing, so a
+backward never silently runs anything but the HIP path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import (POINTER, Structure, c_char_p, c_float, c_int, c_int32, c_int64,
+                    c_uint32, c_void_p)
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
+LIB_PATH = os.path.join(LIB_DIR, "libdsb.so")
+
+ABI_VERSION = 1
+FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
+ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
+PROJS = ("q", "k", "v", "o", "gate", "up", "down")
+PROJ_INDEX = {p: i for i, p in enumerate(PROJS)}
+FLAG_GRAPH, FLAG_NO_CLIP = 1, 2
+
+
+class DsbDesc(Structure):
+    _fields_ = [
+        ("abi_version", c_int32), ("family", c_int32),
+        ("n_layers", c_int32), ("hidden", c_int32), ("n_heads", c_int32),
+        ("n_kv_heads", c_int32), ("head_dim", c_int32), ("intermediate", c_int32),
+        ("vocab", c_int32), ("lora_rank", c_int32),
+        ("lora_scaling", c_float), ("rms_eps", c_float), ("rope_theta", c_float),
+        ("rope_type", c_int32), ("rope_factor", c_float),
+        ("rope_low_freq_factor", c_float), ("rope_high_freq_factor", c_float),
+        ("rope_orig_max_pos", c_float),
+        ("s_max", c_int32), ("max_seqs", c_int32),
+        ("beta1", c_float), ("beta2", c_float), ("adam_eps", c_float),
+        ("weight_decay", c_float), ("max_grad_norm", c_float),
+        ("flags", c_uint32),
+    ]
+
+
+class DsbLayerWeights(Structure):
+    _fields_ = [(k, c_void_p) for k in
+                ("qkv", "o", "gate_up", "down", "in_ln", "post_ln", "q_norm", "k_norm")]
+
+
+class DsbLoraTensors(Structure):
+    _fields_ = [("A", c_void_p), ("B", c_void_p), ("gA", c_void_p), ("gB", c_void_p)]
+
+
+class DsbActivations(Structure):
+    _fields_ = [("layer_in", POINTER(c_void_p)), ("final_in", c_void_p),
+                ("input_ids", c_void_p), ("ld", c_int64)]
+
+
+class DsbCycleInfo(Structure):
+    _fields_ = [("gpu_ms", c_float), ("graph", c_int32), ("n_valid", c_int32)]
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "dsb_create": (c_int, [POINTER(DsbDesc), POINTER(c_void_p)]),
+    "dsb_destroy": (None, [c_void_p]),
+    "dsb_last_error": (c_char_p, [c_void_p]),
+    "dsb_bind_weights": (c_int, [c_void_p, c_int, POINTER(DsbLayerWeights)]),
+    "dsb_bind_head": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "dsb_bind_lora": (c_int, [c_void_p, c_int, c_int, POINTER(DsbLoraTensors)]),
+    "dsb_bind_activations": (c_int, [c_void_p, POINTER(DsbActivations)]),
+    "dsb_step": (c_int, [c_void_p, POINTER(c_int32), c_int, c_int, c_float, c_int64,
+                         c_void_p, POINTER(c_float), POINTER(c_int),
+                         POINTER(DsbCycleInfo)]),
+    "dsb_reset_optimizer": (c_int, [c_void_p, c_float]),
+    "dsb_pack": (c_int, [POINTER(c_int32), c_int, c_int, POINTER(c_int32),
+                         POINTER(c_int32)]),
+    "dsb_rope_inv_freq": (c_int, [c_int, c_float, c_int, c_float, c_float, c_float,
+                                  c_float, POINTER(c_float)]),
+    "dsb_op_gemm": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                            c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p,
+                            c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p]),
+    "dsb_op_rmsnorm": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int,
+                               c_int, c_float, c_void_p]),
+    "dsb_op_rmsnorm_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int64, c_void_p,
+                                   c_void_p, c_int64, c_void_p, c_int64, c_int, c_int,
+                                   c_float, c_void_p]),
+    "dsb_op_rope_table": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p,
+                                  c_void_p]),
+    "dsb_op_rope": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int,
+                            c_int, c_int, c_void_p, c_void_p, c_float, c_void_p]),
+    "dsb_op_rope_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                c_int, c_int, c_int, c_void_p, c_void_p, c_float,
+                                c_void_p]),
+    "dsb_op_attn_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                c_void_p, c_int64, c_void_p, c_void_p, POINTER(c_int32),
+                                c_int, c_int, c_int, c_void_p]),
+    "dsb_op_attn_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
+                                c_void_p, c_int64, c_void_p, c_int64, POINTER(c_int32),
+                                c_int, c_int, c_int, c_void_p]),
+    "dsb_op_head": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, POINTER(c_int32), c_int,
+                            c_int, c_int, c_int, c_void_p, POINTER(c_float), POINTER(c_int),
+                            c_void_p]),
+    "dsb_op_lora_tn": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_int, c_int,
+                               c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "dsb_op_clip_adamw": (c_int, [POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
+                                  POINTER(c_void_p), POINTER(c_int32), POINTER(c_int32),
+                                  c_int, c_int, c_float, c_float, c_float, c_float, c_float,
+                                  c_int64, c_float, c_int, c_void_p]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+_lib = None
+
+
+class DsbError(RuntimeError):
+    """A libdsb call returned non-zero (message from dsb_last_error)."""
+
+
+def load(path: str | None = None):
+    """Load libdsb.so once; raises ``DsbError`` if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise DsbError(
+            f"libdsb.so not found at {p}; build it with "
+            "`make -C deltaserve-vllm_amd/csrc` or __graft_entry__.build()")
+    lib = ctypes.CDLL(p)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error(handle=None) -> str:
+    msg = load().dsb_last_error(handle)
+    return msg.decode(errors="replace") if msg else "unknown error"
+
+
+def check(rc: int, handle=None, what: str = "libdsb") -> None:
+    if rc != 0:
+        raise DsbError(f"{what}: {last_error(handle)}")
+
+
+def i32_array(values):
+    vals = [int(v) for v in values]
+    return (c_int32 * max(len(vals), 1))(*vals)

@@ -1,0 +1,432 @@
+"""``LoraSftTrainerService`` — the drop-in LoRA-SFT backward child on MI355X.
+
+Same surface as the reference's ``bwd_services/common/trainer.py``:
+``_build_state`` turns the shared ``base``/``ft``/``meta`` dicts into bound
+state, ``process_backward(activations, sample_lens, n, epoch) -> (loss,
+n_valid)`` runs one cycle, and ``save_adapter`` / ``export_lora_state`` /
+``switch_adapter`` / ``_publish_to_served`` keep their behaviour. The fp32
+LoRA masters stay torch ``nn.Parameter``s (their ``.grad`` holds the clipped
+gradient after a cycle) so every reader of them is unchanged.
+
+What differs is where the cycle runs: ``libdsb.so`` executes the whole
+head → reversed-layer → clip → AdamW sequence as one captured hipGraph of
+hand-written gfx950 kernels (``include/dsb.h``). There is no eager PyTorch
+path and no CPU path: if the library is missing the service fails to build.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from ctypes import byref, c_float, c_int, c_void_p
+
+import torch
+import torch.nn as nn
+
+from deltaserve_amd import _lib as L
+from deltaserve_amd import dprint
+from deltaserve_amd.bwd_services.base import BackwardService
+from deltaserve_amd.bwd_services.common.family import LORA_PROJS, Family
+from deltaserve_amd.ops import rope_inv_freq  # noqa: F401  (re-exported for callers)
+
+# PEFT adapter keys turned into fp32 masters (trainer.py:46-47, extended to the
+# MLP projections).
+_LORA_KEY_RE = re.compile(
+    r"layers\.(\d+)\.(?:self_attn|mlp)\.(q|k|v|o|gate|up|down)_proj\.lora_([AB])\.weight")
+
+_DEFAULT_MAX_SEQS = 256
+
+
+class LoraSftTrainerService(BackwardService):
+    """Backward child that trains the FT LoRA adapter for one model family."""
+
+    family: Family = None
+
+    def __init__(self, device_index: int) -> None:
+        super().__init__(device_index)
+        assert self.family is not None, f"{type(self).__name__} must set ``family``"
+        self._built = False
+        self.lora: dict = {}
+        self._grads: dict = {}
+        self._ft_keys: dict = {}
+        self._cycles_attempted = 0
+        self._last_cycle_epoch = None
+        self._pending_epoch_save = None
+        self._h = None
+        self._act_key = None
+        self._opt_step = 0
+        self._keep: list = []
+        self.lr = 0.0
+        self.weight_decay = 0.0
+        self.gamma = 1.0
+        self.last_cycle_info = None
+
+    # ------------------------------------------------------------ build
+    def _on_weights_shared(self) -> str | None:
+        """trainer.py:98-110: a build failure is returned to the worker."""
+        try:
+            self._build_state()
+            self._built = True
+            return None
+        except Exception as e:  # noqa: BLE001 — reported to the worker
+            import traceback
+            dprint(f"[backward] {self.family.name} state build failed: {e}")
+            traceback.print_exc()
+            return f"{type(e).__name__}: {e}"
+
+    def _build_state(self) -> None:
+        meta = self.shared["meta"]
+        base = self.shared["base"] or {}
+        ft = self.shared["ft"] or {}
+        fam = self.family
+        if int(meta.get("tp_size", 1)) != 1:
+            raise NotImplementedError("the MI355X backward runs one GPU per model (tp_size 1)")
+        self.tp_size, self.tp_rank = 1, 0
+        self.D = int(meta["hidden_size"])
+        self.L = int(meta["num_hidden_layers"])
+        self.Hq = int(meta["num_attention_heads"])
+        self.Hkv = int(meta["num_key_value_heads"])
+        self.Hd = int(meta["head_dim"])
+        self.q_size, self.kv_size = self.Hq * self.Hd, self.Hkv * self.Hd
+        self.inter = int(meta["intermediate_size"])
+        self.theta = float(meta["rope_theta"])
+        self.rope_scaling = meta.get("rope_scaling")
+        self.eps = float(meta["rms_norm_eps"])
+        self.scaling = float(meta.get("lora_scaling", 1.0))
+        self.vocab = int(meta["vocab_size"])
+        self.lr = float(meta["learning_rate"])
+        self.weight_decay = float(meta.get("weight_decay", 0.0))
+        self.gamma = float(meta.get("gamma", 1.0))
+        if meta.get("backward_fp32"):
+            dprint("[backward] backward_fp32 requested: the MI355X path computes every "
+                   "product with bf16 operands and fp32 accumulation")
+
+        bn = {k.replace(".base_layer.", "."): v for k, v in base.items()}
+
+        def bw(name):
+            if name not in bn:
+                raise KeyError(f"base weight {name!r} not found (have e.g. "
+                               f"{list(bn)[:4]} … {len(bn)} keys)")
+            t = bn[name]
+            if t.dtype != torch.bfloat16 or not t.is_cuda:
+                raise TypeError(f"base weight {name!r} must be a bf16 CUDA tensor")
+            return t
+
+        self.lm_w = bw(meta.get("lm_head_key") or "lm_head.weight")[:self.vocab].contiguous()
+        self.norm_w = bw(meta.get("norm_weight_key") or "model.norm.weight")
+
+        layers = []
+        for i in range(self.L):
+            p = f"model.layers.{i}."
+            lw = {}
+            for key, rel in fam.layer_weights.items():
+                if key == "qkv" and p + rel not in bn:
+                    parts = [bw(p + f"self_attn.{x}_proj.weight") for x in ("q", "k", "v")]
+                    lw[key] = torch.cat(parts, 0).contiguous()
+                elif key == "gate_up" and p + rel not in bn:
+                    parts = [bw(p + f"mlp.{x}_proj.weight") for x in ("gate", "up")]
+                    lw[key] = torch.cat(parts, 0).contiguous()
+                else:
+                    lw[key] = bw(p + rel).contiguous()
+            layers.append(lw)
+        self._base_layers = layers
+
+        params = []
+        rank = None
+        for key, t in ft.items():
+            m = _LORA_KEY_RE.search(key)
+            if m is None:
+                continue
+            layer, proj, ab = int(m.group(1)), m.group(2), m.group(3)
+            param = nn.Parameter(t.detach().to(self.lm_w.device, torch.float32).clone().contiguous())
+            grad = torch.zeros_like(param)
+            param.grad = grad
+            self.lora.setdefault(layer, {}).setdefault(proj, {})[ab] = param
+            self._grads[(layer, proj, ab)] = grad
+            self._ft_keys[(layer, proj, ab)] = key
+            params.append(param)
+            r = param.shape[0] if ab == "A" else param.shape[1]
+            if rank is not None and r != rank:
+                raise ValueError(f"LoRA tensors disagree on the rank ({rank} vs {r})")
+            rank = r
+        if rank is None:
+            raise ValueError("the FT adapter holds no LoRA tensors")
+        self.rank = rank
+        self._train_state_bytes = 4 * 4 * sum(p.numel() for p in params)
+
+        s_max = int(meta.get("max_saved_finetuning_tokens", 0) or 0)
+        self._s_max = s_max
+        self._max_seqs = int(meta.get("backward_max_seqs", 0) or min(max(s_max, 1), _DEFAULT_MAX_SEQS))
+        if s_max > 0:
+            self._create_handle(s_max)
+        dprint(f"[backward] {fam.name} built: {self.L} layers, {len(params)} LoRA tensors, "
+               f"r={self.rank}, scaling={self.scaling}, rope="
+               f"{(self.rope_scaling or {}).get('rope_type', 'default')}(theta={self.theta:g}), "
+               f"lr={self.lr}, wd={self.weight_decay}, gamma={self.gamma}")
+
+    def _create_handle(self, s_max: int) -> None:
+        lib = L.load()
+        rs = self.rope_scaling or {}
+        rtype = rs.get("rope_type", "default") or "default"
+        codes = {"default": L.ROPE_DEFAULT, "linear": L.ROPE_LINEAR, "llama3": L.ROPE_LLAMA3}
+        if rtype not in codes:
+            raise NotImplementedError(f"RoPE type {rtype!r} is not supported")
+        d = L.DsbDesc()
+        d.abi_version = L.ABI_VERSION
+        d.family = self.family.dsb_family
+        d.n_layers, d.hidden, d.n_heads, d.n_kv_heads = self.L, self.D, self.Hq, self.Hkv
+        d.head_dim, d.intermediate, d.vocab, d.lora_rank = self.Hd, self.inter, self.vocab, self.rank
+        d.lora_scaling, d.rms_eps, d.rope_theta = self.scaling, self.eps, self.theta
+        d.rope_type = codes[rtype]
+        d.rope_factor = float(rs.get("factor", 1.0))
+        d.rope_low_freq_factor = float(rs.get("low_freq_factor", 1.0))
+        d.rope_high_freq_factor = float(rs.get("high_freq_factor", 1.0))
+        d.rope_orig_max_pos = float(rs.get("original_max_position_embeddings", 1.0))
+        d.s_max, d.max_seqs = int(s_max), int(self._max_seqs)
+        d.beta1, d.beta2, d.adam_eps = 0.9, 0.999, 1e-8
+        d.weight_decay, d.max_grad_norm = self.weight_decay, 1.0
+        meta = self.shared["meta"]
+        d.flags = L.FLAG_GRAPH if meta.get("backward_hip_graph", True) else 0
+        h = c_void_p()
+        L.check(lib.dsb_create(byref(d), byref(h)), None, "dsb_create")
+        self._h = h
+        self._s_max = int(s_max)
+        for i, lw in enumerate(self._base_layers):
+            w = L.DsbLayerWeights()
+            for key in ("qkv", "o", "gate_up", "down", "in_ln", "post_ln", "q_norm", "k_norm"):
+                t = lw.get(key)
+                setattr(w, key, None if t is None else t.data_ptr())
+            L.check(lib.dsb_bind_weights(h, i, byref(w)), h, "dsb_bind_weights")
+        L.check(lib.dsb_bind_head(h, self.lm_w.data_ptr(), self.norm_w.data_ptr()), h,
+                "dsb_bind_head")
+        for (layer, proj, ab), _ in self._ft_keys.items():
+            if ab != "A":
+                continue
+            pa, pb = self.lora[layer][proj]["A"], self.lora[layer][proj]["B"]
+            t = L.DsbLoraTensors(pa.data_ptr(), pb.data_ptr(), self._grads[(layer, proj, "A")].data_ptr(),
+                                 self._grads[(layer, proj, "B")].data_ptr())
+            L.check(lib.dsb_bind_lora(h, layer, L.PROJ_INDEX[proj], byref(t)), h, "dsb_bind_lora")
+
+    def _bind_activations(self, activations) -> None:
+        li = activations["layer_in"]
+        fi = activations["final_in"]
+        ids = activations["concat_input_ids"]
+        if len(li) != self.L:
+            raise ValueError(f"activations carry {len(li)} layer inputs, the model has {self.L}")
+        ld = fi.stride(0)
+        for t in list(li) + [fi]:
+            if t.dtype != torch.bfloat16 or not t.is_cuda or t.stride(0) != ld or t.stride(1) != 1:
+                raise TypeError("activation buffers must be bf16 CUDA [rows, D] with one row stride")
+        if ids.dtype != torch.int64 or not ids.is_cuda:
+            raise TypeError("concat_input_ids must be an int64 CUDA tensor")
+        key = (tuple(t.data_ptr() for t in li), fi.data_ptr(), ids.data_ptr(), ld)
+        if key == self._act_key:
+            return
+        ptrs = (c_void_p * self.L)(*[t.data_ptr() for t in li])
+        self._act_ptrs = ptrs
+        a = L.DsbActivations(ctypes.cast(ptrs, ctypes.POINTER(c_void_p)), fi.data_ptr(),
+                             ids.data_ptr(), ld)
+        L.check(L.load().dsb_bind_activations(self._h, byref(a)), self._h, "dsb_bind_activations")
+        self._act_key = key
+
+    # ------------------------------------------------------------ the cycle
+    def process_backward(self, activations, sample_lens, n, epoch):
+        """trainer.py:503-678 — one backward + AdamW step; returns (loss, n_valid)."""
+        self._maybe_pause()
+        if not self._built:
+            raise RuntimeError(
+                f"{self.family.name} backward state not built (weights not shared)")
+        self._last_mode = "graph"
+        seq_lens = [int(s) for s in sample_lens]
+        n = int(n)
+        if self._h is None:
+            self._create_handle(int(activations["final_in"].shape[0]) - 1)
+        if n > self._s_max:
+            raise ValueError(f"n={n} exceeds the backward capacity s_max={self._s_max}")
+        self._bind_activations(activations)
+        self._opt_step += 1
+        loss = c_float(0.0)
+        nv = c_int(0)
+        info = L.DsbCycleInfo()
+        stream = c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = L.load().dsb_step(self._h, L.i32_array(seq_lens), len(seq_lens), n, float(self.lr),
+                               int(self._opt_step), stream, byref(loss), byref(nv), byref(info))
+        if rc != 0:
+            self._opt_step -= 1
+            L.check(rc, self._h, "dsb_step")
+        self.last_cycle_info = {"gpu_ms": info.gpu_ms, "graph": bool(info.graph),
+                                "n_valid": info.n_valid}
+        self._last_mode = "graph" if info.graph else "eager"
+        if epoch > self.current_epoch:
+            self.lr *= self.gamma  # StepLR(step_size=1, gamma) stepped per epoch advance
+            self.current_epoch = epoch
+        self._publish_to_served()
+        return float(loss.value), int(nv.value)
+
+    # ------------------------------------------------------------ checkpoints
+    @torch.no_grad()
+    def _gather_adapter(self):
+        try:
+            local = {key: self.lora[k[0]][k[1]][k[2]].detach().to("cpu", copy=True)
+                     for k, key in self._ft_keys.items()}
+            return local, None
+        except Exception as e:  # noqa: BLE001
+            return None, f"rank 0: {type(e).__name__}: {e}"
+
+    def _snapshot(self, reason: str, epoch: int):
+        tensors, error = self._gather_adapter()
+        state = {"reason": reason, "epoch": int(epoch),
+                 "backward_cycles": int(self._cycles_attempted),
+                 "tokens_trained": int(self._total_tokens_trained),
+                 "last_loss": self._last_loss,
+                 "learning_rate": float(self.lr),
+                 "tp_size": 1,
+                 "source_adapter": self.shared["meta"].get("finetuning_lora_path")}
+        return tensors, error, state
+
+    def _write_adapter(self, out_dir: str, save_id: str, snap) -> None:
+        from deltaserve_amd.adapter_io import write_peft_adapter, write_save_error
+
+        tensors, error, state = snap
+        if error is None:
+            try:
+                write_peft_adapter(out_dir, tensors,
+                                   source_dir=self.shared["meta"].get("finetuning_lora_path"),
+                                   scaling=self.scaling, state={"save_id": save_id, **state})
+                dprint(f"[backward] adapter saved ({state['reason']}) → {out_dir}")
+                return
+            except Exception as e:  # noqa: BLE001
+                error = f"{type(e).__name__}: {e}"
+        dprint(f"[backward] adapter save ({state['reason']}) to {out_dir} FAILED: {error}")
+        write_save_error(out_dir, save_id, error)
+
+    def save_adapter(self, out_dir: str, save_id: str, reason: str = "manual") -> None:
+        if not self._built:
+            from deltaserve_amd.adapter_io import write_save_error
+            write_save_error(out_dir, save_id, "trainer state not built")
+            return
+        self._write_adapter(out_dir, save_id, self._snapshot(reason, self.current_epoch))
+
+    def _handle_save_adapter(self, msg) -> None:
+        self.save_adapter(str(msg.get("path")), str(msg.get("save_id")))
+
+    def _save_policy(self):
+        meta = self.shared.get("meta") or {}
+        return (meta.get("adapter_save_path"),
+                int(meta.get("adapter_save_every_backwards", 0) or 0),
+                bool(meta.get("adapter_save_every_epoch", False)),
+                int(meta.get("adapter_save_keep_last", 0) or 0))
+
+    def _before_cycle(self, epoch: int, attempted: bool) -> None:
+        root, _, every_epoch, _ = self._save_policy()
+        if (attempted and root and every_epoch and self._built
+                and self._last_cycle_epoch is not None and epoch > self._last_cycle_epoch):
+            e = self._last_cycle_epoch
+            self._pending_epoch_save = (e, self._snapshot("epoch", e))
+
+    def _after_cycle(self, epoch: int, attempted: bool) -> None:
+        if not attempted:
+            return
+        self._cycles_attempted += 1
+        self._last_cycle_epoch = epoch
+        root, every_n, _, keep_last = self._save_policy()
+        if self._pending_epoch_save is not None:
+            e, snap = self._pending_epoch_save
+            self._pending_epoch_save = None
+            self._write_adapter(os.path.join(root, f"epoch-{e}"), f"epoch-{e}", snap)
+        if root and every_n > 0 and self._built and self._cycles_attempted % every_n == 0:
+            name = f"backward-{self._cycles_attempted:06d}"
+            self._write_adapter(os.path.join(root, name), name,
+                                self._snapshot("every_backwards", epoch))
+            from deltaserve_amd.adapter_io import prune_checkpoints
+            prune_checkpoints(root, "backward-", keep_last)
+
+    # ------------------------------------------------------------ adapters
+    @staticmethod
+    def _key_of(key: str):
+        m = _LORA_KEY_RE.search(key)
+        return None if m is None else (int(m.group(1)), m.group(2), m.group(3))
+
+    def export_lora_state(self) -> dict:
+        """trainer.py:749-754: the masters as {PEFT key: fp32 CPU tensor}."""
+        return {key: self.lora[layer][proj][ab].detach().float().cpu().clone()
+                for (layer, proj, ab), key in self._ft_keys.items()}
+
+    def switch_adapter(self, ft: dict, hparams: dict) -> dict:
+        """trainer.py:680-742: copy another adapter into the masters in place
+        (graph and served slot stay valid), fresh optimizer and schedule."""
+        if not self._built:
+            raise RuntimeError("the trainer was never built (no adapter at launch)")
+        scaling = float(hparams.get("lora_scaling", self.scaling))
+        if abs(scaling - self.scaling) > 1e-9:
+            raise ValueError(f"the adapter's alpha/r is {scaling}, the launch adapter's is "
+                             f"{self.scaling}; they must match")
+        new = {}
+        for key, t in ft.items():
+            k = self._key_of(key)
+            if k is not None:
+                new[k] = t
+        have = {(layer, proj, ab): p for layer, d in self.lora.items()
+                for proj, dd in d.items() for ab, p in dd.items()}
+        if set(new) != set(have):
+            raise ValueError(f"the adapter has {len(new)} LoRA tensors, the launch adapter "
+                             f"{len(have)} (different target modules or layers)")
+        for k, p in have.items():
+            if tuple(new[k].shape) != tuple(p.shape):
+                raise ValueError(f"LoRA tensor {k} has shape {tuple(new[k].shape)}, the launch "
+                                 f"adapter's is {tuple(p.shape)} (different rank?)")
+        if hparams.get("dry_run"):
+            return {"tensors": len(have), "dry_run": True}
+        with torch.no_grad():
+            for k, p in have.items():
+                p.copy_(new[k].to(p.device, torch.float32))
+                self._grads[k].zero_()
+        self.lr = float(hparams["learning_rate"])
+        self.weight_decay = float(hparams["weight_decay"])
+        self.gamma = float(hparams["gamma"])
+        self._opt_step = 0
+        if self._h is not None:
+            L.check(L.load().dsb_reset_optimizer(self._h, self.weight_decay), self._h,
+                    "dsb_reset_optimizer")
+        self.current_epoch = 0
+        self._cur_epoch_seen = 0
+        self._epoch_processed_tokens = 0
+        self._total_tokens_per_epoch = int(hparams.get("total_tokens_per_epoch", 0))
+        self._ft_keys = {k: key for key in ft for k in [self._key_of(key)] if k is not None}
+        self._publish_to_served()
+        dprint(f"[backward] switched to a new adapter: {len(have)} LoRA tensors, "
+               f"lr={self.lr}, wd={self.weight_decay}, gamma={self.gamma}")
+        return {"tensors": len(have)}
+
+    @torch.no_grad()
+    def _publish_to_served(self) -> None:
+        """trainer.py:760-802: clamp ±6.5e4, bake α/r into B, cast, copy into the
+        served slot of vLLM's stacked LoRA buffers (every trained projection)."""
+        if not self.lora_buffers:
+            return
+        slot = int(self.lora_buffers["slot"])
+        for i, projd in self.lora_buffers["layers"].items():
+            ld = self.lora.get(int(i), {})
+            for proj, buf in projd.items():
+                pa = ld.get(proj, {}).get("A")
+                pb = ld.get(proj, {}).get("B")
+                if pa is None:
+                    continue
+                a_buf, b_buf = buf["a"], buf["b"]
+                r, in_dim = pa.shape
+                out_dim = pb.shape[0]
+                a_buf[slot, 0, :r, :in_dim].copy_(pa.clamp(-6.5e4, 6.5e4).to(a_buf.dtype))
+                b_buf[slot, 0, :out_dim, :r].copy_(
+                    (pb * self.scaling).clamp(-6.5e4, 6.5e4).to(b_buf.dtype))
+
+    def close(self) -> None:
+        if self._h is not None:
+            L.load().dsb_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass

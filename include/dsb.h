@@ -1,0 +1,190 @@
+/* dsb.h — C-ABI of the MI355X (gfx950) DeltaServe LoRA-SFT backward.
+ *
+ * One shared library, libdsb.so, loaded by ctypes into the backward child
+ * (PyTorch-ROCm owns device memory and the LoRA master tensors). Plain
+ * pointers and sizes only; every device pointer is a HIP device address.
+ * Every function returns 0 on success and non-zero on failure, with the
+ * message available from dsb_last_error().
+ *
+ * Reference interface replaced (paths relative to the reference checkout):
+ *   the cycle  LoraSftTrainerService.process_backward
+ *              deltaserve-plugin/deltaserve/bwd_services/common/trainer.py:503-678
+ *   its state  LoraSftTrainerService._build_state           trainer.py:112-296
+ *   its math   bwd_services/llama3.py:62-219, qwen3.py:68-204,
+ *              common/{ops,attention,ffn,head}.py
+ */
+#ifndef DSB_H_
+#define DSB_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSB_ABI_VERSION 1
+
+enum { DSB_FAMILY_LLAMA3 = 0, DSB_FAMILY_QWEN3 = 1 };
+enum { DSB_ROPE_DEFAULT = 0, DSB_ROPE_LINEAR = 1, DSB_ROPE_LLAMA3 = 2 };
+enum {
+  DSB_PROJ_Q = 0, DSB_PROJ_K = 1, DSB_PROJ_V = 2, DSB_PROJ_O = 3,
+  DSB_PROJ_GATE = 4, DSB_PROJ_UP = 5, DSB_PROJ_DOWN = 6, DSB_NUM_PROJ = 7
+};
+/* dsb_desc.flags */
+enum { DSB_FLAG_GRAPH = 1u, DSB_FLAG_NO_CLIP = 2u };
+
+typedef struct dsb_handle dsb_handle;
+
+/* Model and trainer constants: the backward `meta` dict of
+ * deltaserve-plugin/deltaserve/ft_meta.py:131-213 plus the AdamW settings of
+ * trainer.py:252-256. head_dim must be 128; lora_rank a multiple of 8. */
+typedef struct dsb_desc {
+  int32_t abi_version;       /* DSB_ABI_VERSION */
+  int32_t family;            /* DSB_FAMILY_* (Qwen3 adds per-head q/k RMSNorm) */
+  int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate, vocab;
+  int32_t lora_rank;
+  float lora_scaling;        /* alpha / r */
+  float rms_eps;
+  float rope_theta;
+  int32_t rope_type;         /* DSB_ROPE_* (ops.py:26-57) */
+  float rope_factor, rope_low_freq_factor, rope_high_freq_factor, rope_orig_max_pos;
+  int32_t s_max;             /* token capacity of one cycle (max_saved_finetuning_tokens) */
+  int32_t max_seqs;          /* sequence capacity of one cycle */
+  float beta1, beta2, adam_eps, weight_decay, max_grad_norm;
+  uint32_t flags;            /* DSB_FLAG_* */
+} dsb_desc;
+
+/* Frozen bf16 base weights of one decoder layer, borrowed (the IPC-shared
+ * vLLM tensors of trainer.py:201-218: fused qkv_proj and gate_up_proj). */
+typedef struct dsb_layer_weights {
+  const void* qkv;      /* [q + 2kv, D] */
+  const void* o;        /* [D, q] */
+  const void* gate_up;  /* [2I, D] (gate rows first) */
+  const void* down;     /* [D, I] */
+  const void* in_ln;    /* [D] */
+  const void* post_ln;  /* [D] */
+  const void* q_norm;   /* [head_dim] (Qwen3) or NULL */
+  const void* k_norm;   /* [head_dim] (Qwen3) or NULL */
+} dsb_layer_weights;
+
+/* One LoRA projection: fp32 PEFT masters A [r, in], B [out, r] and their
+ * gradient buffers (torch-owned; the cycle writes the clipped gradient). */
+typedef struct dsb_lora_tensors {
+  float* A;
+  float* B;
+  float* gA;
+  float* gB;
+} dsb_lora_tensors;
+
+/* The captured-activation store (accumulate.py:236-252): per-layer residual
+ * inputs and the pre-final-norm residual, bf16 [s_max + 1, D] rows of stride
+ * `ld`, and the token ids int64 [s_max]. Only rows [0, n) are read. */
+typedef struct dsb_activations {
+  const void* const* layer_in;  /* n_layers pointers */
+  const void* final_in;
+  const int64_t* input_ids;
+  int64_t ld;
+} dsb_activations;
+
+/* Per-cycle device timing (ms), filled by dsb_step when requested. */
+typedef struct dsb_cycle_info {
+  float gpu_ms;
+  int32_t graph;       /* 1 if the cycle replayed the captured hipGraph */
+  int32_t n_valid;
+} dsb_cycle_info;
+
+/* Creates the backward state (replaces _build_state's dims/optimizer part,
+ * trainer.py:112-256). */
+int dsb_create(const dsb_desc* desc, dsb_handle** out);
+void dsb_destroy(dsb_handle* h);
+/* Message of the last failure on this thread (h may be NULL). */
+const char* dsb_last_error(const dsb_handle* h);
+
+/* Binds layer `layer`'s base weights (trainer.py:201-218). Makes the
+ * transposed copies the dX products read, once. */
+int dsb_bind_weights(dsb_handle* h, int layer, const dsb_layer_weights* w);
+/* Binds the LM head [vocab, D] and the final RMSNorm weight [D] (trainer.py:194-195). */
+int dsb_bind_head(dsb_handle* h, const void* lm_head, const void* final_norm);
+/* Binds one LoRA projection (trainer.py:231-243); proj is DSB_PROJ_*. q/k/v
+ * must be bound together, and gate/up together. */
+int dsb_bind_lora(dsb_handle* h, int layer, int proj, const dsb_lora_tensors* t);
+/* Binds the shared activation buffers (base.py:438-461 share_activations). */
+int dsb_bind_activations(dsb_handle* h, const dsb_activations* a);
+
+/* One backward cycle + AdamW step: trainer.py:503-678 without the publish.
+ * seq_lens: host int32[nseq] in request order, summing to n <= s_max.
+ * lr: this cycle's learning rate; step: the optimizer step count t >= 1.
+ * stream: the caller's hipStream_t (work is ordered after it and it waits
+ * for the cycle). Writes the mean loss and the number of predicting rows. */
+int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, int64_t step,
+             void* stream, float* loss, int* n_valid, dsb_cycle_info* info);
+
+/* Zeroes the AdamW moments and sets the weight decay: the fresh optimizer
+ * of LoraSftTrainerService.switch_adapter (trainer.py:725-731). The masters
+ * keep their addresses, so a captured graph stays valid. */
+int dsb_reset_optimizer(dsb_handle* h, float weight_decay);
+
+/* Integer packing of a cycle, host only (trainer.py:510-518, head.py:63-72):
+ * positions[n], pred[n] (1 if row t predicts ids[t+1]), returns n_valid or -1. */
+int dsb_pack(const int32_t* seq_lens, int nseq, int n, int32_t* positions, int32_t* pred);
+
+/* RoPE inverse frequencies [head_dim/2] (ops.py:26-57), host only. */
+int dsb_rope_inv_freq(int head_dim, float theta, int rope_type, float factor, float low,
+                      float high, float orig_max, float* out);
+
+/* ---- single-op entry points (parity tests; synchronous on `stream`) ---- */
+
+/* C = A·Bᵀ (+ A2·B2ᵀ) [+ R]; out_f32 selects fp32 C (accumulate adds to C). */
+int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
+                int64_t lda2, const void* B2, int64_t ldb2, int M, int N, int K1, int K2,
+                void* C, int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr,
+                int cfg, void* stream);
+/* ops.py:84-88 */
+int dsb_op_rmsnorm(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int rows,
+                   int D, float eps, void* stream);
+/* ops.py:91-100, plus the bf16 residual add of llama3.py:205 / ffn.py:47-48. */
+int dsb_op_rmsnorm_bwd(const void* x, int64_t ldx, const void* g, int g_f32, int64_t ldg,
+                       const void* w, const void* resid, int64_t ldr, void* out, int64_t ldo,
+                       int rows, int D, float eps, void* stream);
+/* ops.py:60-65 cos/sin table [n, head_dim/2] fp32 from int32 positions. */
+int dsb_op_rope_table(const int32_t* pos, int n, const float* inv_freq, int half, float* cos_out,
+                      float* sin_out, void* stream);
+/* ops.py:68-73 (+ qwen3.py:96-107 when norm weights are given). */
+int dsb_op_rope(const void* qkv_pre, int64_t ldin, void* qk_out, int64_t ldout,
+                const float* cos_t, const float* sin_t, int n, int Hq, int Hkv,
+                const void* q_norm, const void* k_norm, float eps, void* stream);
+/* ops.py:76-81 (+ qwen3.py:133-144), in place on g. */
+int dsb_op_rope_bwd(void* g, int64_t ldg, const void* qkv_pre, int64_t ldp, const float* cos_t,
+                    const float* sin_t, int n, int Hq, int Hkv, const void* q_norm,
+                    const void* k_norm, float eps, void* stream);
+/* attention.py:20-45; o32 [n, Hq*128] fp32 and lse [Hq, n] (log2 domain) out. */
+int dsb_op_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                    int64_t ldv, void* ctx, int64_t ldc, float* o32, float* lse,
+                    const int32_t* seq_lens, int nseq, int Hq, int Hkv, void* stream);
+/* attention.py:48-112 given the forward's o32/lse. */
+int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                    int64_t ldv, const float* o32, const float* lse, const void* dout,
+                    int64_t lddo, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
+                    int64_t lddv, const int32_t* seq_lens, int nseq, int Hq, int Hkv,
+                    void* stream);
+/* head.py:42-100 from the normed rows: loss, n_valid and dH [n, D] fp32
+ * (grad wrt the normed rows; the final-norm backward is dsb_op_rmsnorm_bwd). */
+int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t* ids,
+                const int32_t* seq_lens, int nseq, int n, int D, int V, float* dH, float* loss,
+                int* n_valid, void* stream);
+/* grad_A / grad_B of ops.py:143-144: out = Pᵀ·X over n rows (rows of out in
+ * groups of rg written to outs[j / rg]; transpose_out writes out[c, j]). */
+int dsb_op_lora_tn(const float* P, int64_t ldp, const void* X, int64_t ldx, int n, int R, int C,
+                   float* out0, float* out1, float* out2, int rg, int transpose_out,
+                   void* stream);
+/* trainer.py:624-636 + :668 on a flat tensor list: per-group clip then AdamW. */
+int dsb_op_clip_adamw(float* const* w, float* const* g, float* const* m, float* const* v,
+                      const int32_t* numel, const int32_t* group, int ntensors, int ngroups,
+                      float lr, float beta1, float beta2, float eps, float wd, int64_t step,
+                      float max_norm, int do_clip, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSB_H_ */

@@ -1,0 +1,220 @@
+"""Per-kernel parity of libdsb's HIP kernels against the CPU oracle.
+
+Every case calls the C-ABI single-op entry points (deltaserve_amd.ops) on a
+seeded input and compares with the oracle's restatement of the reference op
+(oracle/dsb_oracle.py) on the same bf16-valued inputs in fp32. Tolerances are
+stated per test: fp32 outputs ~1e-4 relative (summation order), bf16 outputs
+a few bf16 ulps (2^-8 relative), attention/head outputs that pass P or dS
+through bf16 MFMA operands 2e-2 max-relative.
+"""
+
+import math
+
+import pytest
+import torch
+
+from harness import O, cosine, max_rel
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _bf(t):
+    return t.to(torch.bfloat16)
+
+
+def _rnd(*shape, seed=0, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * std
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from deltaserve_amd import _lib as L
+    L.load()
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K,K2", [(300, 520, 264, 24), (64, 64, 64, 0), (513, 260, 1024, 16),
+                                      (1, 8, 8, 8)])
+def test_gemm_nt(cfg, M, N, K, K2):
+    from deltaserve_amd import ops
+    A = _bf(_rnd(M, K, seed=1))
+    B = _bf(_rnd(N, K, seed=2))
+    A2 = _bf(_rnd(M, K2, seed=3)) if K2 else None
+    B2 = _bf(_rnd(N, K2, seed=4)) if K2 else None
+    ref = A.float() @ B.float().t()
+    if K2:
+        ref += A2.float() @ B2.float().t()
+    c32 = ops.gemm_nt(A.to(DEV), B.to(DEV), None if A2 is None else A2.to(DEV),
+                      None if B2 is None else B2.to(DEV), out_dtype=torch.float32, cfg=cfg)
+    assert max_rel(c32, ref) < 1e-5
+    R = _bf(_rnd(M, N, seed=5))
+    c16 = ops.gemm_nt(A.to(DEV), B.to(DEV), None if A2 is None else A2.to(DEV),
+                      None if B2 is None else B2.to(DEV), R=R.to(DEV), cfg=cfg)
+    assert max_rel(c16, ref + R.float()) < 8e-3
+    # accumulate into an fp32 output
+    acc = c32.clone()
+    ops.gemm_nt(A.to(DEV), B.to(DEV), out_dtype=torch.float32, out=acc, accumulate=True, cfg=cfg)
+    assert max_rel(acc, ref + A.float() @ B.float().t()) < 1e-5
+
+
+def test_gemm_strided_views():
+    """Row strides and column offsets (the fused qkv / gate_up slices)."""
+    from deltaserve_amd import ops
+    big = _bf(_rnd(200, 96, seed=7)).to(DEV)
+    A = big[:, 32:96]          # ld 96
+    B = _bf(_rnd(40, 64, seed=8)).to(DEV)
+    out = ops.gemm_nt(A, B, out_dtype=torch.float32)
+    assert max_rel(out, A.float().cpu() @ B.float().cpu().t()) < 1e-5
+
+
+def test_rmsnorm_fwd_bwd():
+    from deltaserve_amd import ops
+    x = _bf(_rnd(77, 1024, seed=11) * 3)
+    w = _bf(1 + _rnd(1024, seed=12).abs() * 0.1)
+    g32 = _rnd(77, 1024, seed=13)
+    r = _bf(_rnd(77, 1024, seed=14))
+    eps = 1e-5
+    y = ops.rmsnorm(x.to(DEV), w.to(DEV), eps)
+    assert max_rel(y, O.rmsnorm(x.float(), w.float(), eps)) < 8e-3
+    dx = ops.rmsnorm_backward(x.to(DEV), g32.to(DEV), w.to(DEV), eps, resid=r.to(DEV))
+    ref = O.rmsnorm_backward(x.float(), g32, w.float(), eps) + r.float()
+    assert max_rel(dx, ref) < 8e-3
+    dxb = ops.rmsnorm_backward(x.to(DEV), _bf(g32).to(DEV), w.to(DEV), eps)
+    assert max_rel(dxb, O.rmsnorm_backward(x.float(), _bf(g32).float(), w.float(), eps)) < 8e-3
+
+
+@pytest.mark.parametrize("scaling", [None, {"rope_type": "llama3", "factor": 8.0,
+                                            "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                            "original_max_position_embeddings": 8192.0}])
+def test_rope_table(scaling):
+    from deltaserve_amd import ops
+    pos = torch.tensor(list(range(300)) + list(range(8000, 8192)), dtype=torch.int32)
+    inv = ops.rope_inv_freq(128, 5e5, scaling)
+    assert max_rel(inv, O.rope_inv_freq(128, 5e5, scaling)) < 1e-6
+    c, s = ops.rope_cos_sin(pos.to(DEV), inv.to(DEV))
+    rc, rs = O.rope_cos_sin(pos, 128, 5e5, scaling)
+    assert (c.cpu() - rc).abs().max().item() < 2e-3
+    assert (s.cpu() - rs).abs().max().item() < 2e-3
+
+
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_rope_fwd_bwd(qk_norm):
+    from deltaserve_amd import ops
+    n, Hq, Hkv = 50, 4, 2
+    q, kv = Hq * 128, Hkv * 128
+    pre = _bf(_rnd(n, q + 2 * kv, seed=21))
+    pos = torch.arange(n, dtype=torch.int32)
+    cos, sin = O.rope_cos_sin(pos, 128, 1e6)
+    qn = _bf(1 + _rnd(128, seed=22).abs() * 0.2) if qk_norm else None
+    kn = _bf(1 + _rnd(128, seed=23).abs() * 0.2) if qk_norm else None
+    out = ops.apply_rope(pre.to(DEV), Hq, Hkv, cos.to(DEV), sin.to(DEV),
+                         None if qn is None else qn.to(DEV), None if kn is None else kn.to(DEV), 1e-6)
+    qp = pre.float()[:, :q].view(n, Hq, 128)
+    kp = pre.float()[:, q:q + kv].view(n, Hkv, 128)
+    if qk_norm:
+        qp = O.rmsnorm(qp, qn.float(), 1e-6)
+        kp = O.rmsnorm(kp, kn.float(), 1e-6)
+    ref = torch.cat([O.apply_rope(qp, cos, sin).reshape(n, q), O.apply_rope(kp, cos, sin).reshape(n, kv)], 1)
+    assert max_rel(out, ref) < 1e-2
+    g = _bf(_rnd(n, q + 2 * kv, seed=24))
+    gd = g.to(DEV).clone()
+    ops.rope_backward_(gd, pre.to(DEV), Hq, Hkv, cos.to(DEV), sin.to(DEV),
+                       None if qn is None else qn.to(DEV), None if kn is None else kn.to(DEV), 1e-6)
+    gq = O.rope_backward(g.float()[:, :q].view(n, Hq, 128), cos, sin)
+    gk = O.rope_backward(g.float()[:, q:q + kv].view(n, Hkv, 128), cos, sin)
+    if qk_norm:
+        gq = O.rmsnorm_backward(pre.float()[:, :q].view(n, Hq, 128), gq, qn.float(), 1e-6)
+        gk = O.rmsnorm_backward(pre.float()[:, q:q + kv].view(n, Hkv, 128), gk, kn.float(), 1e-6)
+    assert max_rel(gd[:, :q], gq.reshape(n, q)) < 1e-2
+    assert max_rel(gd[:, q:q + kv], gk.reshape(n, kv)) < 1e-2
+    assert torch.equal(gd[:, q + kv:].cpu(), g[:, q + kv:])  # v columns untouched
+
+
+@pytest.mark.parametrize("seq_lens,Hq,Hkv", [([37, 128, 1, 200, 64], 4, 2), ([300], 8, 2),
+                                             ([5, 129, 256], 2, 1), ([1, 1, 2], 4, 4)])
+def test_attention(seq_lens, Hq, Hkv):
+    from deltaserve_amd import ops
+    n = sum(seq_lens)
+    b_start, *_ = O.pack(seq_lens)
+    qh = _bf(_rnd(n, Hq, 128, seed=31))
+    kh = _bf(_rnd(n, Hkv, 128, seed=32))
+    vh = _bf(_rnd(n, Hkv, 128, seed=33))
+    ctx, o32, lse = ops.attn_forward(qh.reshape(n, -1).to(DEV), kh.reshape(n, -1).to(DEV),
+                                     vh.reshape(n, -1).to(DEV), seq_lens, Hq, Hkv)
+    ref = O.attn_forward(qh.float(), kh.float(), vh.float(), seq_lens, b_start, Hq, Hkv)
+    assert max_rel(o32, ref) < 1e-2
+    assert cosine(o32, ref) > 0.9999
+    assert max_rel(ctx, ref) < 1.5e-2
+    g = _bf(_rnd(n, Hq * 128, seed=34))
+    dq, dk, dv = ops.attn_backward(qh.reshape(n, -1).to(DEV), kh.reshape(n, -1).to(DEV),
+                                   vh.reshape(n, -1).to(DEV), o32, lse, g.to(DEV), seq_lens, Hq, Hkv)
+    rq, rk, rv = O.attn_backward(qh.float(), kh.float(), vh.float(), g.float(), seq_lens, b_start,
+                                 Hq, Hkv)
+    for got, want in ((dq, rq), (dk, rk), (dv, rv)):
+        want = want.reshape(n, -1)
+        assert max_rel(got, want) < 2e-2
+        assert cosine(got, want) > 0.999
+
+
+def test_head():
+    from deltaserve_amd import ops
+    seq_lens = [5, 1, 64, 300]
+    n, D, V = sum(seq_lens), 256, 1000
+    normed = _bf(_rnd(n, D, seed=41))
+    W = _bf(_rnd(V, D, seed=42) * 0.05)
+    ids = torch.randint(0, V, (n,), generator=torch.Generator().manual_seed(43))
+    loss, nv, dH = ops.head_backward(normed.to(DEV), W.to(DEV), ids.to(DEV), seq_lens)
+    _, _, rows, tgt, n_valid = O.pack(seq_lens)
+    logits = normed.float()[rows] @ W.float().t()
+    ref_loss = torch.nn.functional.cross_entropy(logits, ids[tgt], reduction="sum").item() / n_valid
+    p = torch.softmax(logits, -1)
+    p[torch.arange(n_valid), ids[tgt]] -= 1
+    p /= n_valid
+    ref_dH = torch.zeros(n, D)
+    ref_dH[rows] = p @ W.float()
+    assert nv == n_valid
+    assert abs(loss - ref_loss) / ref_loss < 1e-4
+    assert max_rel(dH, ref_dH) < 1e-2
+    assert cosine(dH, ref_dH) > 0.9999
+    last = [sum(seq_lens[:i + 1]) - 1 for i in range(len(seq_lens))]
+    assert dH[last].abs().max().item() == 0.0  # rows that predict nothing
+
+
+def test_lora_tn():
+    from deltaserve_amd import ops
+    n, r, C = 333, 24, 520
+    P = _rnd(n, r, seed=51).to(DEV)
+    X = _bf(_rnd(n, C, seed=52)).to(DEV)
+    ref = P.cpu().t() @ X.float().cpu()
+    outs = [torch.empty(8, C, device=DEV) for _ in range(3)]
+    ops.lora_tn(P, X, 8, False, outs)
+    assert max_rel(torch.cat([o.cpu() for o in outs], 0), ref) < 1e-5
+    outT = torch.empty(C, r, device=DEV)
+    ops.lora_tn(P, X, r, True, [outT])
+    assert max_rel(outT, ref.t()) < 1e-5
+
+
+def test_clip_adamw():
+    from deltaserve_amd import ops
+    shapes = [(8, 64), (96, 8), (8, 4100), (33,)]
+    groups = [0, 0, 1, 2]
+    ws = [_rnd(*s, seed=60 + i) for i, s in enumerate(shapes)]
+    gs = [_rnd(*s, seed=70 + i) * (3.0 if i < 2 else 0.01) for i, s in enumerate(shapes)]
+    ms = [_rnd(*s, seed=80 + i) * 0.1 for i, s in enumerate(shapes)]
+    vs = [_rnd(*s, seed=90 + i).abs() * 0.1 for i, s in enumerate(shapes)]
+    dw, dg, dm, dv = ([t.clone().to(DEV) for t in x] for x in (ws, gs, ms, vs))
+    ops.clip_adamw_(dw, dg, dm, dv, groups, lr=1e-3, step=3, wd=0.01)
+    for gi in range(3):
+        idx = [i for i, g in enumerate(groups) if g == gi]
+        O.clip_([gs[i] for i in idx], 1.0)
+    for i in range(len(ws)):
+        O.adamw_(ws[i], gs[i], ms[i], vs[i], 3, 1e-3, wd=0.01)
+        assert max_rel(dg[i], gs[i]) < 1e-5
+        assert max_rel(dm[i], ms[i]) < 1e-5
+        assert max_rel(dv[i], vs[i]) < 1e-5
+        assert max_rel(dw[i], ws[i]) < 1e-5
