@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256) void lora_tn_partial_kernel(TnArgs a) {
       for (int e = 0; e < TN_CPT; ++e) x[e] = (float)xv[e];
 #pragma unroll
       for (int j = 0; j < TN_RB; ++j) {
-        const float pj = j < nj ? pr[j] : 0.f;
+        const float pv = pr[j < nj ? j : nj - 1];  // clamped: never reads past row t
+        const float pj = j < nj ? pv : 0.f;
 #pragma unroll
         for (int e = 0; e < TN_CPT; ++e) acc[j][e] += pj * x[e];
       }
