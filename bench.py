@@ -1,0 +1,297 @@
+#!/usr/bin/env python
+"""FT backward tokens/s of the MI355X LoRA-SFT backward on a BASELINE config.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+
+One step = one ``process_backward`` cycle (head → 32 reversed decoder layers
+with forward recompute → per-layer clip → AdamW) replayed as one hipGraph,
+over one batch of synthetic packed tokens resident in HBM. Prints ONE JSON
+line. Weights are random-init of the named architecture (N(0, 0.02) linear
+weights, unit norms, LoRA A kaiming-uniform, B N(0, 0.01)); token ids are
+uniform over the vocab; the per-layer activation store holds seeded N(0, 1)
+bf16 rows (the timed kernels do not depend on the values).
+
+`roofline` is for the dominant kernel class (largest total time), from HIP
+event pairs recorded around every kernel inside the timed graph replays.
+`cpu_baseline` times the oracle (fp32 PyTorch on the host cores) on a bounded
+sample: one decoder layer + the LM head over the first sequences of the same
+draw, extrapolated to the full layer count.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "deltaserve-vllm_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+MFMA_CLASSES = ("gemm", "attn_fwd", "attn_dkdv", "attn_dq")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_synthetic(cfg, device, seed=0, timing=True):
+    """The reference's shared dicts (fused bf16 base weights, PEFT fp32 LoRA,
+    meta) for a random-init model of the config, generated on the GPU."""
+    import torch
+    from deltaserve_amd.configs import kaiming_bound
+
+    g = torch.Generator(device=device)
+    L, D, I, V, r = cfg["L"], cfg["D"], cfg["I"], cfg["V"], cfg["r"]
+    q, kv = cfg["Hq"] * 128, cfg["Hkv"] * 128
+    ctr = [seed * 1000003]
+
+    def randn(*shape, std):
+        ctr[0] += 1
+        g.manual_seed(ctr[0])
+        return (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std)
+
+    def w(*shape):
+        return randn(*shape, std=0.02).to(torch.bfloat16)
+
+    ones = lambda n: torch.ones(n, dtype=torch.bfloat16, device=device)  # noqa: E731
+    base = {"model.norm.weight": ones(D)}
+    lm = w(V, D)
+    if cfg.get("tie"):
+        base["model.embed_tokens.weight"] = lm
+    else:
+        base["lm_head.weight"] = lm
+    ft = {}
+    shapes = {"q": (q, D), "k": (kv, D), "v": (kv, D), "o": (D, q), "gate": (I, D),
+              "up": (I, D), "down": (D, I)}
+    mod = {"q": "self_attn", "k": "self_attn", "v": "self_attn", "o": "self_attn",
+           "gate": "mlp", "up": "mlp", "down": "mlp"}
+    for i in range(L):
+        p = f"model.layers.{i}."
+        base[p + "self_attn.qkv_proj.weight"] = w(q + 2 * kv, D)
+        base[p + "self_attn.o_proj.weight"] = w(D, q)
+        base[p + "mlp.gate_up_proj.weight"] = w(2 * I, D)
+        base[p + "mlp.down_proj.weight"] = w(D, I)
+        base[p + "input_layernorm.weight"] = ones(D)
+        base[p + "post_attention_layernorm.weight"] = ones(D)
+        if cfg["family"] == "qwen3":
+            base[p + "self_attn.q_norm.weight"] = ones(128)
+            base[p + "self_attn.k_norm.weight"] = ones(128)
+        for proj, (out, inp) in shapes.items():
+            key = f"base_model.model.model.layers.{i}.{mod[proj]}.{proj}_proj.lora_"
+            b = kaiming_bound(inp)
+            ctr[0] += 1
+            g.manual_seed(ctr[0])
+            ft[key + "A.weight"] = (torch.rand(r, inp, generator=g, device=device) * 2 - 1) * b
+            ft[key + "B.weight"] = randn(out, r, std=0.01)
+    meta = dict(hidden_size=D, num_hidden_layers=L, num_attention_heads=cfg["Hq"],
+                num_key_value_heads=cfg["Hkv"], head_dim=128, intermediate_size=I,
+                vocab_size=V, rope_theta=cfg["theta"], rope_scaling=cfg["rope_scaling"],
+                rms_norm_eps=cfg["eps"], lora_scaling=cfg["alpha"] / r, learning_rate=1e-4,
+                weight_decay=0.0, gamma=1.0,
+                lm_head_key="model.embed_tokens.weight" if cfg.get("tie") else "lm_head.weight",
+                norm_weight_key="model.norm.weight")
+    return base, ft, meta
+
+
+def synthetic_activations(cfg, s_max, n, device, seed=0):
+    import torch
+    g = torch.Generator(device=device)
+    D, L, V = cfg["D"], cfg["L"], cfg["V"]
+    layer_in = []
+    for i in range(L + 1):
+        g.manual_seed(7919 * (seed + 1) + i)
+        t = torch.zeros(s_max + 1, D, dtype=torch.bfloat16, device=device)
+        t[:n] = torch.randn(n, D, generator=g, device=device).to(torch.bfloat16)
+        layer_in.append(t)
+    g.manual_seed(104729 + seed)
+    ids = torch.zeros(s_max, dtype=torch.int64, device=device)
+    ids[:n] = torch.randint(0, V, (n,), generator=g, device=device)
+    return {"layer_in": layer_in[:L], "final_in": layer_in[L], "concat_input_ids": ids}
+
+
+def cpu_baseline(cfg, seq_lens, budget_tokens):
+    """The oracle on the host cores: one full-width decoder layer (recompute +
+    backward) and the LM head over the first sequences of the draw
+    (>= budget_tokens), extrapolated as t_cycle = L·t_layer + t_head."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import dsb_oracle as O
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    sample, tot = [], 0
+    for s in seq_lens:
+        sample.append(s)
+        tot += s
+        if tot >= budget_tokens:
+            break
+    n = sum(sample)
+    meta = dict(family=cfg["family"], num_hidden_layers=1, hidden_size=cfg["D"],
+                num_attention_heads=cfg["Hq"], num_key_value_heads=cfg["Hkv"], head_dim=128,
+                intermediate_size=cfg["I"], vocab_size=cfg["V"], lora_rank=cfg["r"],
+                rope_theta=cfg["theta"], rms_norm_eps=cfg["eps"],
+                lora_scaling=cfg["alpha"] / cfg["r"], rope_scaling=cfg["rope_scaling"])
+    meta["tie_word_embeddings"] = True  # one [V, D] draw serves as the head
+    model = O.make_model(meta, seed=0, bf16_round=False)
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(n, cfg["D"], generator=gen)
+    fin = torch.randn(n, cfg["D"], generator=gen)
+    ids = torch.randint(0, cfg["V"], (n,), generator=gen)
+    b_start, positions, *_ = O.pack(sample)
+    cos, sin = O.rope_cos_sin(positions, 128, cfg["theta"], cfg["rope_scaling"])
+    s, eps, dims = meta["lora_scaling"], meta["rms_norm_eps"], model.dims
+    qk = cfg["family"] == "qwen3"
+    lw = model.layers[0]
+    t0 = time.perf_counter()
+    _, _, g = O.head_backward(fin, model.lm_w, model.norm_w, eps, ids, sample)
+    t_head = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    c = O.layer_forward(x, lw, s, cos, sin, sample, b_start, dims, eps, qk)
+    _, grads = O.layer_backward(g, c, lw, s, cos, sin, sample, b_start, dims, eps, qk)
+    O.clip_([grads[k] for k in sorted(grads)])
+    for key, gk in grads.items():
+        O.adamw_(lw[key], gk, torch.zeros_like(gk), torch.zeros_like(gk), 1, 1e-4)
+    t_layer = time.perf_counter() - t0
+    t_cycle = cfg["L"] * t_layer + t_head
+    return {"value": n / t_cycle, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"{len(sample)} sequences ({n} tokens) of the same draw: 1 of {cfg['L']} "
+                       f"decoder layers + LM head timed once in fp32 (layer {t_layer:.2f}s, head "
+                       f"{t_head:.2f}s), cycle extrapolated as L*layer+head")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=2048)
+    ap.add_argument("--classes-out", default=os.path.join(ROOT, "gpurun_out", "kernel_classes.json"))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU (no collectives, no sharding); "
+              f"--gpus {args.gpus} is not supported. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from deltaserve_amd.bwd_services.registry import get_service
+    from deltaserve_amd.configs import CONFIGS, algorithmic_flops, draw_lengths
+
+    cfg = CONFIGS[args.config]
+    dev = "cuda"
+    torch.cuda.set_device(0)
+    seq_lens = draw_lengths(cfg["nseq"], cfg["lo"], cfg["hi"], cfg["total"], seed=0)
+    n = sum(seq_lens)
+    log(f"[bench] config {args.config} ({cfg['name']}): {len(seq_lens)} sequences, {n} tokens")
+    base, ft, meta = build_synthetic(cfg, dev)
+    meta["max_saved_finetuning_tokens"] = n
+    meta["backward_max_seqs"] = len(seq_lens)
+    svc = get_service(cfg["family"])(0)
+    svc.shared = {"base": base, "ft": ft, "meta": meta}
+    err = svc._on_weights_shared()
+    if err:
+        raise SystemExit(f"build failed: {err}")
+    acts = synthetic_activations(cfg, n, n, dev)
+    torch.cuda.synchronize()
+    log("[bench] state built; warming up")
+    for _ in range(args.warmup):
+        loss, nv = svc.process_backward(acts, seq_lens, n, epoch=0)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done (loss {loss:.4f}, graph={svc.last_cycle_info['graph']}); timing "
+        f"{args.steps} steps")
+    svc.reset_kernel_stats()
+    gpu_ms = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss, nv = svc.process_backward(acts, seq_lens, n, epoch=0)
+        gpu_ms.append(svc.last_cycle_info["gpu_ms"])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_step = dt / args.steps * 1e3
+    fl = algorithmic_flops(cfg, seq_lens)
+    mfma_frac = fl["total"] / (ms_step * 1e-3) / (PEAK_BF16_TFLOPS * 1e12)
+    log(f"[bench] {ms_step:.2f} ms/step wall, {sum(gpu_ms) / len(gpu_ms):.2f} ms/step GPU, "
+        f"{n * args.steps / dt:.0f} tok/s, {100 * mfma_frac:.1f}% of bf16 MFMA peak "
+        f"({fl['total'] / 1e12:.1f} TFLOP/cycle)")
+
+    # Per-kernel-class timing: the same cycle replayed eagerly on the same
+    # stream with a HIP event pair around every kernel.
+    ksteps = max(1, min(args.steps, 3))
+    svc.set_kernel_timing(True)
+    svc.process_backward(acts, seq_lens, n, epoch=0)
+    svc.reset_kernel_stats()
+    for _ in range(ksteps):
+        svc.process_backward(acts, seq_lens, n, epoch=0)
+    svc.set_kernel_timing(False)
+    stats = svc.kernel_stats()
+    steps = ksteps
+    rows = []
+    for c in stats:
+        if c["calls"] == 0:
+            continue
+        mfma = c["name"].startswith(MFMA_CLASSES)
+        sec = c["ms"] * 1e-3
+        rate = (c["flops"] / sec / 1e12) if mfma else (c["bytes"] / sec / 1e9)
+        peak = PEAK_BF16_TFLOPS if mfma else PEAK_HBM_GBS
+        rows.append({"class": c["name"], "calls_per_step": c["calls"] / steps,
+                     "ms_per_step": c["ms"] / steps, "bound": "mfma" if mfma else "hbm",
+                     "achieved": rate, "unit": "TFLOP/s" if mfma else "GB/s", "frac": rate / peak,
+                     "flops_per_launch": c["flops"] / c["calls"],
+                     "bytes_per_launch": c["bytes"] / c["calls"],
+                     "avg_launch_us": c["ms"] / c["calls"] * 1e3})
+    rows.sort(key=lambda r: -r["ms_per_step"])
+    total_k = sum(r["ms_per_step"] for r in rows)
+    log(f"[bench] per-class kernel time (sum {total_k:.2f} ms/step):")
+    for r in rows:
+        log(f"   {r['class']:22s} {r['ms_per_step']:9.3f} ms  x{r['calls_per_step']:6.0f}  "
+            f"{r['achieved']:9.1f} {r['unit']:7s} ({100 * r['frac']:5.1f}% {r['bound']})  "
+            f"avg {r['avg_launch_us']:.1f} us")
+    try:
+        os.makedirs(os.path.dirname(args.classes_out), exist_ok=True)
+        with open(args.classes_out, "w") as f:
+            json.dump({"config": args.config, "steps": args.steps, "classes": rows}, f, indent=1)
+    except OSError:
+        pass
+    dom = rows[0] if rows else None
+    roofline = None
+    if dom:
+        roofline = {"bound": dom["bound"], "achieved": round(dom["achieved"], 2),
+                    "peak": PEAK_BF16_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBS,
+                    "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": None,
+                    "kernel": dom["class"],
+                    "avg_launch_us": round(dom["avg_launch_us"], 2),
+                    "algorithmic_per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma"
+                    else dom["bytes_per_launch"]}
+    svc.close()
+    del svc, base, ft, acts
+    torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU baseline (oracle, fp32, host cores)")
+        cpu = cpu_baseline(cfg, seq_lens, args.cpu_tokens)
+        log(f"[bench] cpu baseline {cpu['value']:.1f} tok/s on {cpu['cores']} cores")
+
+    out = {"metric": "FT backward tokens/sec, Llama-3-8B LoRA r=16 bf16, 1 MI355X; % MFMA peak",
+           "value": round(n * args.steps / dt, 1), "unit": "tokens/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (random-init weights, uniform ids, N(0,1) activation store)",
+           "config": {"workload": f"{args.config}: {cfg['name']} LoRA r={cfg['r']} on 7 "
+                                  f"projections, {len(seq_lens)} packed sequences, {n} tokens",
+                      "global_batch": n, "seq_len": max(seq_lens), "parallelism": "none (1 GPU)"},
+           "mfma_peak_frac": round(mfma_frac, 4),
+           "algorithmic_tflop_per_step": round(fl["total"] / 1e12, 2),
+           "gpu_ms_per_step": round(sum(gpu_ms) / len(gpu_ms), 3),
+           "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -377,13 +377,30 @@ hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t attn_bwd(const AttnArgs& a, hipStream_t s) {
-  if (a.max_tiles <= 0 || a.n <= 0) return hipSuccess;
+hipError_t attn_bwd_prep(const AttnArgs& a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
   const long items = (long)a.n * a.Hq;
   hipLaunchKernelGGL(attn_dsum_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
+  if (a.max_tiles <= 0) return hipSuccess;
   hipLaunchKernelGGL(attn_dkdv_kernel, dim3(a.max_tiles, a.Hkv), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
+  if (a.max_tiles <= 0) return hipSuccess;
   hipLaunchKernelGGL(attn_dq_kernel, dim3(a.max_tiles, a.Hq), dim3(256), 0, s, a);
   return hipGetLastError();
+}
+
+hipError_t attn_bwd(const AttnArgs& a, hipStream_t s) {
+  hipError_t e;
+  if ((e = attn_bwd_prep(a, s)) != hipSuccess) return e;
+  if ((e = attn_bwd_dkdv(a, s)) != hipSuccess) return e;
+  return attn_bwd_dq(a, s);
 }
 
 }  // namespace dsb

@@ -164,6 +164,17 @@ struct StepHdr {  // device-resident per-cycle scalars (64 bytes)
 };
 static_assert(sizeof(StepHdr) == 64, "StepHdr layout");
 
+struct KRec {
+  int cls;
+  double fa, fb, fc, ba, bb, bc;
+  hipEvent_t e0, e1;
+};
+struct KClass {
+  std::string name;
+  long calls = 0;
+  double ms = 0, flops = 0, bytes = 0;
+};
+
 struct LayerState {
   dsb_layer_weights w{};
   bool bound = false;
@@ -229,6 +240,13 @@ struct dsb_handle {
   int nopt_tensors = 0;
   int2* d_layer_chunks = nullptr;
   float *d_opt_partial = nullptr, *d_sq = nullptr;
+  long cast_elems = 0;
+  long opt_elems = 0;
+  // per-kernel-class timing (DSB_FLAG_KTIMING)
+  bool ktiming = false;
+  std::vector<KRec> krec;
+  size_t kpos = 0, kcount = 0;
+  std::vector<KClass> kcls;
   // graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -469,6 +487,8 @@ int finalize(dsb_handle* h) {
     for (long st = 0; st < tot; st += 1024) cast_chunks.push_back(int2{j, (int)st});
   }
   h->ncast_chunks = (int)cast_chunks.size();
+  for (const CastJob& j : jobs) h->cast_elems += (long)j.rows * j.cols;
+  for (const OptTensor& t : opt) h->opt_elems += t.numel;
   h->nopt_chunks = (int)opt_chunks.size();
   h->nopt_tensors = (int)opt.size();
   if (!jobs.empty()) {
@@ -505,13 +525,65 @@ int finalize(dsb_handle* h) {
     }                                                                            \
   } while (0)
 
+// ---- per-kernel-class timing: event pairs recorded on the launch stream
+// around each kernel (captured into the graph as event nodes). Each record
+// carries its algorithmic work as  a·n + b·S + c  (n = live tokens,
+// S = sum_i L_i(L_i + 1)), evaluated with the cycle's actual packing.
+int kclass(dsb_handle* h, const std::string& name) {
+  for (size_t i = 0; i < h->kcls.size(); ++i)
+    if (h->kcls[i].name == name) return (int)i;
+  h->kcls.push_back(KClass{name});
+  return (int)h->kcls.size() - 1;
+}
+
+struct KScope {
+  dsb_handle* h;
+  hipStream_t s;
+  long idx = -1;
+  KScope(dsb_handle* h_, hipStream_t s_, const std::string& name, double fa, double fb,
+         double fc, double ba, double bb, double bc)
+      : h(h_), s(s_) {
+    if (!h->ktiming) return;
+    if (h->kpos == h->krec.size()) {
+      KRec r{};
+      if (hipEventCreate(&r.e0) != hipSuccess || hipEventCreate(&r.e1) != hipSuccess) return;
+      h->krec.push_back(r);
+    }
+    idx = (long)h->kpos++;
+    KRec& r = h->krec[idx];
+    r.cls = kclass(h, name);
+    r.fa = fa; r.fb = fb; r.fc = fc; r.ba = ba; r.bb = bb; r.bc = bc;
+    (void)hipEventRecord(r.e0, s);
+  }
+  ~KScope() {
+    if (idx >= 0) (void)hipEventRecord(h->krec[idx].e1, s);
+  }
+};
+
+const char* cfg_name(int cfg) {
+  return cfg == GEMM_BIG ? "gemm256" : cfg == GEMM_MID ? "gemm128" : "gemm64";
+}
+
+// One NT GEMM launch of the cycle (M = live tokens), timed under
+// "<tile>_<epilogue>". Algorithmic flops 2·n·N·(K1+K2); bytes: A, B once,
+// C once at `ob` bytes per element, plus `xrow` extra bytes per output row.
+template <class Epi>
+int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hipStream_t st,
+         double ob, double xrow, int cfg = -1) {
+  if (cfg < 0) cfg = pick_gemm_cfg(p.M, p.N);
+  const double K = (double)p.K1 + p.K2;
+  KScope ks(h, st, std::string(cfg_name(cfg)) + "_" + epi, 2.0 * p.N * K, 0, 0,
+            2.0 * K + ob * p.N + xrow, 0, 2.0 * p.N * K);
+  LK(launch_gemm(p, e, st, cfg));
+  return 0;
+}
+
 // Z-type skinny product: Zb = bf16(sb·(A·Bᵀ)), Zf = sf·(A·Bᵀ).
 int skinny(dsb_handle* h, const bf16* A, long lda, const bf16* B, int Nout, int K, float* Zf,
            long ldzf, float sf, bf16* Zb, long ldzb, float sb, hipStream_t s) {
   GemmProblem p{A, lda, B, (long)K, nullptr, 0, nullptr, 0, h->N, Nout, K, 0, &h->d_hdr->n};
   EpiLoraZ e{Zf, ldzf, sf, Zb, ldzb, sb, Nout};
-  LK(launch_gemm(p, e, s, GEMM_SKINNY));
-  return 0;
+  return gemm(h, "loraz", p, e, s, 6.0, 0.0, GEMM_SKINNY);
 }
 
 int tn(dsb_handle* h, const float* P, long ldp, const bf16* X, long ldx, int R, int C,
@@ -527,6 +599,7 @@ int tn(dsb_handle* h, const float* P, long ldp, const bf16* X, long ldx, int R, 
   a.nsplit = std::max(ns, 1);
   a.outs[0] = o0; a.outs[1] = o1; a.outs[2] = o2;
   a.rg = rg; a.transpose_out = transpose;
+  KScope ks(h, s, "lora_tn", 2.0 * R * C, 0, 0, 2.0 * C + 4.0 * R, 0, 4.0 * R * C);
   LK(lora_tn(a, s));
   return 0;
 }
@@ -536,27 +609,61 @@ int enqueue(dsb_handle* h, hipStream_t st) {
   const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
   const int* nd = &h->d_hdr->n;
   const float eps = h->d.rms_eps;
-  const bf16* qn = nullptr;
-  (void)qn;
-  LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
-  LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
+  const double Hq = h->Hq;
+  h->kpos = 0;
+  {
+    KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
+    LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
+  }
+  {
+    KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
+    LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
+  }
 
   // ---- head: loss and grad wrt final_in (head.py:42-100)
-  LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
-  LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
   {
-    HeadArgs a{};
-    a.normed = h->normed; a.ldh = D; a.W = h->lm_w; a.WT = h->lm_wT; a.labels = h->labels;
-    a.n = N; a.n_dev = nd; a.D = D; a.V = h->V; a.stats = h->stats; a.ntn = h->ntn;
-    a.tgt_logit = h->tgt_logit; a.lse = h->lse_h; a.loss_row = h->loss_row;
-    a.loss_out = &h->d_hdr->loss; a.inv_nvalid = &h->d_hdr->inv_nvalid;
-    a.dlog = h->dlog; a.vchunk = h->vchunk; a.dH = h->dH;
-    LK(head_fwd_bwd(a, st));
+    KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
+    LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
+  }
+  {
+    KScope ks(h, st, "labels", 0, 0, 0, 16, 0, 0);
+    LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
+  }
+  HeadArgs ha{};
+  ha.normed = h->normed; ha.ldh = D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.labels = h->labels;
+  ha.n = N; ha.n_dev = nd; ha.D = D; ha.V = h->V; ha.stats = h->stats; ha.ntn = h->ntn;
+  ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
+  ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
+  ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH;
+  {
+    // logits recompute in the LSE pass is not algorithmic work (6·M·D·V vs 4·M·D·V)
+    KScope ks(h, st, "gemm256_ce_stats", 0, 0, 0, 2.0 * D + 8.0 * h->ntn, 0, 2.0 * h->V * D);
+    LK(head_stats(ha, st));
+  }
+  {
+    KScope ks(h, st, "ce_reduce", 0, 0, 0, 8.0 * h->ntn + 16, 0, 0);
+    LK(head_reduce(ha, st));
+  }
+  for (int c0 = 0; c0 < h->V; c0 += h->vchunk) {
+    const int Nc = std::min(h->vchunk, h->V - c0);
+    {
+      KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, Nc))) + "_ce_grad", 2.0 * Nc * D, 0,
+                0, 2.0 * D + 2.0 * Nc, 0, 2.0 * Nc * D);
+      LK(head_chunk_grad(ha, c0, st));
+    }
+    {
+      KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, D))) + "_f32", 2.0 * Nc * D, 0, 0,
+                2.0 * Nc + 8.0 * D, 0, 2.0 * Nc * D);
+      LK(head_chunk_dh(ha, c0, st));
+    }
   }
   bf16* g = h->g0;
   bf16* gnext = h->g1;
-  LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, g, D, N, nd, D,
-                 eps, st));
+  {
+    KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
+    LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, g, D, N, nd, D,
+                   eps, st));
+  }
 
   AttnArgs at{};
   at.q = h->qk; at.ldq = q + kv;
@@ -570,6 +677,9 @@ int enqueue(dsb_handle* h, hipStream_t st) {
   at.dv = h->gqkv + q + kv; at.lddv = W3;
   at.tiles = h->d_tiles; at.ntiles_dev = &h->d_hdr->ntiles; at.max_tiles = h->max_tiles;
   at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
+  // one causal attention matmul = Hq·Hd·S flops (S = sum L(L+1), unmasked pairs ×2)
+  const double au = Hq * 128.0;
+  const double arow = 2.0 * (q + 2.0 * kv);
 
   for (int li = h->L - 1; li >= 0; --li) {
     LayerState& ls = h->layers[li];
@@ -584,34 +694,49 @@ int enqueue(dsb_handle* h, hipStream_t st) {
     const bf16* knw = (const bf16*)ls.w.k_norm;
 
     // ================= forward recompute (llama3.py:62-146, qwen3.py:68-130)
-    LK(rmsnorm_fwd(x, ldx, (const bf16*)ls.w.in_ln, h->xn1, D, N, nd, D, eps, st));
+    {
+      KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_fwd(x, ldx, (const bf16*)ls.w.in_ln, h->xn1, D, N, nd, D, eps, st));
+    }
     if (hq) CKR(skinny(h, h->xn1, D, ls.Aqkv, 3 * r, D, h->Pqkv, 3 * r, h->s, h->Zqkv_b, 3 * r, 1.f, st));
     {
       GemmProblem p{h->xn1, (long)D, wqkv, (long)D, hq ? h->Zqkv_b : nullptr, 3L * r,
                     hq ? ls.B2qkv : nullptr, 3L * r, N, W3, D, hq ? 3 * r : 0, nd};
       EpiBF16 e{h->qkv_pre, (long)W3, W3, nullptr, 0};
-      LK(launch_gemm(p, e, st));
+      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
-    LK(rope_fwd(h->qkv_pre, W3, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
-                h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
-    LK(attn_fwd(at, st));
+    {
+      KScope ks(h, st, "rope_fwd", 0, 0, 0, 2.0 * (q + kv) * 2 + 512.0, 0, 0);
+      LK(rope_fwd(h->qkv_pre, W3, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
+                  h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+    }
+    {
+      KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 6.0 * q + 4.0 * Hq, 0, 0);
+      LK(attn_fwd(at, st));
+    }
     if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Po, r, h->s, h->Zo_b, r, 1.f, st));
     {
       GemmProblem p{h->ctx, (long)q, wo, (long)q, ho ? h->Zo_b : nullptr, (long)r,
                     ho ? ls.Bo : nullptr, (long)r, N, D, q, ho ? r : 0, nd};
       EpiBF16 e{h->resid, (long)D, D, x, ldx};
-      LK(launch_gemm(p, e, st));
+      CKR(gemm(h, "bf16", p, e, st, 2.0, 2.0 * D));
     }
-    LK(rmsnorm_fwd(h->resid, D, (const bf16*)ls.w.post_ln, h->xn2, D, N, nd, D, eps, st));
+    {
+      KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_fwd(h->resid, D, (const bf16*)ls.w.post_ln, h->xn2, D, N, nd, D, eps, st));
+    }
     if (hg) CKR(skinny(h, h->xn2, D, ls.Agu, 2 * r, D, h->Pgu, 2 * r, h->s, h->Zgu_b, 2 * r, 1.f, st));
     {
       GemmProblem p{h->xn2, (long)D, wgu, (long)D, hg ? h->Zgu_b : nullptr, 2L * r,
                     hg ? ls.B2gu : nullptr, 2L * r, N, 2 * I, D, hg ? 2 * r : 0, nd};
       EpiBF16 e{h->gu, 2L * I, 2 * I, nullptr, 0};
-      LK(launch_gemm(p, e, st));
+      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
     if (hd) {
-      LK(swiglu_h(h->gu, 2L * I, h->hb, I, N, nd, I, st));
+      {
+        KScope ks(h, st, "swiglu_h", 0, 0, 0, 6.0 * I, 0, 0);
+        LK(swiglu_h(h->gu, 2L * I, h->hb, I, N, nd, I, st));
+      }
       CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Pd, r, h->s, h->Zd_b, r, 1.f, st));
     }
 
@@ -621,7 +746,7 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
                     hd ? ls.AdT : nullptr, (long)r, N, I, D, hd ? r : 0, nd};
       EpiSwiGLUBwd e{h->gu, 2L * I, h->Ggu, 2L * I, I};
-      LK(launch_gemm(p, e, st));
+      CKR(gemm(h, "swiglu", p, e, st, 4.0, 4.0 * I));
     }
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
@@ -637,7 +762,7 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
                     hg ? ls.AguT : nullptr, 2L * r, N, D, 2 * I, hg ? 2 * r : 0, nd};
       EpiF32 e{h->gxn2, (long)D, D, 0};
-      LK(launch_gemm(p, e, st));
+      CKR(gemm(h, "f32", p, e, st, 4.0, 0.0));
     }
     if (hg) {
       const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
@@ -646,23 +771,40 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       CKR(tn(h, h->Pgu, 2 * r, h->Ggu, 2L * I, r, I, tg.gB, nullptr, nullptr, r, 1, st));
       CKR(tn(h, h->Pgu + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1, st));
     }
-    LK(rmsnorm_bwd(h->resid, D, h->gxn2, true, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
-                   nd, D, eps, st));
+    {
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 10.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(h->resid, D, h->gxn2, true, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
+                     nd, D, eps, st));
+    }
     if (ho) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_f, r, 1.f, h->gZo_b, r, 1.f, st));
     {
       GemmProblem p{h->grm, (long)D, ls.oT, (long)D, ho ? h->gZo_b : nullptr, (long)r,
                     ho ? ls.AoT : nullptr, (long)r, N, q, D, ho ? r : 0, nd};
       EpiBF16 e{h->gctx, (long)q, q, nullptr, 0};
-      LK(launch_gemm(p, e, st));
+      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
     if (ho) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
       CKR(tn(h, h->gZo_f, r, h->ctx, q, r, q, t.gA, nullptr, nullptr, r, 0, st));
       CKR(tn(h, h->Po, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, st));
     }
-    LK(attn_bwd(at, st));
-    LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
-                h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+    {
+      KScope ks(h, st, "attn_dsum", 0, 0, 0, 6.0 * q + 4.0 * Hq, 0, 0);
+      LK(attn_bwd_prep(at, st));
+    }
+    {
+      KScope ks(h, st, "attn_dkdv", 0, 4.0 * au, 0, arow + 2.0 * q + 4.0 * kv, 0, 0);
+      LK(attn_bwd_dkdv(at, st));
+    }
+    {
+      KScope ks(h, st, "attn_dq", 0, au, 0, arow + 2.0 * q + 2.0 * q, 0, 0);
+      LK(attn_bwd_dq(at, st));
+    }
+    {
+      KScope ks(h, st, "rope_bwd", 0, 0, 0, 4.0 * (q + kv) + 512.0, 0, 0);
+      LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
+                  h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+    }
     if (hq) {
       CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_f, 3 * r, 1.f, h->gZqkv_b, 3 * r, 1.f, st));
       CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_f + r, 3 * r, 1.f, h->gZqkv_b + r,
@@ -674,7 +816,7 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
                     hq ? ls.AqkvT : nullptr, 3L * r, N, D, W3, hq ? 3 * r : 0, nd};
       EpiF32 e{h->gxn1, (long)D, D, 0};
-      LK(launch_gemm(p, e, st));
+      CKR(gemm(h, "f32", p, e, st, 4.0, 0.0));
     }
     if (hq) {
       const dsb_lora_tensors& tq = ls.lora[DSB_PROJ_Q];
@@ -686,15 +828,22 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       CKR(tn(h, h->Pqkv + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, tv.gB, nullptr, nullptr, r, 1,
              st));
     }
-    LK(rmsnorm_bwd(x, ldx, h->gxn1, true, D, (const bf16*)ls.w.in_ln, h->grm, D, gnext, D, N, nd,
-                   D, eps, st));
+    {
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 10.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(x, ldx, h->gxn1, true, D, (const bf16*)ls.w.in_ln, h->grm, D, gnext, D, N,
+                     nd, D, eps, st));
+    }
     std::swap(g, gnext);
   }
 
   // ---- per-layer clip + AdamW (trainer.py:624-636, :668)
-  LK(clip_adamw(h->d_opt, h->d_opt_chunks, h->nopt_chunks, h->d_layer_chunks, h->L,
-                h->d_opt_partial, h->d_sq, &h->d_hdr->hyper,
-                (h->d.flags & DSB_FLAG_NO_CLIP) ? 0 : 1, st));
+  {
+    KScope ks(h, st, "clip_adamw", 0, 0, 0, 0, 0, (double)h->opt_elems * 28.0);
+    LK(clip_adamw(h->d_opt, h->d_opt_chunks, h->nopt_chunks, h->d_layer_chunks, h->L,
+                  h->d_opt_partial, h->d_sq, &h->d_hdr->hyper,
+                  (h->d.flags & DSB_FLAG_NO_CLIP) ? 0 : 1, st));
+  }
+  h->kcount = h->kpos;
   return 0;
 }
 
@@ -737,6 +886,7 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
     h->vchunk = (int)std::min<long>(vc, ((long)h->V + 255) / 256 * 256);
   }
   h->layers.resize(h->L);
+  h->ktiming = (d->flags & DSB_FLAG_KTIMING) != 0;
   hipError_t e = hipStreamCreateWithFlags(&h->hs, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_in, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_out, hipEventDisableTiming);
@@ -756,6 +906,10 @@ void dsb_destroy(dsb_handle* h) {
   if (h->hs) (void)hipStreamSynchronize(h->hs);
   if (h->gexec) (void)hipGraphExecDestroy(h->gexec);
   if (h->graph) (void)hipGraphDestroy(h->graph);
+  for (KRec& r : h->krec) {
+    (void)hipEventDestroy(r.e0);
+    (void)hipEventDestroy(r.e1);
+  }
   for (void* p : h->allocs) (void)hipFree(p);
   for (auto& ls : h->layers) {
     if (ls.qkvT) (void)hipFree(ls.qkvT);
@@ -866,6 +1020,38 @@ int dsb_reset_optimizer(dsb_handle* h, float weight_decay) {
   return 0;
 }
 
+int dsb_kernel_stats(const dsb_handle* h, int idx, char* name, int name_len, int64_t* calls,
+                     double* total_ms, double* flops, double* bytes) {
+  if (!h) return fail(nullptr, "dsb_kernel_stats: null handle");
+  const int nc = (int)h->kcls.size();
+  if (idx < 0) return nc;
+  if (idx >= nc) return fail(nullptr, "dsb_kernel_stats: index out of range");
+  const KClass& c = h->kcls[idx];
+  if (name && name_len > 0) snprintf(name, name_len, "%s", c.name.c_str());
+  if (calls) *calls = c.calls;
+  if (total_ms) *total_ms = c.ms;
+  if (flops) *flops = c.flops;
+  if (bytes) *bytes = c.bytes;
+  return nc;
+}
+
+int dsb_set_kernel_timing(dsb_handle* h, int on) {
+  if (!h) return fail(nullptr, "dsb_set_kernel_timing: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  h->ktiming = on != 0;
+  return 0;
+}
+
+int dsb_kernel_stats_reset(dsb_handle* h) {
+  if (!h) return fail(nullptr, "dsb_kernel_stats_reset: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  for (KClass& c : h->kcls) {
+    c.calls = 0;
+    c.ms = c.flops = c.bytes = 0;
+  }
+  return 0;
+}
+
 int dsb_pack(const int32_t* seq_lens, int nseq, int n, int32_t* positions, int32_t* pred) {
   if (nseq < 0 || n < 0 || (nseq > 0 && !seq_lens)) return -1;
   return pack_cycle(seq_lens, nseq, n, positions, pred, nullptr);
@@ -916,7 +1102,10 @@ int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, 
   CK(hipMemcpyAsync(h->d_stage, h->h_stage, h->stage_bytes, hipMemcpyHostToDevice, h->hs));
   CK(hipEventRecord(h->ev_t0, h->hs));
   bool used_graph = false;
-  if ((h->d.flags & DSB_FLAG_GRAPH) && !h->graph_failed) {
+  // Kernel timing needs an elapsed time per kernel: HIP reports none for
+  // event pairs recorded inside a captured graph, so timed cycles replay the
+  // same kernel sequence eagerly on the same stream.
+  if ((h->d.flags & DSB_FLAG_GRAPH) && !h->graph_failed && !h->ktiming) {
     if (!h->gexec) {
       hipError_t e = hipStreamBeginCapture(h->hs, hipStreamCaptureModeThreadLocal);
       if (e == hipSuccess) {
@@ -952,6 +1141,20 @@ int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, 
   CK(hipEventSynchronize(h->ev_out));
   StepHdr back;
   memcpy(&back, hs, sizeof(back));
+  if (h->ktiming) {
+    double S = 0;
+    for (int i = 0; i < nseq; ++i) S += (double)seq_lens[i] * (seq_lens[i] + 1);
+    for (size_t i = 0; i < h->kcount && i < h->krec.size(); ++i) {
+      const KRec& rr = h->krec[i];
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, rr.e0, rr.e1) != hipSuccess) continue;
+      KClass& c = h->kcls[rr.cls];
+      c.calls += 1;
+      c.ms += ms;
+      c.flops += rr.fa * n + rr.fb * S + rr.fc;
+      c.bytes += rr.ba * n + rr.bb * S + rr.bc;
+    }
+  }
   if (back.err & 1) return fail(h, "dsb_step: a target token id is outside [0, vocab)");
   if (loss) *loss = back.loss;
   if (n_valid) *n_valid = nv;

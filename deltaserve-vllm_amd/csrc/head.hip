@@ -169,31 +169,49 @@ __global__ __launch_bounds__(1024) void ce_loss_kernel(const float* __restrict__
   if (threadIdx.x == 0) out[0] = s * (*inv_nvalid);
 }
 
+hipError_t head_stats(const HeadArgs& a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  GemmProblem p{a.normed, a.ldh, a.W, (long)a.D, nullptr, 0, nullptr, 0,
+                a.n, a.V, a.D, 0, a.n_dev};
+  EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.V};
+  return launch_gemm_cfg<256, CE_BN, 2, 2>(p, epi, s);
+}
+
+hipError_t head_reduce(const HeadArgs& a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ce_reduce_kernel, dim3((a.n + 3) / 4), dim3(256), 0, s, a.stats, a.ntn,
+                     a.labels, a.tgt_logit, a.lse, a.loss_row, a.n, a.n_dev);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(ce_loss_kernel, dim3(1), dim3(1024), 0, s, a.loss_row, a.n, a.n_dev,
+                     a.inv_nvalid, a.loss_out);
+  return hipGetLastError();
+}
+
+hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s) {
+  const int Nc = min(a.vchunk, a.V - c0);
+  GemmProblem p{a.normed, a.ldh, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
+                a.n, Nc, a.D, 0, a.n_dev};
+  EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Nc};
+  return launch_gemm(p, epi, s);
+}
+
+hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
+  const int Nc = min(a.vchunk, a.V - c0);
+  GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, (long)a.V, nullptr, 0, nullptr, 0,
+                a.n, a.D, Nc, 0, a.n_dev};
+  EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
+  return launch_gemm(q, ef, s);
+}
+
 hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s) {
   hipError_t e;
   if (a.n <= 0) return hipSuccess;
-  {
-    GemmProblem p{a.normed, a.ldh, a.W, (long)a.D, nullptr, 0, nullptr, 0,
-                  a.n, a.V, a.D, 0, a.n_dev};
-    EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.V};
-    if ((e = launch_gemm_cfg<256, CE_BN, 2, 2>(p, epi, s)) != hipSuccess) return e;
-  }
-  hipLaunchKernelGGL(ce_reduce_kernel, dim3((a.n + 3) / 4), dim3(256), 0, s, a.stats, a.ntn,
-                     a.labels, a.tgt_logit, a.lse, a.loss_row, a.n, a.n_dev);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(ce_loss_kernel, dim3(1), dim3(1024), 0, s, a.loss_row, a.n, a.n_dev,
-                     a.inv_nvalid, a.loss_out);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = head_stats(a, s)) != hipSuccess) return e;
+  if ((e = head_reduce(a, s)) != hipSuccess) return e;
   for (int c0 = 0; c0 < a.V; c0 += a.vchunk) {
-    const int Nc = min(a.vchunk, a.V - c0);
-    GemmProblem p{a.normed, a.ldh, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
-                  a.n, Nc, a.D, 0, a.n_dev};
-    EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Nc};
-    if ((e = launch_gemm(p, epi, s)) != hipSuccess) return e;
-    GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, (long)a.V, nullptr, 0, nullptr, 0,
-                  a.n, a.D, Nc, 0, a.n_dev};
-    EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
-    if ((e = launch_gemm(q, ef, s)) != hipSuccess) return e;
+    if ((e = head_chunk_grad(a, c0, s)) != hipSuccess) return e;
+    if ((e = head_chunk_dh(a, c0, s)) != hipSuccess) return e;
   }
   return hipSuccess;
 }

@@ -49,6 +49,9 @@ struct AttnArgs {
 };
 hipError_t attn_fwd(const AttnArgs& a, hipStream_t s);
 hipError_t attn_bwd(const AttnArgs& a, hipStream_t s);
+hipError_t attn_bwd_prep(const AttnArgs& a, hipStream_t s);
+hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s);
+hipError_t attn_bwd_dq(const AttnArgs& a, hipStream_t s);
 
 // ---- lora.hip
 struct CastJob {
@@ -95,6 +98,10 @@ struct HeadArgs {
   float* dH;                      // [n, D] fp32
 };
 hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s);
+hipError_t head_stats(const HeadArgs& a, hipStream_t s);
+hipError_t head_reduce(const HeadArgs& a, hipStream_t s);
+hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s);
+hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s);
 
 // ---- optim.hip
 struct OptTensor {

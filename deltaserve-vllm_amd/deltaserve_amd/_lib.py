@@ -10,8 +10,8 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import (POINTER, Structure, c_char_p, c_float, c_int, c_int32, c_int64,
-                    c_uint32, c_void_p)
+from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32,
+                    c_int64, c_uint32, c_void_p)
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libdsb.so")
@@ -21,7 +21,7 @@ FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
 ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
 PROJ_INDEX = {p: i for i, p in enumerate(PROJS)}
-FLAG_GRAPH, FLAG_NO_CLIP = 1, 2
+FLAG_GRAPH, FLAG_NO_CLIP, FLAG_KTIMING = 1, 2, 4
 
 
 class DsbDesc(Structure):
@@ -72,6 +72,10 @@ _SIGS = {
                          c_void_p, POINTER(c_float), POINTER(c_int),
                          POINTER(DsbCycleInfo)]),
     "dsb_reset_optimizer": (c_int, [c_void_p, c_float]),
+    "dsb_kernel_stats": (c_int, [c_void_p, c_int, c_char_p, c_int, POINTER(c_int64),
+                                 POINTER(c_double), POINTER(c_double), POINTER(c_double)]),
+    "dsb_kernel_stats_reset": (c_int, [c_void_p]),
+    "dsb_set_kernel_timing": (c_int, [c_void_p, c_int]),
     "dsb_pack": (c_int, [POINTER(c_int32), c_int, c_int, POINTER(c_int32),
                          POINTER(c_int32)]),
     "dsb_rope_inv_freq": (c_int, [c_int, c_float, c_int, c_float, c_float, c_float,
@@ -151,3 +155,21 @@ def check(rc: int, handle=None, what: str = "libdsb") -> None:
 def i32_array(values):
     vals = [int(v) for v in values]
     return (c_int32 * max(len(vals), 1))(*vals)
+
+
+def kernel_stats(handle) -> list[dict]:
+    """Per-kernel-class timing table of a handle created with FLAG_KTIMING."""
+    lib = load()
+    n = lib.dsb_kernel_stats(handle, -1, None, 0, None, None, None, None)
+    if n < 0:
+        raise DsbError(last_error(handle))
+    out = []
+    for i in range(n):
+        name = ctypes.create_string_buffer(128)
+        calls, ms, fl, by = c_int64(), c_double(), c_double(), c_double()
+        if lib.dsb_kernel_stats(handle, i, name, 128, ctypes.byref(calls), ctypes.byref(ms),
+                                ctypes.byref(fl), ctypes.byref(by)) < 0:
+            raise DsbError(last_error(handle))
+        out.append({"name": name.value.decode(), "calls": calls.value, "ms": ms.value,
+                    "flops": fl.value, "bytes": by.value})
+    return out

@@ -420,6 +420,21 @@ class LoraSftTrainerService(BackwardService):
                 b_buf[slot, 0, :out_dim, :r].copy_(
                     (pb * self.scaling).clamp(-6.5e4, 6.5e4).to(b_buf.dtype))
 
+    def kernel_stats(self) -> list[dict]:
+        """Per-kernel-class timing (meta ``backward_kernel_timing``): calls,
+        total ms, algorithmic flops and HBM bytes over the cycles run so far."""
+        return L.kernel_stats(self._h) if self._h is not None else []
+
+    def set_kernel_timing(self, on: bool) -> None:
+        """Per-kernel timing on eager replays of the cycle (off: graph replays)."""
+        if self._h is not None:
+            L.check(L.load().dsb_set_kernel_timing(self._h, int(bool(on))), self._h,
+                    "dsb_set_kernel_timing")
+
+    def reset_kernel_stats(self) -> None:
+        if self._h is not None:
+            L.check(L.load().dsb_kernel_stats_reset(self._h), self._h, "dsb_kernel_stats_reset")
+
     def close(self) -> None:
         if self._h is not None:
             L.load().dsb_destroy(self._h)

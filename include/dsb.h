@@ -31,7 +31,7 @@ enum {
   DSB_PROJ_GATE = 4, DSB_PROJ_UP = 5, DSB_PROJ_DOWN = 6, DSB_NUM_PROJ = 7
 };
 /* dsb_desc.flags */
-enum { DSB_FLAG_GRAPH = 1u, DSB_FLAG_NO_CLIP = 2u };
+enum { DSB_FLAG_GRAPH = 1u, DSB_FLAG_NO_CLIP = 2u, DSB_FLAG_KTIMING = 4u };
 
 typedef struct dsb_handle dsb_handle;
 
@@ -118,6 +118,19 @@ int dsb_bind_activations(dsb_handle* h, const dsb_activations* a);
  * for the cycle). Writes the mean loss and the number of predicting rows. */
 int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, int64_t step,
              void* stream, float* loss, int* n_valid, dsb_cycle_info* info);
+
+/* Per-kernel-class timing. While enabled (DSB_FLAG_KTIMING at create, or
+ * dsb_set_kernel_timing), each cycle replays the captured kernel sequence
+ * eagerly on its stream with a HIP event pair around every kernel, and adds
+ * the elapsed time and the launch's algorithmic flops / HBM bytes (evaluated
+ * for the cycle's live n and packing) to its class. dsb_kernel_stats returns
+ * the number of classes (idx < 0 only counts). No counterpart in the
+ * reference (it times whole cycles with CUDA events, base.py:528-534); used
+ * by bench.py for per-class rooflines. */
+int dsb_set_kernel_timing(dsb_handle* h, int on);
+int dsb_kernel_stats(const dsb_handle* h, int idx, char* name, int name_len, int64_t* calls,
+                     double* total_ms, double* flops, double* bytes);
+int dsb_kernel_stats_reset(dsb_handle* h);
 
 /* Zeroes the AdamW moments and sets the weight decay: the fresh optimizer
  * of LoraSftTrainerService.switch_adapter (trainer.py:725-731). The masters

@@ -456,22 +456,3 @@ def make_model(meta: dict, seed: int = 0, projs=PROJS, w_std=0.02, b_std=0.01,
     lm_w = embed if meta.get("tie_word_embeddings") else rnd("lm_head", V, D, std=w_std)
     return Model(meta=dict(meta), layers=layers, lm_w=lm_w, norm_w=norm("norm", D),
                  embed=embed)
-
-
-def draw_lengths(n_seq, lo, hi, total=None, seed=0):
-    """Sequence lengths uniform in [lo, hi] (seeded); with ``total`` set, a
-    deterministic ±1 round-robin adjustment within the bounds makes them sum
-    to ``total`` (the exact-sum rule of the BASELINE configs)."""
-    g = torch.Generator()
-    g.manual_seed(int(seed))
-    lens = torch.randint(lo, hi + 1, (n_seq,), generator=g).tolist()
-    if total is not None:
-        if not (n_seq * lo <= total <= n_seq * hi):
-            raise ValueError("total outside the reachable range")
-        i = 0
-        while sum(lens) != total:
-            d = 1 if sum(lens) < total else -1
-            if lo <= lens[i] + d <= hi:
-                lens[i] += d
-            i = (i + 1) % n_seq
-    return lens
