@@ -210,9 +210,7 @@ struct dsb_handle {
   bf16 *xn1, *qkv_pre, *qk, *ctx, *resid, *xn2, *gu, *hb;
   float *o32, *lse, *dsum;
   bf16 *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
-  float *Pqkv, *Po, *Pgu, *Pd;
   bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
-  float *gZd_f, *gZgu_f, *gZo_f, *gZqkv_f;
   bf16 *g0, *g1, *Ggu, *grm, *gctx, *gqkv;
   float *gxn2, *gxn1;
   bf16 *normed, *dlog;
@@ -335,18 +333,10 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->Zo_b, NN * r));
   CKR(dalloc(h, &h->Zgu_b, NN * 2 * r));
   CKR(dalloc(h, &h->Zd_b, NN * r));
-  CKR(dalloc(h, &h->Pqkv, NN * 3 * r));
-  CKR(dalloc(h, &h->Po, NN * r));
-  CKR(dalloc(h, &h->Pgu, NN * 2 * r));
-  CKR(dalloc(h, &h->Pd, NN * r));
   CKR(dalloc(h, &h->gZd_b, NN * r));
   CKR(dalloc(h, &h->gZgu_b, NN * 2 * r));
   CKR(dalloc(h, &h->gZo_b, NN * r));
   CKR(dalloc(h, &h->gZqkv_b, NN * 3 * r));
-  CKR(dalloc(h, &h->gZd_f, NN * r));
-  CKR(dalloc(h, &h->gZgu_f, NN * 2 * r));
-  CKR(dalloc(h, &h->gZo_f, NN * r));
-  CKR(dalloc(h, &h->gZqkv_f, NN * 3 * r));
   CKR(dalloc(h, &h->g0, NN * D));
   CKR(dalloc(h, &h->g1, NN * D));
   CKR(dalloc(h, &h->Ggu, NN * 2 * I));
@@ -578,28 +568,31 @@ int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hip
   return 0;
 }
 
-// Z-type skinny product: Zb = bf16(sb·(A·Bᵀ)), Zf = sf·(A·Bᵀ).
-int skinny(dsb_handle* h, const bf16* A, long lda, const bf16* B, int Nout, int K, float* Zf,
-           long ldzf, float sf, bf16* Zb, long ldzb, float sb, hipStream_t s) {
-  GemmProblem p{A, lda, B, (long)K, nullptr, 0, nullptr, 0, h->N, Nout, K, 0, &h->d_hdr->n};
-  EpiLoraZ e{Zf, ldzf, sf, Zb, ldzb, sb, Nout};
-  return gemm(h, "loraz", p, e, s, 6.0, 0.0, GEMM_SKINNY);
+// Rank-r product keeping tokens: Z = bf16(X·Bᵀ) (B [R, K]).
+int skinny(dsb_handle* h, const bf16* X, long ldx, const bf16* B, int R, int K, bf16* Z,
+           long ldz, hipStream_t s) {
+  SkinnyArgs a{X, ldx, B, (long)K, R, K, Z, ldz, h->N, &h->d_hdr->n};
+  KScope ks(h, s, "lora_skinny", 2.0 * R * K, 0, 0, 2.0 * K + 2.0 * R, 0, 2.0 * R * K);
+  LK(lora_skinny(a, s));
+  return 0;
 }
 
-int tn(dsb_handle* h, const float* P, long ldp, const bf16* X, long ldx, int R, int C,
-       float* o0, float* o1, float* o2, int rg, int transpose, hipStream_t s) {
+int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, int C,
+       float* o0, float* o1, float* o2, int rg, int transpose, float scale, hipStream_t s) {
   TnArgs a{};
   a.P = P; a.ldp = ldp; a.X = X; a.ldx = ldx; a.R = R; a.C = C;
   a.n = h->N; a.n_dev = &h->d_hdr->n; a.work = h->tn_work;
-  const int cb = (C + 1023) / 1024, rb = (R + 15) / 16;
-  int ns = (512 + cb * rb - 1) / (cb * rb);
+  const int nrb = (R + 31) / 32;
+  const int cb = nrb == 1 ? (C + 1023) / 1024 : (C + 511) / 512;
+  const int zb = (nrb + 1) / 2;
+  int ns = (768 + cb * zb - 1) / (cb * zb);
   ns = std::min(ns, 64);
   ns = std::min<long>(ns, h->tn_work_elems / ((long)R * C));
-  ns = std::min(ns, std::max(1, h->N / 32));
+  ns = std::min(ns, std::max(1, h->N / 64));
   a.nsplit = std::max(ns, 1);
   a.outs[0] = o0; a.outs[1] = o1; a.outs[2] = o2;
-  a.rg = rg; a.transpose_out = transpose;
-  KScope ks(h, s, "lora_tn", 2.0 * R * C, 0, 0, 2.0 * C + 4.0 * R, 0, 4.0 * R * C);
+  a.rg = rg; a.transpose_out = transpose; a.scale = scale;
+  KScope ks(h, s, "lora_tn", 2.0 * R * C, 0, 0, 2.0 * C + 2.0 * R, 0, 4.0 * R * C);
   LK(lora_tn(a, s));
   return 0;
 }
@@ -698,7 +691,7 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
       LK(rmsnorm_fwd(x, ldx, (const bf16*)ls.w.in_ln, h->xn1, D, N, nd, D, eps, st));
     }
-    if (hq) CKR(skinny(h, h->xn1, D, ls.Aqkv, 3 * r, D, h->Pqkv, 3 * r, h->s, h->Zqkv_b, 3 * r, 1.f, st));
+    if (hq) CKR(skinny(h, h->xn1, D, ls.Aqkv, 3 * r, D, h->Zqkv_b, 3 * r, st));
     {
       GemmProblem p{h->xn1, (long)D, wqkv, (long)D, hq ? h->Zqkv_b : nullptr, 3L * r,
                     hq ? ls.B2qkv : nullptr, 3L * r, N, W3, D, hq ? 3 * r : 0, nd};
@@ -714,7 +707,7 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 6.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_fwd(at, st));
     }
-    if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Po, r, h->s, h->Zo_b, r, 1.f, st));
+    if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Zo_b, r, st));
     {
       GemmProblem p{h->ctx, (long)q, wo, (long)q, ho ? h->Zo_b : nullptr, (long)r,
                     ho ? ls.Bo : nullptr, (long)r, N, D, q, ho ? r : 0, nd};
@@ -725,7 +718,7 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
       LK(rmsnorm_fwd(h->resid, D, (const bf16*)ls.w.post_ln, h->xn2, D, N, nd, D, eps, st));
     }
-    if (hg) CKR(skinny(h, h->xn2, D, ls.Agu, 2 * r, D, h->Pgu, 2 * r, h->s, h->Zgu_b, 2 * r, 1.f, st));
+    if (hg) CKR(skinny(h, h->xn2, D, ls.Agu, 2 * r, D, h->Zgu_b, 2 * r, st));
     {
       GemmProblem p{h->xn2, (long)D, wgu, (long)D, hg ? h->Zgu_b : nullptr, 2L * r,
                     hg ? ls.B2gu : nullptr, 2L * r, N, 2 * I, D, hg ? 2 * r : 0, nd};
@@ -737,11 +730,11 @@ int enqueue(dsb_handle* h, hipStream_t st) {
         KScope ks(h, st, "swiglu_h", 0, 0, 0, 6.0 * I, 0, 0);
         LK(swiglu_h(h->gu, 2L * I, h->hb, I, N, nd, I, st));
       }
-      CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Pd, r, h->s, h->Zd_b, r, 1.f, st));
+      CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
     }
 
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
-    if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_f, r, 1.f, h->gZd_b, r, 1.f, st));
+    if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
     {
       GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
                     hd ? ls.AdT : nullptr, (long)r, N, I, D, hd ? r : 0, nd};
@@ -750,13 +743,12 @@ int enqueue(dsb_handle* h, hipStream_t st) {
     }
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
-      CKR(tn(h, h->gZd_f, r, h->hb, I, r, I, t.gA, nullptr, nullptr, r, 0, st));
-      CKR(tn(h, h->Pd, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, st));
+      CKR(tn(h, h->gZd_b, r, h->hb, I, r, I, t.gA, nullptr, nullptr, r, 0, 1.f, st));
+      CKR(tn(h, h->Zd_b, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     if (hg) {
-      CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_f, 2 * r, 1.f, h->gZgu_b, 2 * r, 1.f, st));
-      CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_f + r, 2 * r, 1.f, h->gZgu_b + r,
-                 2 * r, 1.f, st));
+      CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
+      CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
     }
     {
       GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
@@ -767,16 +759,16 @@ int enqueue(dsb_handle* h, hipStream_t st) {
     if (hg) {
       const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
       const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
-      CKR(tn(h, h->gZgu_f, 2 * r, h->xn2, D, 2 * r, D, tg.gA, tu.gA, nullptr, r, 0, st));
-      CKR(tn(h, h->Pgu, 2 * r, h->Ggu, 2L * I, r, I, tg.gB, nullptr, nullptr, r, 1, st));
-      CKR(tn(h, h->Pgu + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1, st));
+      CKR(tn(h, h->gZgu_b, 2 * r, h->xn2, D, 2 * r, D, tg.gA, tu.gA, nullptr, r, 0, 1.f, st));
+      CKR(tn(h, h->Zgu_b, 2 * r, h->Ggu, 2L * I, r, I, tg.gB, nullptr, nullptr, r, 1, h->s, st));
+      CKR(tn(h, h->Zgu_b + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
       KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 10.0 * D, 0, 2.0 * D);
       LK(rmsnorm_bwd(h->resid, D, h->gxn2, true, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
                      nd, D, eps, st));
     }
-    if (ho) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_f, r, 1.f, h->gZo_b, r, 1.f, st));
+    if (ho) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_b, r, st));
     {
       GemmProblem p{h->grm, (long)D, ls.oT, (long)D, ho ? h->gZo_b : nullptr, (long)r,
                     ho ? ls.AoT : nullptr, (long)r, N, q, D, ho ? r : 0, nd};
@@ -785,8 +777,8 @@ int enqueue(dsb_handle* h, hipStream_t st) {
     }
     if (ho) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
-      CKR(tn(h, h->gZo_f, r, h->ctx, q, r, q, t.gA, nullptr, nullptr, r, 0, st));
-      CKR(tn(h, h->Po, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, st));
+      CKR(tn(h, h->gZo_b, r, h->ctx, q, r, q, t.gA, nullptr, nullptr, r, 0, 1.f, st));
+      CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
       KScope ks(h, st, "attn_dsum", 0, 0, 0, 6.0 * q + 4.0 * Hq, 0, 0);
@@ -806,11 +798,9 @@ int enqueue(dsb_handle* h, hipStream_t st) {
                   h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     if (hq) {
-      CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_f, 3 * r, 1.f, h->gZqkv_b, 3 * r, 1.f, st));
-      CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_f + r, 3 * r, 1.f, h->gZqkv_b + r,
-                 3 * r, 1.f, st));
-      CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_f + 2 * r, 3 * r, 1.f,
-                 h->gZqkv_b + 2 * r, 3 * r, 1.f, st));
+      CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
+      CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_b + r, 3 * r, st));
+      CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_b + 2 * r, 3 * r, st));
     }
     {
       GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
@@ -822,11 +812,11 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       const dsb_lora_tensors& tq = ls.lora[DSB_PROJ_Q];
       const dsb_lora_tensors& tk = ls.lora[DSB_PROJ_K];
       const dsb_lora_tensors& tv = ls.lora[DSB_PROJ_V];
-      CKR(tn(h, h->gZqkv_f, 3 * r, h->xn1, D, 3 * r, D, tq.gA, tk.gA, tv.gA, r, 0, st));
-      CKR(tn(h, h->Pqkv, 3 * r, h->gqkv, W3, r, q, tq.gB, nullptr, nullptr, r, 1, st));
-      CKR(tn(h, h->Pqkv + r, 3 * r, h->gqkv + q, W3, r, kv, tk.gB, nullptr, nullptr, r, 1, st));
-      CKR(tn(h, h->Pqkv + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, tv.gB, nullptr, nullptr, r, 1,
-             st));
+      CKR(tn(h, h->gZqkv_b, 3 * r, h->xn1, D, 3 * r, D, tq.gA, tk.gA, tv.gA, r, 0, 1.f, st));
+      CKR(tn(h, h->Zqkv_b, 3 * r, h->gqkv, W3, r, q, tq.gB, nullptr, nullptr, r, 1, h->s, st));
+      CKR(tn(h, h->Zqkv_b + r, 3 * r, h->gqkv + q, W3, r, kv, tk.gB, nullptr, nullptr, r, 1, h->s, st));
+      CKR(tn(h, h->Zqkv_b + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, tv.gB, nullptr, nullptr, r, 1,
+             h->s, st));
     }
     {
       KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 10.0 * D, 0, 2.0 * D);
@@ -1376,21 +1366,31 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   return 0;
 }
 
-int dsb_op_lora_tn(const float* P, int64_t ldp, const void* X, int64_t ldx, int n, int R, int C,
-                   float* out0, float* out1, float* out2, int rg, int transpose_out,
+int dsb_op_lora_tn(const void* P, int64_t ldp, const void* X, int64_t ldx, int n, int R, int C,
+                   float scale, float* out0, float* out1, float* out2, int rg, int transpose_out,
                    void* stream) {
-  if (C % 4 || ldx % 4 || rg <= 0 || (R + rg - 1) / rg > 3)
-    return fail(nullptr, "dsb_op_lora_tn: C and ldx must be multiples of 4, at most 3 groups");
+  if (C % 8 || ldx % 8 || rg <= 0 || (R + rg - 1) / rg > 3)
+    return fail(nullptr, "dsb_op_lora_tn: C and ldx must be multiples of 8, at most 3 groups");
   hipStream_t s = (hipStream_t)stream;
   TmpDev tmp;
   const int ns = 8;
   float* work = tmp.alloc<float>((size_t)ns * R * C);
   if (!work) return fail(nullptr, "dsb_op_lora_tn: hipMalloc failed");
   TnArgs a{};
-  a.P = P; a.ldp = ldp; a.X = (const bf16*)X; a.ldx = ldx; a.R = R; a.C = C; a.n = n;
+  a.P = (const bf16*)P; a.ldp = ldp; a.X = (const bf16*)X; a.ldx = ldx; a.R = R; a.C = C; a.n = n;
   a.n_dev = nullptr; a.work = work; a.nsplit = ns; a.outs[0] = out0; a.outs[1] = out1;
-  a.outs[2] = out2; a.rg = rg; a.transpose_out = transpose_out;
+  a.outs[2] = out2; a.rg = rg; a.transpose_out = transpose_out; a.scale = scale;
   OPCK(lora_tn(a, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, int n, int R, int K,
+                       void* Z, int64_t ldz, void* stream) {
+  if (K % 8 || ldx % 8 || ldb % 8) return fail(nullptr, "dsb_op_lora_skinny: K, ldx, ldb must be multiples of 8");
+  hipStream_t s = (hipStream_t)stream;
+  SkinnyArgs a{(const bf16*)X, ldx, (const bf16*)B, ldb, R, K, (bf16*)Z, ldz, n, nullptr};
+  OPCK(lora_skinny(a, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
 }

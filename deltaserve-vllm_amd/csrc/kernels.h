@@ -64,18 +64,28 @@ struct CastJob {
 };
 hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunks,
                      hipStream_t s);
-// out[j, c] (or out[c, j] when transposed) = sum_t P[t, j] * X[t, c], t < n.
-// Output rows j are split into groups of `rg` rows written to outs[j / rg].
+// Z[t, j] = sum_k X[t, k] · B[j, k] for t < n, j < R; bf16 out.
+struct SkinnyArgs {
+  const bf16* X; long ldx;
+  const bf16* B; long ldb;
+  int R, K;
+  bf16* Z; long ldz;
+  int n; const int* n_dev;
+};
+hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s);
+// out[j, c] (or out[c, j] when transposed) = scale · sum_t P[t, j] * X[t, c],
+// t < n. Output rows j are split into groups of `rg` written to outs[j / rg].
 struct TnArgs {
-  const float* P; long ldp;
+  const bf16* P; long ldp;
   const bf16* X; long ldx;
   int R, C;
   int n; const int* n_dev;
-  float* work;     // [nsplit, R, C]
+  float* work;     // [nsplit, C, R]
   int nsplit;
   float* outs[3];
   int rg;
   int transpose_out;
+  float scale;
 };
 hipError_t lora_tn(const TnArgs& a, hipStream_t s);
 

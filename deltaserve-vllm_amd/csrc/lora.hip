@@ -3,11 +3,19 @@
 //    NT GEMM consumes (A, Aᵀ, s·B into block-diagonal K-concat slabs, (s·B)ᵀ).
 //    The reference casts the masters inline per call (ops.py:103-146:
 //    `A.to(xin.dtype)`, `B.to(xin.dtype)`); here one multi-tensor launch does it.
+//  * lora_skinny: the rank-r products that keep the token dimension,
+//      Z = X·Aᵀ (ops.py:141) and gZ = G·(s·B) (ops.py:142), [n, R] bf16 out.
 //  * lora_tn: the rank-r weight gradients that reduce over tokens,
 //      gA = gZᵀ·X   (ops.py:143, grad_A = grad_Z.t() @ xin)
 //      gB = s·Gᵀ·Z  (ops.py:144, grad_B = scaling * (gy.t() @ Z))
-//    as a token-split fp32 FMA reduction (each thread: 4 columns × 16 ranks)
-//    followed by a fixed-order reduction over splits into the fp32 grads.
+//
+// Both rank-r products are HBM-bound (they stream an [n, width] activation
+// once for a few flops per byte), so neither stages through LDS: lanes load
+// 16-byte row segments straight into MFMA operand registers. For the TN
+// reduction the token dimension is the MFMA K, which the row-major
+// activation does not hold contiguously per column; each lane therefore
+// loads 8 columns × 8 tokens (eight 16-byte loads) and regroups them in
+// registers into 8 operands of 8 tokens each, one per column.
 #include "kernels.h"
 
 namespace dsb {
@@ -35,56 +43,165 @@ hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunk
   return hipGetLastError();
 }
 
-namespace {
-constexpr int TN_CPT = 4;   // columns per thread
-constexpr int TN_RB = 16;   // ranks per block
-}  // namespace
+// ------------------------------------------------------------------ skinny NT
+// Block: 32 tokens, 4 waves splitting K; wave w covers K-slices of 128
+// (lane half h takes k0 + 64h + 8kk, kk < 8). MFMA rows = tokens, cols =
+// ranks, so each lane ends with 16 tokens × 1 rank per 32-rank block.
+template <int RB>
+__global__ __launch_bounds__(256) void lora_skinny_kernel(SkinnyArgs a) {
+  int N = a.n;
+  if (a.n_dev) N = min(N, *a.n_dev);
+  const int t0 = blockIdx.x * 32;
+  if (t0 >= N) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, lh = lane >> 5;
+  const int j0 = blockIdx.y * RB * 32;
+  __shared__ float red[4][RB][32 * 33];
+  f32x16 acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[rb][r] = 0.f;
+  const int t = t0 + li;
+  const bool tok = t < N;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  for (int kb = wave * 128; kb < a.K; kb += 4 * 128) {
+    u32x4 xv[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int k = kb + 64 * lh + 8 * kk;
+      const bool ok = tok && k < a.K;
+      const u32x4 v = ldg128(a.X + (ok ? (long)t * a.ldx + k : 0L));
+      xv[kk] = ok ? v : zero;
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int j = j0 + rb * 32 + li;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int k = kb + 64 * lh + 8 * kk;
+        const bool ok = j < a.R && k < a.K;
+        u32x4 bv = ldg128(a.B + (ok ? (long)j * a.ldb + k : 0L));
+        bv = ok ? bv : zero;
+        acc[rb] = mfma32(__builtin_bit_cast(bf16x8, xv[kk]), __builtin_bit_cast(bf16x8, bv),
+                         acc[rb]);
+      }
+    }
+  }
+  // acc[rb][r]: token t0 + 8(r/4) + 4lh + r%4, rank j0 + rb*32 + li
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      red[wave][rb][(8 * (r >> 2) + 4 * lh + (r & 3)) * 33 + li] = acc[rb][r];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < RB * 32 * 32; idx += 256) {
+    const int rb = idx / 1024, rem = idx % 1024, tt = rem / 32, jj = rem % 32;
+    const int tk = t0 + tt, j = j0 + rb * 32 + jj;
+    if (tk >= N || j >= a.R) continue;
+    const float v = red[0][rb][tt * 33 + jj] + red[1][rb][tt * 33 + jj] +
+                    red[2][rb][tt * 33 + jj] + red[3][rb][tt * 33 + jj];
+    a.Z[(long)tk * a.ldz + j] = (bf16)v;
+  }
+}
 
+hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s) {
+  if (a.R <= 0 || a.n <= 0) return hipSuccess;
+  const int nrb = (a.R + 31) / 32;
+  const dim3 grid((a.n + 31) / 32, (nrb + 1) / 2);
+  if (nrb == 1)
+    hipLaunchKernelGGL(lora_skinny_kernel<1>, dim3(grid.x, 1), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(lora_skinny_kernel<2>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ TN
+// Block: 4 waves × (32 lanes × CPL columns); one token split; RB rank blocks.
+// Per 16-token step, lane (li, lh) loads CPL columns c0 + CPL·li .. of tokens
+// t + 8lh + e (e < 8), and MFMA #cc consumes column c0 + CPL·li + cc across
+// those 8 tokens. Output lane: rank j0 + 32rb + li, columns
+// c0 + CPL·(8(r/4) + 4lh + r%4) + cc. Partials go to work[split][C][R].
+template <int RB, int CPL>
 __global__ __launch_bounds__(256) void lora_tn_partial_kernel(TnArgs a) {
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
-  const int c = (blockIdx.x * 256 + threadIdx.x) * TN_CPT;
-  const int j0 = blockIdx.z * TN_RB;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, lh = lane >> 5;
+  const int c0 = (blockIdx.x * 4 + wave) * 32 * CPL;
+  const int j0 = blockIdx.z * RB * 32;
   const int sp = blockIdx.y;
-  const int per = (N + a.nsplit - 1) / a.nsplit;
-  const int t0 = min(N, sp * per), t1 = min(N, t0 + per);
-  float acc[TN_RB][TN_CPT];
+  int per = (N + a.nsplit - 1) / a.nsplit;
+  per = (per + 15) & ~15;
+  const int ta = min(N, sp * per), tb = min(N, ta + per);
+  f32x16 acc[RB][CPL];
 #pragma unroll
-  for (int j = 0; j < TN_RB; ++j)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int e = 0; e < TN_CPT; ++e) acc[j][e] = 0.f;
-  const int nj = min(TN_RB, a.R - j0);
-  if (c < a.C) {
-#pragma unroll 2
-    for (int t = t0; t < t1; ++t) {
-      const bf16x4 xv = *reinterpret_cast<const bf16x4*>(a.X + (long)t * a.ldx + c);
-      const float* pr = a.P + (long)t * a.ldp + j0;
-      float x[TN_CPT];
+    for (int cc = 0; cc < CPL; ++cc)
 #pragma unroll
-      for (int e = 0; e < TN_CPT; ++e) x[e] = (float)xv[e];
+      for (int r = 0; r < 16; ++r) acc[rb][cc][r] = 0.f;
+  const int cl = c0 + CPL * li;
+  const bool cok = cl < a.C;
+  for (int t = ta; t < tb; t += 16) {
+    bf16 xs[8][CPL];
 #pragma unroll
-      for (int j = 0; j < TN_RB; ++j) {
-        const float pv = pr[j < nj ? j : nj - 1];  // clamped: never reads past row t
-        const float pj = j < nj ? pv : 0.f;
+    for (int e = 0; e < 8; ++e) {
+      const int tt = t + 8 * lh + e;
+      const bool ok = cok && tt < tb;
+      if constexpr (CPL == 8) {
+        u32x4 v = ldg128(a.X + (ok ? (long)tt * a.ldx + cl : 0L));
+        if (!ok) v = u32x4{0u, 0u, 0u, 0u};
+        const bf16x8 b = __builtin_bit_cast(bf16x8, v);
 #pragma unroll
-        for (int e = 0; e < TN_CPT; ++e) acc[j][e] += pj * x[e];
+        for (int cc = 0; cc < 8; ++cc) xs[e][cc] = b[cc];
+      } else {
+        u32x2 v = *reinterpret_cast<const u32x2*>(a.X + (ok ? (long)tt * a.ldx + cl : 0L));
+        if (!ok) v = u32x2{0u, 0u};
+        const bf16x4 b = __builtin_bit_cast(bf16x4, v);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) xs[e][cc] = b[cc];
       }
     }
 #pragma unroll
-    for (int j = 0; j < TN_RB; ++j) {
-      if (j >= nj) break;
-      float* w = a.work + ((long)sp * a.R + j0 + j) * a.C + c;
-      *reinterpret_cast<f32x4*>(w) = f32x4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+    for (int rb = 0; rb < RB; ++rb) {
+      const int j = j0 + rb * 32 + li;
+      bf16x8 pb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int tt = t + 8 * lh + e;
+        const bool ok = j < a.R && tt < tb;
+        const bf16 v = a.P[ok ? (long)tt * a.ldp + j : 0L];
+        pb[e] = ok ? v : (bf16)0.f;
+      }
+#pragma unroll
+      for (int cc = 0; cc < CPL; ++cc) {
+        bf16x8 av;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) av[e] = xs[e][cc];
+        acc[rb][cc] = mfma32(av, pb, acc[rb][cc]);
+      }
     }
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int j = j0 + rb * 32 + li;
+    if (j >= a.R) continue;
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int col = c0 + CPL * (8 * (r >> 2) + 4 * lh + (r & 3)) + cc;
+        if (col < a.C) a.work[((long)sp * a.C + col) * a.R + j] = acc[rb][cc][r];
+      }
   }
 }
 
 __global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnArgs a) {
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long)a.R * a.C) return;
-  const int j = (int)(idx / a.C), c = (int)(idx % a.C);
+  const int c = (int)(idx / a.R), j = (int)(idx % a.R);
   float s = 0.f;
-  for (int sp = 0; sp < a.nsplit; ++sp) s += a.work[((long)sp * a.R + j) * a.C + c];
+  for (int sp = 0; sp < a.nsplit; ++sp) s += a.work[((long)sp * a.C + c) * a.R + j];
+  s *= a.scale;
   const int grp = j / a.rg, jj = j % a.rg;
   float* o = a.outs[grp];
   if (a.transpose_out)
@@ -95,11 +212,17 @@ __global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnArgs a) {
 
 hipError_t lora_tn(const TnArgs& a, hipStream_t s) {
   if (a.R <= 0 || a.C <= 0) return hipSuccess;
-  const int cb = (a.C + 256 * TN_CPT - 1) / (256 * TN_CPT);
-  const int rb = (a.R + TN_RB - 1) / TN_RB;
-  hipLaunchKernelGGL(lora_tn_partial_kernel, dim3(cb, a.nsplit, rb), dim3(256), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  const int nrb = (a.R + 31) / 32;
+  hipError_t e;
+  if (nrb == 1) {
+    const int cb = (a.C + 4 * 256 - 1) / (4 * 256);
+    hipLaunchKernelGGL((lora_tn_partial_kernel<1, 8>), dim3(cb, a.nsplit, 1), dim3(256), 0, s, a);
+  } else {
+    const int cb = (a.C + 4 * 128 - 1) / (4 * 128);
+    hipLaunchKernelGGL((lora_tn_partial_kernel<2, 4>), dim3(cb, a.nsplit, (nrb + 1) / 2),
+                       dim3(256), 0, s, a);
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return e;
   const long tot = (long)a.R * a.C;
   hipLaunchKernelGGL(lora_tn_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
                      s, a);

@@ -188,16 +188,28 @@ def head_backward(normed, lm_w, ids, seq_lens):
 
 # ---------------------------------------------------------------- LoRA grads / optimizer
 
-def lora_tn(P, X, rg, transpose_out, outs):
-    """ops.py:143-144: Pᵀ·X over rows (grad_A, or grad_B when transpose_out)."""
+def lora_tn(P, X, rg, transpose_out, outs, scale=1.0):
+    """ops.py:143-144: scale · Pᵀ·X over rows (grad_A, or grad_B when
+    transpose_out); P bf16 [n, R]."""
     _dev(P, X, *outs)
     n, R = P.shape
     C = X.shape[1]
     o = list(outs) + [None] * (3 - len(outs))
-    L.check(L.load().dsb_op_lora_tn(_p(P), _ld(P), _p(X), _ld(X), n, R, C, _p(o[0]), _p(o[1]),
-                                    _p(o[2]), rg, int(transpose_out), _stream()),
+    L.check(L.load().dsb_op_lora_tn(_p(P), _ld(P), _p(X), _ld(X), n, R, C, float(scale), _p(o[0]),
+                                    _p(o[1]), _p(o[2]), rg, int(transpose_out), _stream()),
             what="dsb_op_lora_tn")
     return outs
+
+
+def lora_skinny(X, B):
+    """ops.py:141-142: bf16(X·Bᵀ) for a rank-r factor B [R, K]."""
+    _dev(X, B)
+    n, K = X.shape
+    R = B.shape[0]
+    Z = torch.empty(n, R, dtype=BF16, device=X.device)
+    L.check(L.load().dsb_op_lora_skinny(_p(X), _ld(X), _p(B), _ld(B), n, R, K, _p(Z), _ld(Z),
+                                        _stream()), what="dsb_op_lora_skinny")
+    return Z
 
 
 def clip_adamw_(ws, gs, ms, vs, groups, lr, step, beta1=0.9, beta2=0.999, eps=1e-8, wd=0.0,

@@ -185,11 +185,15 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
 int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t* ids,
                 const int32_t* seq_lens, int nseq, int n, int D, int V, float* dH, float* loss,
                 int* n_valid, void* stream);
-/* grad_A / grad_B of ops.py:143-144: out = Pᵀ·X over n rows (rows of out in
- * groups of rg written to outs[j / rg]; transpose_out writes out[c, j]). */
-int dsb_op_lora_tn(const float* P, int64_t ldp, const void* X, int64_t ldx, int n, int R, int C,
-                   float* out0, float* out1, float* out2, int rg, int transpose_out,
+/* grad_A / grad_B of ops.py:143-144: out = scale · Pᵀ·X over n rows, P bf16
+ * [n, R] (rows of out in groups of rg written to outs[j / rg]; transpose_out
+ * writes out[c, j]). */
+int dsb_op_lora_tn(const void* P, int64_t ldp, const void* X, int64_t ldx, int n, int R, int C,
+                   float scale, float* out0, float* out1, float* out2, int rg, int transpose_out,
                    void* stream);
+/* Z / grad_Z of ops.py:141-142: Z = bf16(X·Bᵀ), X [n, K], B [R, K]. */
+int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, int n, int R, int K,
+                       void* Z, int64_t ldz, void* stream);
 /* trainer.py:624-636 + :668 on a flat tensor list: per-group clip then AdamW. */
 int dsb_op_clip_adamw(float* const* w, float* const* g, float* const* m, float* const* v,
                       const int32_t* numel, const int32_t* group, int ntensors, int ngroups,

@@ -185,18 +185,30 @@ def test_head():
     assert dH[last].abs().max().item() == 0.0  # rows that predict nothing
 
 
-def test_lora_tn():
+@pytest.mark.parametrize("n,R,C", [(333, 24, 520), (8192, 16, 4096), (1000, 48, 1024), (17, 96, 256)])
+def test_lora_tn(n, R, C):
     from deltaserve_amd import ops
-    n, r, C = 333, 24, 520
-    P = _rnd(n, r, seed=51).to(DEV)
+    P = _bf(_rnd(n, R, seed=51)).to(DEV)
     X = _bf(_rnd(n, C, seed=52)).to(DEV)
-    ref = P.cpu().t() @ X.float().cpu()
-    outs = [torch.empty(8, C, device=DEV) for _ in range(3)]
-    ops.lora_tn(P, X, 8, False, outs)
+    ref = P.float().cpu().t() @ X.float().cpu()
+    rg = R // 3 if R % 3 == 0 else R
+    ng = R // rg
+    outs = [torch.empty(rg, C, device=DEV) for _ in range(ng)]
+    ops.lora_tn(P, X, rg, False, outs)
     assert max_rel(torch.cat([o.cpu() for o in outs], 0), ref) < 1e-5
-    outT = torch.empty(C, r, device=DEV)
-    ops.lora_tn(P, X, r, True, [outT])
-    assert max_rel(outT, ref.t()) < 1e-5
+    outT = torch.empty(C, R, device=DEV)
+    ops.lora_tn(P, X, R, True, [outT], scale=2.0)
+    assert max_rel(outT, 2.0 * ref.t()) < 1e-5
+
+
+@pytest.mark.parametrize("n,R,K", [(333, 24, 520), (8192, 48, 4096), (100, 16, 14336), (5, 64, 64)])
+def test_lora_skinny(n, R, K):
+    from deltaserve_amd import ops
+    X = _bf(_rnd(n, K, seed=53)).to(DEV)
+    B = _bf(_rnd(R, K, seed=54)).to(DEV)
+    Z = ops.lora_skinny(X, B)
+    ref = X.float().cpu() @ B.float().cpu().t()
+    assert max_rel(Z, ref) < 8e-3
 
 
 def test_clip_adamw():
