@@ -9,9 +9,11 @@
 //
 // Tiling: BM×BN block tile, BK = 64, WM×WN waves, each wave owns a
 // (BM/WM)×(BN/WN) sub-tile of 32×32 MFMA fragments. Global→LDS staging is
-// double-buffered through registers (one barrier per K step). LDS rows are
-// 128 B with a 16-byte-chunk XOR swizzle (chunk ^ row%8) so the per-lane
-// 16-byte fragment reads of 32 consecutive rows spread over all banks.
+// double-buffered through registers (one barrier per K step) with buffer
+// loads: rows past M/N fall outside the descriptor and read as zero, and the
+// first use of a loaded value is the LDS store after the MFMAs of the current
+// step, so the loads overlap the math. LDS rows are 128 B with a 16-byte-chunk
+// XOR swizzle so fragment reads of 16 consecutive rows hit distinct banks.
 // Block ids are remapped so each XCD (round-robin dispatch over 8 XCDs) gets a
 // contiguous run of tiles, grouped 8 deep along M for L2 reuse.
 #pragma once
@@ -70,8 +72,8 @@ DSB_DEV void for_each_quad(const f32x16 (&acc)[FM][FN], int mw, int nw, int M,
 }
 
 template <int BM, int BN, int WM, int WN, class Epi>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmProblem p,
-                                                               Epi epi) {
+__global__ __launch_bounds__(WM* WN * 64)
+__attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_kernel(GemmProblem p, Epi epi) {
   constexpr int BK = 64, CH = 8;
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -96,47 +98,59 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmProblem p,
   const int nk2 = p.K2 > 0 ? (p.K2 + BK - 1) / BK : 0;
   const int nk = nk1 + nk2;
 
-  u32x4 ra[LA], rb[LB];
-  const u32x4 zero = {0u, 0u, 0u, 0u};
+  // Buffer resources over this tile's rows of each operand: rows past M (N)
+  // fall outside num_records and load as zeros. Thread t loads 16-byte chunk
+  // ch = t % 8 of rows t/8 + i·(NT/8); the row step goes in the scalar offset.
+  constexpr int RSTEP = NT / CH;
+  const int ch = tid % CH, r0 = tid / CH;
+  const int rowsA = min(M - m0, BM), rowsB = min(p.N - n0, BN);
+  auto rsrc = [](const bf16* base, long ld, int rows, int K) {
+    const long bytes = rows > 0 ? (((long)(rows - 1) * ld + K) * 2) : 0;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t ra1 = rsrc(p.A + (long)m0 * p.lda, p.lda, rowsA, p.K1);
+  const __amdgpu_buffer_rsrc_t rb1 = rsrc(p.B + (long)n0 * p.ldb, p.ldb, rowsB, p.K1);
+  const __amdgpu_buffer_rsrc_t ra2 = rsrc(p.A2 ? p.A2 + (long)m0 * p.lda2 : p.A, p.lda2, nk2 ? rowsA : 0, p.K2);
+  const __amdgpu_buffer_rsrc_t rb2 = rsrc(p.B2 ? p.B2 + (long)n0 * p.ldb2 : p.B, p.ldb2, nk2 ? rowsB : 0, p.K2);
+  const int voffA1 = (int)(r0 * p.lda * 2 + ch * 16), voffB1 = (int)(r0 * p.ldb * 2 + ch * 16);
+  const int voffA2 = (int)(r0 * p.lda2 * 2 + ch * 16), voffB2 = (int)(r0 * p.ldb2 * 2 + ch * 16);
 
+  u32x4 ra[LA], rb[LB];
+  bool kok = true;  // this thread's chunk lies below K (only the last K step can fail)
   auto gload = [&](int kt) {
-    const bf16* A;
-    const bf16* B;
-    long lda, ldb;
-    int K, k0;
     if (kt < nk1) {
-      A = p.A; B = p.B; lda = p.lda; ldb = p.ldb; K = p.K1; k0 = kt * BK;
+      const int k0 = kt * BK;
+      kok = k0 + ch * 8 < p.K1;
+#pragma unroll
+      for (int i = 0; i < LA; ++i)
+        ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra1, voffA1, (int)(i * RSTEP * p.lda * 2 + k0 * 2), 0);
+#pragma unroll
+      for (int i = 0; i < LB; ++i)
+        rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb1, voffB1, (int)(i * RSTEP * p.ldb * 2 + k0 * 2), 0);
     } else {
-      A = p.A2; B = p.B2; lda = p.lda2; ldb = p.ldb2; K = p.K2; k0 = (kt - nk1) * BK;
-    }
+      const int k0 = (kt - nk1) * BK;
+      kok = k0 + ch * 8 < p.K2;
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int c = tid + i * NT, row = c / CH, k = k0 + (c % CH) * 8;
-      const bool ok = (m0 + row < M) && (k < K);
-      const u32x4 v = ldg128(A + (ok ? (long)(m0 + row) * lda + k : 0L));
-      ra[i] = ok ? v : zero;
-    }
+      for (int i = 0; i < LA; ++i)
+        ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra2, voffA2, (int)(i * RSTEP * p.lda2 * 2 + k0 * 2), 0);
 #pragma unroll
-    for (int i = 0; i < LB; ++i) {
-      const int c = tid + i * NT, row = c / CH, k = k0 + (c % CH) * 8;
-      const bool ok = (n0 + row < p.N) && (k < K);
-      const u32x4 v = ldg128(B + (ok ? (long)(n0 + row) * ldb + k : 0L));
-      rb[i] = ok ? v : zero;
+      for (int i = 0; i < LB; ++i)
+        rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb2, voffB2, (int)(i * RSTEP * p.ldb2 * 2 + k0 * 2), 0);
     }
   };
+  // LDS: [row][8 × 16-byte chunks], chunk slot = ch ^ ((row >> 1) & 7) so that
+  // 16 consecutive rows read at one logical chunk hit 16 distinct bank groups.
+  auto slot = [](int row, int c) { return row * BK + ((c ^ ((row >> 1) & 7)) << 3); };
   auto sstore = [&](int buf) {
     bf16* sA = smem + buf * (SA + SB);
     bf16* sB = sA + SA;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int c = tid + i * NT, row = c / CH, ch = c % CH;
-      *reinterpret_cast<u32x4*>(sA + row * BK + ((ch ^ (row & 7)) << 3)) = ra[i];
-    }
+    for (int i = 0; i < LA; ++i)
+      *reinterpret_cast<u32x4*>(sA + slot(r0 + i * RSTEP, ch)) = kok ? ra[i] : zero;
 #pragma unroll
-    for (int i = 0; i < LB; ++i) {
-      const int c = tid + i * NT, row = c / CH, ch = c % CH;
-      *reinterpret_cast<u32x4*>(sB + row * BK + ((ch ^ (row & 7)) << 3)) = rb[i];
-    }
+    for (int i = 0; i < LB; ++i)
+      *reinterpret_cast<u32x4*>(sB + slot(r0 + i * RSTEP, ch)) = kok ? rb[i] : zero;
   };
 
   f32x16 acc[FM][FN];
@@ -148,27 +162,32 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmProblem p,
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int lr = lane & 31, lh = lane >> 5;
+  // Fragments double-buffered across the four 16-deep K slices of a step: the
+  // LDS reads of slice kk+1 are issued before the MFMAs of slice kk.
+  bf16x8 af[2][FM], bfr[2][FN];
+  auto load_frags = [&](const bf16* sA, const bf16* sB, int kk, int b) {
+    const int kc = kk * 2 + lh;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+      af[b][fm] = *reinterpret_cast<const bf16x8*>(sA + slot(wm * TM + fm * 32 + lr, kc));
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+      bfr[b][fn] = *reinterpret_cast<const bf16x8*>(sB + slot(wn * TN + fn * 32 + lr, kc));
+  };
   auto compute = [&](int buf) {
     const bf16* sA = smem + buf * (SA + SB);
     const bf16* sB = sA + SA;
+    load_frags(sA, sB, 0, 0);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      const int ch = kk * 2 + lh;
-      bf16x8 af[FM], bfr[FN];
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
-        const int row = wm * TM + fm * 32 + lr;
-        af[fm] = *reinterpret_cast<const bf16x8*>(sA + row * BK + ((ch ^ (row & 7)) << 3));
-      }
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int row = wn * TN + fn * 32 + lr;
-        bfr[fn] = *reinterpret_cast<const bf16x8*>(sB + row * BK + ((ch ^ (row & 7)) << 3));
-      }
+      if (kk + 1 < BK / 16) load_frags(sA, sB, kk + 1, (kk + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = mfma32(bfr[fn], af[fm], acc[fm][fn]);
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fm][fn] = mfma32(bfr[kk & 1][fn], af[kk & 1][fm], acc[fm][fn]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
