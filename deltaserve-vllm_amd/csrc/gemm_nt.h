@@ -73,7 +73,7 @@ DSB_DEV void for_each_quad(const f32x16 (&acc)[FM][FN], int mw, int nw, int M,
 
 template <int BM, int BN, int WM, int WN, class Epi>
 __global__ __launch_bounds__(WM* WN * 64)
-__attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_kernel(GemmProblem p, Epi epi) {
+__attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel(GemmProblem p, Epi epi) {
   constexpr int BK = 64, CH = 8;
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;

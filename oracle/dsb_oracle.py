@@ -292,7 +292,7 @@ def head_backward(final_in, lm_w, norm_w, eps, ids, seq_lens):
     p = torch.softmax(logits, dim=-1)
     p[torch.arange(n_valid), t] -= 1.0
     p /= n_valid
-    gn = torch.zeros(n, final_in.shape[1])
+    gn = torch.zeros(n, final_in.shape[1], dtype=final_in.dtype)
     gn[rows] = p @ lm_w
     return float(loss.item() / n_valid), n_valid, rmsnorm_backward(final_in, gn, norm_w, eps)
 
