@@ -15,7 +15,30 @@ import time
 
 import torch
 
-from deltaserve_amd import dprint
+from deltaserve_amd import dprint, mark_backward_process
+
+
+def service_main(conn, mps_percentage: int, device_index: int, service_name: str,
+                 gpu_grant=None) -> None:
+    """Child-process entry point (base.py:48-70): select the service by
+    architecture string, bind the GPU-yield event and run the pipe loop.
+    ``mps_percentage`` is accepted for signature compatibility; the MI355X
+    child does not partition CUs."""
+    from deltaserve_amd.bwd_services.registry import get_service
+
+    mark_backward_process()
+    if torch.cuda.is_available():
+        torch.cuda.set_device(device_index)
+    svc = get_service(service_name)(device_index)
+    svc._gpu_grant = gpu_grant
+    try:
+        svc.run(conn)
+    except KeyboardInterrupt:
+        dprint("[backward] child interrupted by shutdown; exiting")
+    finally:
+        close = getattr(svc, "close", None)
+        if close is not None:
+            close()
 
 
 class BackwardService:

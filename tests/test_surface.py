@@ -249,3 +249,23 @@ def test_c3_algorithmic_flops():
     assert f["dense"] == 32 * 8192 * (4 * 4096 * 6144 + 4 * 4096 * 4096 + 10 * 4096 * 14336)
     assert f["head"] == 4 * (8192 - 32) * 4096 * 128256
     assert 218e12 < f["total"] < 221e12
+
+
+def test_service_main_runs_the_protocol_child():
+    """The spawn entry (base.py:48-70) on the protocol-only service, over a
+    real multiprocessing pipe in this process."""
+    import multiprocessing as mp
+    import threading
+
+    from deltaserve_amd.bwd_services import service_main
+
+    parent, child = mp.Pipe()
+    t = threading.Thread(target=service_main, args=(child, 100, 0, "ipc", None))
+    t.start()
+    assert parent.recv()["event"] == "ready"
+    parent.send({"cmd": "ping"})
+    assert parent.recv()["event"] == "pong"
+    parent.send({"cmd": "shutdown"})
+    assert parent.recv()["event"] == "shutdown_ack"
+    t.join(10)
+    assert not t.is_alive()
