@@ -199,7 +199,8 @@ struct dsb_handle {
   std::vector<LayerState> layers;
   const bf16* lm_w = nullptr;
   const bf16* norm_w = nullptr;
-  bf16* lm_wT = nullptr;
+  bf16* lm_wT = nullptr;  // [D, ldwt], columns V..ldwt zero
+  long ldwt = 0;
   std::vector<const bf16*> layer_in;
   const bf16* final_in = nullptr;
   const int64_t* ids = nullptr;
@@ -623,7 +624,8 @@ int enqueue(dsb_handle* h, hipStream_t st) {
     LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
   }
   HeadArgs ha{};
-  ha.normed = h->normed; ha.ldh = D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.labels = h->labels;
+  ha.normed = h->normed; ha.ldh = D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.ldwt = h->ldwt;
+  ha.labels = h->labels;
   ha.n = N; ha.n_dev = nd; ha.D = D; ha.V = h->V; ha.stats = h->stats; ha.ntn = h->ntn;
   ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
   ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
@@ -856,8 +858,8 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
     return fail(nullptr, "dsb_create: n_heads must be a positive multiple of n_kv_heads");
   if (d->lora_rank <= 0 || d->lora_rank % 8 || d->lora_rank > 64)
     return fail(nullptr, "dsb_create: lora_rank must be a multiple of 8 in [8, 64]");
-  if (d->hidden % 8 || d->hidden > 8192 || d->intermediate % 8 || d->vocab % 8)
-    return fail(nullptr, "dsb_create: hidden (<= 8192), intermediate and vocab must be multiples of 8");
+  if (d->hidden % 8 || d->hidden > 8192 || d->intermediate % 8 || d->vocab <= 0)
+    return fail(nullptr, "dsb_create: hidden (<= 8192) and intermediate must be multiples of 8, vocab positive");
   if (d->s_max <= 0 || d->max_seqs <= 0 || d->n_layers <= 0)
     return fail(nullptr, "dsb_create: s_max, max_seqs, n_layers must be positive");
   if (d->family != DSB_FAMILY_LLAMA3 && d->family != DSB_FAMILY_QWEN3)
@@ -950,8 +952,12 @@ int dsb_bind_head(dsb_handle* h, const void* lm_head, const void* final_norm) {
   if (h->finalized) return fail(h, "dsb_bind_head: state already finalized");
   h->lm_w = (const bf16*)lm_head;
   h->norm_w = (const bf16*)final_norm;
-  if (!h->lm_wT) CK(hipMalloc(&h->lm_wT, (size_t)h->V * h->D * 2));
-  CK(transpose_bf16(h->lm_w, h->D, h->lm_wT, h->V, h->V, h->D, h->hs));
+  h->ldwt = ((long)h->V + 7) / 8 * 8;
+  if (!h->lm_wT) {
+    CK(hipMalloc(&h->lm_wT, (size_t)h->ldwt * h->D * 2));
+    CK(hipMemsetAsync(h->lm_wT, 0, (size_t)h->ldwt * h->D * 2, h->hs));
+  }
+  CK(transpose_bf16(h->lm_w, h->D, h->lm_wT, h->ldwt, h->V, h->D, h->hs));
   CK(hipStreamSynchronize(h->hs));
   return 0;
 }
@@ -1324,7 +1330,7 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
 int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t* ids,
                 const int32_t* seq_lens, int nseq, int n, int D, int V, float* dH, float* loss,
                 int* n_valid, void* stream) {
-  if (D % 8 || V % 8 || ldh % 8) return fail(nullptr, "dsb_op_head: D, V, ldh must be multiples of 8");
+  if (D % 8 || V <= 0 || ldh % 8) return fail(nullptr, "dsb_op_head: D and ldh must be multiples of 8, V positive");
   hipStream_t s = (hipStream_t)stream;
   std::vector<int32_t> pred(n > 0 ? n : 1);
   const int nv = pack_cycle(seq_lens, nseq, n, nullptr, pred.data(), nullptr);
@@ -1332,7 +1338,8 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   TmpDev tmp;
   const int ntn = (V + 255) / 256;
   const int vchunk = std::min(((V + 255) / 256) * 256, 4096);
-  bf16* WT = tmp.alloc<bf16>((size_t)V * D);
+  const long ldwt = ((long)V + 7) / 8 * 8;
+  bf16* WT = tmp.alloc<bf16>((size_t)ldwt * D);
   int* dpred = tmp.alloc<int>(n + 1);
   int* labels = tmp.alloc<int>(n + 1);
   float2* stats = tmp.alloc<float2>((size_t)(n + 1) * ntn);
@@ -1348,10 +1355,11 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   OPCK(hipMemcpy(scal, hsc, sizeof(hsc), hipMemcpyHostToDevice));
   OPCK(hipMemcpy(dpred, pred.data(), n * sizeof(int32_t), hipMemcpyHostToDevice));
   OPCK(hipMemset(err, 0, sizeof(int)));
-  OPCK(transpose_bf16((const bf16*)lm_w, D, WT, V, V, D, s));
+  OPCK(hipMemsetAsync(WT, 0, (size_t)ldwt * D * 2, s));
+  OPCK(transpose_bf16((const bf16*)lm_w, D, WT, ldwt, V, D, s));
   OPCK(build_labels(ids, dpred, labels, n, nullptr, V, err, s));
   HeadArgs a{};
-  a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w; a.WT = WT;
+  a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w; a.WT = WT; a.ldwt = ldwt;
   a.labels = labels; a.n = n; a.n_dev = nullptr; a.D = D; a.V = V; a.stats = stats; a.ntn = ntn;
   a.tgt_logit = tl; a.lse = lse; a.loss_row = lr; a.loss_out = scal + 1; a.inv_nvalid = scal;
   a.dlog = dlog; a.vchunk = vchunk; a.dH = dH;

@@ -94,6 +94,8 @@ struct EpiCEStats {
   }
 };
 
+// Columns [Nc, Nc8) of the chunk (Nc8 = round_up(Nc, 8)) are written as zero
+// so the dH product can run its K loop over whole 16-byte chunks.
 struct EpiCEGrad {
   const int* labels;
   const float* lse;
@@ -102,28 +104,29 @@ struct EpiCEGrad {
   long ldd;
   int c0;
   int Nc;
+  int Nc8;
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int,
                    void*) const {
     const float sc = *inv_nvalid;
     for_each_quad(acc, mw, nw, M, lane, [&](int m, int n, float* v) {
-      if (n >= Nc) return;
+      if (n >= Nc8) return;
       const int t = labels[m];
       const float l = lse[m];
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float e = __expf(v[i] - l) - ((c0 + n + i) == t ? 1.f : 0.f);
-        p[i] = t >= 0 ? e * sc : 0.f;
+        p[i] = (t >= 0 && n + i < Nc) ? e * sc : 0.f;
       }
       bf16* d = D + (long)m * ldd + n;
-      if (n + 3 < Nc) {
+      if (n + 3 < Nc8) {
         bf16x4 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (bf16)p[i];
         *reinterpret_cast<bf16x4*>(d) = o;
       } else {
-        for (int i = 0; i < 4 && n + i < Nc; ++i) d[i] = (bf16)p[i];
+        for (int i = 0; i < 4 && n + i < Nc8; ++i) d[i] = (bf16)p[i];
       }
     });
   }
@@ -192,14 +195,14 @@ hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s) {
   const int Nc = min(a.vchunk, a.V - c0);
   GemmProblem p{a.normed, a.ldh, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
                 a.n, Nc, a.D, 0, a.n_dev};
-  EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Nc};
+  EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Nc, (Nc + 7) / 8 * 8};
   return launch_gemm(p, epi, s);
 }
 
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
-  const int Nc = min(a.vchunk, a.V - c0);
-  GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, (long)a.V, nullptr, 0, nullptr, 0,
-                a.n, a.D, Nc, 0, a.n_dev};
+  const int Nc8 = (min(a.vchunk, a.V - c0) + 7) / 8 * 8;
+  GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, a.ldwt, nullptr, 0, nullptr, 0,
+                a.n, a.D, Nc8, 0, a.n_dev};
   EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
   return launch_gemm(q, ef, s);
 }

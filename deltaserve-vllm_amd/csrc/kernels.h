@@ -93,7 +93,8 @@ hipError_t lora_tn(const TnArgs& a, hipStream_t s);
 struct HeadArgs {
   const bf16* normed; long ldh;   // [n, D]
   const bf16* W;                  // [V, D]
-  const bf16* WT;                 // [D, V]
+  const bf16* WT;                 // [D, ldwt], columns V..ldwt zero
+  long ldwt;                      // round_up(V, 8)
   const int* labels;              // [n] target id or -1
   int n; const int* n_dev;
   int D, V;

@@ -161,10 +161,11 @@ def test_attention(seq_lens, Hq, Hkv):
         assert cosine(got, want) > 0.999
 
 
-def test_head():
+@pytest.mark.parametrize("V", [1000, 211, 1027])
+def test_head(V):
     from deltaserve_amd import ops
     seq_lens = [5, 1, 64, 300]
-    n, D, V = sum(seq_lens), 256, 1000
+    n, D = sum(seq_lens), 256
     normed = _bf(_rnd(n, D, seed=41))
     W = _bf(_rnd(V, D, seed=42) * 0.05)
     ids = torch.randint(0, V, (n,), generator=torch.Generator().manual_seed(43))
