@@ -7,16 +7,36 @@
 // LoRA factor rides along as a second K segment (K-concatenation), so
 // y = x·Wᵀ + (x·Aᵀ)·(s·B)ᵀ is one kernel with K = in + r.
 //
-// Tiling: BM×BN block tile, BK = 64, WM×WN waves, each wave owns a
-// (BM/WM)×(BN/WN) sub-tile of 32×32 MFMA fragments. Global→LDS staging is
-// double-buffered through registers (one barrier per K step) with buffer
-// loads: rows past M/N fall outside the descriptor and read as zero, and the
-// first use of a loaded value is the LDS store after the MFMAs of the current
-// step, so the loads overlap the math. LDS rows are 128 B with a 16-byte-chunk
-// XOR swizzle so fragment reads of 16 consecutive rows hit distinct banks.
+// Main loop. BK = 32; the K tiles stream through a ring of NS LDS stages that
+// are filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): no
+// VGPR staging and no ds_write instructions, so up to NS-2 stages are in
+// flight while the waves run MFMAs. Each wave owns a (BM/WM)×(BN/WN) sub-tile
+// of v_mfma_f32_32x32x16_bf16 accumulators. Per K step (two 16-deep slices):
+//   read slice-1 fragments → MFMAs of slice 0 → wait for the own loads of the
+//   next stage → barrier → issue the loads of stage kt+NS-1 into the slot
+//   freed by stage kt-1 → read slice-0 fragments of the next stage → MFMAs of
+//   slice 1.
+// The single barrier per step both publishes stage kt+1 (every wave's loads
+// landed) and retires stage kt-1 (every wave is past its reads), and the
+// next stage's first fragments are read under the current stage's last MFMAs.
+// One loop iteration per K step with a rotating stage slot; the ring always
+// issues one stage per step (zero-filled past K), so the vmcnt waits are
+// constants.
+//
+// LDS layout per stage and operand: rows of 64 B (32 bf16) as four 16-byte
+// chunks; chunk c of row r sits in slot c ^ g(r), g(r) = ((r>>1)&3) ^ ((r>>3)&1),
+// which makes the 32-row fragment reads conflict-free for both 128-byte and
+// 256-byte bank windows. The loads write LDS linearly (lane i of a load lands
+// at byte 16·i of its 1 KB segment = 16 rows), so the swizzle is applied on
+// the global side: the lane filling slot s of row r fetches chunk s ^ g(r).
+// Out-of-range rows (past M or N) and chunks past K are fetched from an offset
+// outside the buffer descriptor and land as zeros.
+//
 // Block ids are remapped so each XCD (round-robin dispatch over 8 XCDs) gets a
 // contiguous run of tiles, grouped 8 deep along M for L2 reuse.
 #pragma once
+
+#include <type_traits>
 
 #include "dsb_common.h"
 
@@ -71,18 +91,77 @@ DSB_DEV void for_each_quad(const f32x16 (&acc)[FM][FN], int mw, int nw, int M,
   }
 }
 
-template <int BM, int BN, int WM, int WN, class Epi>
+DSB_DEV int lds_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
+// The direct-to-LDS loads and the waits on them are issued as inline asm:
+// the compiler's wait-count pass then neither tracks them nor inserts its own
+// conservative vmcnt(0) before fragment reads (it loses track of which LDS
+// stage a pending load targets across the loop back edge). Correctness rests
+// on the explicit vmcnt waits below plus the barrier; the "memory" clobbers
+// keep the compiler from moving LDS accesses across them. No compiler-visible
+// global loads are outstanding while the ring runs.
+template <int N>
+DSB_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without a memory fence (a fence would wait for every
+// outstanding load, including the prefetched stages); the empty asm statements
+// keep the compiler from moving memory accesses across it.
+DSB_DEV void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// buffer_load_dwordx4 ... lds: 64 lanes × 16 B land at lds_addr + 16·lane.
+// M0 holds the LDS address (saved and restored around the load: M0 is a
+// reserved register the compiler assumes preserved); one wait state
+// separates the M0 write from the load.
+DSB_DEV void lds_dma16(u32x4 rsrc, int voff, unsigned lds_addr) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(rsrc), "s"(lds_addr)
+      : "memory");
+}
+
+// Buffer descriptor (gfx9): base, stride 0, num_records bytes, raw dword access.
+DSB_DEV u32x4 make_rsrc(const void* base, int bytes) {
+  const unsigned long a = (unsigned long)base;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((unsigned)a);
+  r[1] = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane((unsigned)bytes);
+  r[3] = 0x00020000u;
+  return r;
+}
+
+typedef __attribute__((address_space(3))) bf16 lds_bf16;
+DSB_DEV unsigned lds_addr(bf16* p) {
+  return __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)(lds_bf16*)p);
+}
+
+template <int BM, int BN, int WM, int WN, int NS, class Epi>
 __global__ __launch_bounds__(WM* WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel(GemmProblem p, Epi epi) {
-  constexpr int BK = 64, CH = 8;
-  constexpr int NT = WM * WN * 64;
+  constexpr int BK = 32;
+  constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
-  constexpr int LA = BM * CH / NT, LB = BN * CH / NT;
+  // direct-to-LDS loads per lane per stage: one load = 64 lanes × 16 B = 16 rows
+  constexpr int IA = BM / (16 * NW), IB = BN / (16 * NW), IAB = IA + IB;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be 32-aligned");
-  static_assert((BM * CH) % NT == 0 && (BN * CH) % NT == 0, "loader split");
-  constexpr int SA = BM * BK, SB = BN * BK;
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (SA + SB)];
+  static_assert(IA >= 1 && IB >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "loader split");
+  static_assert(NS >= 3 && (NS - 2) * IAB < 64, "stage ring / vmcnt range");
+  constexpr int SA = BM * BK, SE = (BM + BN) * BK;  // elements
+  __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
 
   int M = p.M;
   if (p.M_dev) M = min(M, *p.M_dev);
@@ -92,65 +171,71 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   const int m0 = pm * BM, n0 = pn * BN;
   if (m0 >= M) return;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int nk1 = (p.K1 + BK - 1) / BK;
   const int nk2 = p.K2 > 0 ? (p.K2 + BK - 1) / BK : 0;
   const int nk = nk1 + nk2;
 
-  // Buffer resources over this tile's rows of each operand: rows past M (N)
-  // fall outside num_records and load as zeros. Thread t loads 16-byte chunk
-  // ch = t % 8 of rows t/8 + i·(NT/8); the row step goes in the scalar offset.
-  constexpr int RSTEP = NT / CH;
-  const int ch = tid % CH, r0 = tid / CH;
+  // Loader geometry: lane fills slot (lane & 3) of row (lane >> 2) of its
+  // 16-row segment; every segment starts at a multiple of 16 rows, so the
+  // fetched chunk (lane & 3) ^ g(lane >> 2) is the same for every load.
+  const int lrow = lane >> 2;
+  const int lch = (lane & 3) ^ lds_swz(lrow);
   const int rowsA = min(M - m0, BM), rowsB = min(p.N - n0, BN);
+  // One descriptor per operand and K segment, over the tile's rows that
+  // exist: rows past M (N) and chunks past K (offset OR-ed with OOB) fall
+  // outside it and load as zeros, and nothing outside the operand is read.
   auto rsrc = [](const bf16* base, long ld, int rows, int K) {
-    const long bytes = rows > 0 ? (((long)(rows - 1) * ld + K) * 2) : 0;
-    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+    const int bytes = rows > 0 && K > 0 ? (int)((((long)(rows - 1) * ld) + K) * 2) : 0;
+    return make_rsrc(base, bytes);
   };
-  const __amdgpu_buffer_rsrc_t ra1 = rsrc(p.A + (long)m0 * p.lda, p.lda, rowsA, p.K1);
-  const __amdgpu_buffer_rsrc_t rb1 = rsrc(p.B + (long)n0 * p.ldb, p.ldb, rowsB, p.K1);
-  const __amdgpu_buffer_rsrc_t ra2 = rsrc(p.A2 ? p.A2 + (long)m0 * p.lda2 : p.A, p.lda2, nk2 ? rowsA : 0, p.K2);
-  const __amdgpu_buffer_rsrc_t rb2 = rsrc(p.B2 ? p.B2 + (long)n0 * p.ldb2 : p.B, p.ldb2, nk2 ? rowsB : 0, p.K2);
-  const int voffA1 = (int)(r0 * p.lda * 2 + ch * 16), voffB1 = (int)(r0 * p.ldb * 2 + ch * 16);
-  const int voffA2 = (int)(r0 * p.lda2 * 2 + ch * 16), voffB2 = (int)(r0 * p.ldb2 * 2 + ch * 16);
+  const int K2 = nk2 ? p.K2 : 0;
+  const u32x4 dA1 = rsrc(p.A + (long)m0 * p.lda, p.lda, rowsA, p.K1);
+  const u32x4 dB1 = rsrc(p.B + (long)n0 * p.ldb, p.ldb, rowsB, p.K1);
+  const u32x4 dA2 = rsrc(nk2 ? p.A2 + (long)m0 * p.lda2 : p.A, p.lda2, rowsA, K2);
+  const u32x4 dB2 = rsrc(nk2 ? p.B2 + (long)n0 * p.ldb2 : p.B, p.ldb2, rowsB, K2);
+  // lane byte offset of its first row; load i adds i·16·NW rows
+  const int rw = 16 * wave + lrow;
+  const int voA1 = (rw * (int)p.lda + lch * 8) * 2, voB1 = (rw * (int)p.ldb + lch * 8) * 2;
+  const int voA2 = (rw * (int)p.lda2 + lch * 8) * 2, voB2 = (rw * (int)p.ldb2 + lch * 8) * 2;
+  const int stA1 = 32 * NW * (int)p.lda, stB1 = 32 * NW * (int)p.ldb;   // bytes per 16·NW rows
+  const int stA2 = 32 * NW * (int)p.lda2, stB2 = 32 * NW * (int)p.ldb2;
+  // OR-ed into the offset of chunks past K: beyond any descriptor, loads zero
+  constexpr int OOB = 0x7ff00000;
+  const unsigned lds0 = lds_addr(smem);
 
-  u32x4 ra[LA], rb[LB];
-  bool kok = true;  // this thread's chunk lies below K (only the last K step can fail)
-  auto gload = [&](int kt) {
-    if (kt < nk1) {
-      const int k0 = kt * BK;
-      kok = k0 + ch * 8 < p.K1;
-#pragma unroll
-      for (int i = 0; i < LA; ++i)
-        ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra1, voffA1, (int)(i * RSTEP * p.lda * 2 + k0 * 2), 0);
-#pragma unroll
-      for (int i = 0; i < LB; ++i)
-        rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb1, voffB1, (int)(i * RSTEP * p.ldb * 2 + k0 * 2), 0);
-    } else {
-      const int k0 = (kt - nk1) * BK;
-      kok = k0 + ch * 8 < p.K2;
-#pragma unroll
-      for (int i = 0; i < LA; ++i)
-        ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra2, voffA2, (int)(i * RSTEP * p.lda2 * 2 + k0 * 2), 0);
-#pragma unroll
-      for (int i = 0; i < LB; ++i)
-        rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb2, voffB2, (int)(i * RSTEP * p.ldb2 * 2 + k0 * 2), 0);
-    }
+  // Loads of K tile kt into stage slot `slot`: IAB loads per lane, issued one
+  // at a time by issue_one(j) so they can be spread over a run of MFMAs.
+  // Tiles past the end (kt >= nk) fall past K of the second segment and fill
+  // the slot with zeros without touching memory, so every step issues the
+  // same number of loads and the vmcnt arithmetic never changes.
+  struct Fill {
+    u32x4 dA, dB;
+    int voA, voB, stA, stB;
+    unsigned dst;
   };
-  // LDS: [row][8 × 16-byte chunks], chunk slot = ch ^ ((row >> 1) & 7) so that
-  // 16 consecutive rows read at one logical chunk hit 16 distinct bank groups.
-  auto slot = [](int row, int c) { return row * BK + ((c ^ ((row >> 1) & 7)) << 3); };
-  auto sstore = [&](int buf) {
-    bf16* sA = smem + buf * (SA + SB);
-    bf16* sB = sA + SA;
-    const u32x4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < LA; ++i)
-      *reinterpret_cast<u32x4*>(sA + slot(r0 + i * RSTEP, ch)) = kok ? ra[i] : zero;
-#pragma unroll
-    for (int i = 0; i < LB; ++i)
-      *reinterpret_cast<u32x4*>(sB + slot(r0 + i * RSTEP, ch)) = kok ? rb[i] : zero;
+  auto make_fill = [&](int kt, int slot) {
+    Fill f;
+    const bool s1 = kt < nk1;
+    const int k0 = s1 ? kt * BK : (kt - nk1) * BK;
+    const int K = s1 ? p.K1 : K2;
+    const int kb = (k0 * 2) | ((k0 + lch * 8 < K) ? 0 : OOB);
+    f.dA = s1 ? dA1 : dA2;
+    f.dB = s1 ? dB1 : dB2;
+    f.voA = (s1 ? voA1 : voA2) + kb;
+    f.voB = (s1 ? voB1 : voB2) + kb;
+    f.stA = s1 ? stA1 : stA2;
+    f.stB = s1 ? stB1 : stB2;
+    f.dst = lds0 + (unsigned)(slot * SE * 2) + (unsigned)(16 * wave * BK * 2);
+    return f;
+  };
+  auto issue_one = [&](const Fill& f, int j) {
+    if (j < IA)
+      lds_dma16(f.dA, f.voA + j * f.stA, f.dst + j * 16 * NW * BK * 2);
+    else
+      lds_dma16(f.dB, f.voB + (j - IA) * f.stB, f.dst + (SA + (j - IA) * 16 * NW * BK) * 2);
   };
 
   f32x16 acc[FM][FN];
@@ -162,46 +247,89 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int lr = lane & 31, lh = lane >> 5;
-  // Fragments double-buffered across the four 16-deep K slices of a step: the
-  // LDS reads of slice kk+1 are issued before the MFMAs of slice kk.
-  bf16x8 af[2][FM], bfr[2][FN];
-  auto load_frags = [&](const bf16* sA, const bf16* sB, int kk, int b) {
-    const int kc = kk * 2 + lh;
+  // Fragment addresses (elements) inside a stage for slice kk: row r, chunk
+  // 2·kk + lh. Fragments are 32 rows apart, a multiple of 16, so g depends
+  // on lr only.
+  const int g = lds_swz(lr);
+  const int fa0 = (wm * TM + lr) * BK + (((0 + lh) ^ g) << 3);
+  const int fa1 = (wm * TM + lr) * BK + (((2 + lh) ^ g) << 3);
+  const int fb0 = SA + (wn * TN + lr) * BK + (((0 + lh) ^ g) << 3);
+  const int fb1 = SA + (wn * TN + lr) * BK + (((2 + lh) ^ g) << 3);
+  bf16x8 af0[FM], bf0[FN], af1[FM], bf1[FN];
+  auto read0 = [&](const bf16* b) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) af0[fm] = *reinterpret_cast<const bf16x8*>(b + fa0 + fm * 32 * BK);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) bf0[fn] = *reinterpret_cast<const bf16x8*>(b + fb0 + fn * 32 * BK);
+  };
+  auto read1 = [&](const bf16* b) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) af1[fm] = *reinterpret_cast<const bf16x8*>(b + fa1 + fm * 32 * BK);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) bf1[fn] = *reinterpret_cast<const bf16x8*>(b + fb1 + fn * 32 * BK);
+  };
+  auto mma0 = [&]() {
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
-      af[b][fm] = *reinterpret_cast<const bf16x8*>(sA + slot(wm * TM + fm * 32 + lr, kc));
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-      bfr[b][fn] = *reinterpret_cast<const bf16x8*>(sB + slot(wn * TN + fn * 32 + lr, kc));
+      for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = mfma32(bf0[fn], af0[fm], acc[fm][fn]);
   };
-  auto compute = [&](int buf) {
-    const bf16* sA = smem + buf * (SA + SB);
-    const bf16* sB = sA + SA;
-    load_frags(sA, sB, 0, 0);
+  // Slice-1 MFMAs with the next stage's loads spread among them: the loads'
+  // scalar set-up and issue run in the MFMA shadow instead of stalling it.
+  auto mma1_interleaved = [&](const Fill& f) {
+    constexpr int NM = FM * FN;
+    constexpr int EVERY = NM / IAB > 0 ? NM / IAB : 1;
+    int j = 0;
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      if (kk + 1 < BK / 16) load_frags(sA, sB, kk + 1, (kk + 1) & 1);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-          acc[fm][fn] = mfma32(bfr[kk & 1][fn], af[kk & 1][fm], acc[fm][fn]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < NM; ++t) {
+      const int fm = t / FN, fn = t % FN;
+      acc[fm][fn] = mfma32(bf1[fn], af1[fm], acc[fm][fn]);
+      if (t % EVERY == EVERY - 1 && j < IAB) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue_one(f, j++);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+#pragma unroll
+    for (; j < IAB; ++j) issue_one(f, j);
   };
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  // Prologue: stages 0 .. NS-2 in flight; wait for stage 0, read its slice 0.
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) {
+    const Fill f = make_fill(s, s);
+#pragma unroll
+    for (int j = 0; j < IAB; ++j) issue_one(f, j);
+  }
+  wait_vm<(NS - 2) * IAB>();
+  lds_barrier();
+  read0(smem);
+
+  int cur = 0;  // slot of stage kt
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-    compute(cur);
-    if (kt + 1 < nk) sstore(cur ^ 1);
-    __syncthreads();
+    const int nxt = cur + 1 == NS ? 0 : cur + 1;
+    const int fill = cur == 0 ? NS - 1 : cur - 1;  // slot of stage kt-1 = kt+NS-1
+    // slice-0 fragments (read one half-step ago) are complete; the compiler
+    // then waits only on the slice-1 reads where they are used.
+    __builtin_amdgcn_s_waitcnt((0 << 8) | (7 << 4) | 15 | (3 << 14));  // lgkmcnt(0)
+    read1(smem + cur * SE);
+    __builtin_amdgcn_sched_barrier(0);
+    mma0();
+    __builtin_amdgcn_sched_barrier(0);
+    // own loads of stage kt+1 landed (stages kt+2 .. kt+NS-2 may fly) → the
+    // barrier publishes stage kt+1 and retires stage kt-1's slot.
+    wait_vm<(NS - 3) * IAB>();
+    lds_barrier();
+    read0(smem + nxt * SE);
+    const Fill f = make_fill(kt + NS - 1, fill);
+    __builtin_amdgcn_sched_barrier(0);
+    mma1_interleaved(f);
+    __builtin_amdgcn_sched_barrier(0);
+    cur = nxt;
   }
 
+  wait_vm<0>();
+  __syncthreads();  // every wave is done with the stages before the epilogue reuses them
   epi.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
                                    (void*)smem);
 }
@@ -319,12 +447,13 @@ struct EpiLoraZ {
 // Tile configurations. Big: 256×256, 4 waves of 128×128 (256 accumulators per
 // lane). Mid: 128×128, 4 waves of 64×64. Skinny: 64×64, 4 waves of 32×32.
 enum GemmCfg { GEMM_BIG = 0, GEMM_MID = 1, GEMM_SKINNY = 2 };
+constexpr int GEMM_STAGES = 4;
 
 template <int BM, int BN, int WM, int WN, class Epi>
 hipError_t launch_gemm_cfg(const GemmProblem& p, const Epi& e, hipStream_t s) {
   const int nbm = (p.M + BM - 1) / BM, nbn = (p.N + BN - 1) / BN;
   if (nbm == 0 || nbn == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WM, WN, Epi>), dim3(nbm * nbn),
+  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WM, WN, GEMM_STAGES, Epi>), dim3(nbm * nbn),
                      dim3(WM * WN * 64), 0, s, p, e);
   return hipGetLastError();
 }
