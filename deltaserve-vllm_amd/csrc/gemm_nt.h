@@ -91,6 +91,72 @@ DSB_DEV void for_each_quad(const f32x16 (&acc)[FM][FN], int mw, int nw, int M,
   }
 }
 
+// Visit the wave's accumulator tile as runs of 8 consecutive output columns
+// of one row (n a multiple of 8), staged through the wave's own LDS region
+// (32 rows × TN fp32, row pitch TN + 4 floats) one 32-row fragment row at a
+// time, so TN/8 consecutive lanes cover one row and every global access of
+// the epilogue is a 16- or 32-byte row-contiguous transfer. Needs
+// 32·(TN + 4)·4 bytes of LDS per wave at `smem`; wave-local (a wave's LDS
+// accesses complete in order), so no barrier beyond the one before the
+// epilogue.
+template <int FM, int FN, class F>
+DSB_DEV void for_each_row8(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
+                           int wave, void* smem, F&& f) {
+  constexpr int TN = FN * 32, PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG;
+  static_assert(64 % CG == 0, "row groups");
+  float* buf = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int rsub = lane / CG, cg = lane % CG;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    if (mw + fm * 32 >= M) break;  // uniform: the rest of the wave tile is past M
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                         acc[fm][fn][4 * g + 3]};
+        *reinterpret_cast<f32x4*>(buf + lr * PITCH + fn * 32 + 8 * g + 4 * lh) = v;
+      }
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+      const int row = it * RPI + rsub;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
+      float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      const int m = mw + fm * 32 + row;
+      if (m < M) f(m, nw + cg * 8, v);
+    }
+  }
+}
+
+// 8 values to bf16 at p[0 .. min(8, lim)); 16-byte store when whole and aligned.
+DSB_DEV void store8_bf16(bf16* p, const float* v, int lim) {
+  if (lim >= 8 && ((unsigned long)p & 15) == 0) {
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (bf16)v[i];
+    *reinterpret_cast<bf16x8*>(p) = o;
+  } else {
+    for (int i = 0; i < 8 && i < lim; ++i) p[i] = (bf16)v[i];
+  }
+}
+// v[i] += bf16 r[i] for i < min(8, lim)
+DSB_DEV void add8_bf16(float* v, const bf16* r, int lim) {
+  if (lim >= 8 && ((unsigned long)r & 15) == 0) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] += (float)x[i];
+  } else {
+    for (int i = 0; i < 8 && i < lim; ++i) v[i] += (float)r[i];
+  }
+}
+DSB_DEV void load8_bf16(float* v, const bf16* r, int lim) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  add8_bf16(v, r, lim);
+}
+
 DSB_DEV int lds_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 
 // The direct-to-LDS loads and the waits on them are issued as inline asm:
@@ -276,14 +342,22 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   };
   // Slice-1 MFMAs with the next stage's loads spread among them: the loads'
   // scalar set-up and issue run in the MFMA shadow instead of stalling it.
-  auto mma1_interleaved = [&](const Fill& f) {
+  // The next stage's slice-0 fragment reads go out after the first MFMA so
+  // the MFMA pipe restarts right after the barrier.
+  auto mma1_interleaved = [&](const Fill& f, const bf16* next) {
     constexpr int NM = FM * FN;
     constexpr int EVERY = NM / IAB > 0 ? NM / IAB : 1;
     int j = 0;
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < NM; ++t) {
       const int fm = t / FN, fn = t % FN;
       acc[fm][fn] = mfma32(bf1[fn], af1[fm], acc[fm][fn]);
+      if (t == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        read0(next);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (t % EVERY == EVERY - 1 && j < IAB) {
         __builtin_amdgcn_sched_barrier(0);
         issue_one(f, j++);
@@ -292,6 +366,7 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     }
 #pragma unroll
     for (; j < IAB; ++j) issue_one(f, j);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Prologue: stages 0 .. NS-2 in flight; wait for stage 0, read its slice 0.
@@ -318,13 +393,10 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     __builtin_amdgcn_sched_barrier(0);
     // own loads of stage kt+1 landed (stages kt+2 .. kt+NS-2 may fly) → the
     // barrier publishes stage kt+1 and retires stage kt-1's slot.
+    const Fill f = make_fill(kt + NS - 1, fill);  // scalar set-up before the barrier
     wait_vm<(NS - 3) * IAB>();
     lds_barrier();
-    read0(smem + nxt * SE);
-    const Fill f = make_fill(kt + NS - 1, fill);
-    __builtin_amdgcn_sched_barrier(0);
-    mma1_interleaved(f);
-    __builtin_amdgcn_sched_barrier(0);
+    mma1_interleaved(f, smem + nxt * SE);
     cur = nxt;
   }
 
@@ -344,26 +416,13 @@ struct EpiBF16 {
   const bf16* R;
   long ldr;
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
-                   int, void*) const {
-    for_each_quad(acc, mw, nw, M, lane, [&](int m, int n, float* v) {
-      if (n + 3 < N) {
-        if (R) {
-          const bf16x4 r = *reinterpret_cast<const bf16x4*>(R + (long)m * ldr + n);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] += (float)r[i];
-        }
-        bf16x4 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (bf16)v[i];
-        *reinterpret_cast<bf16x4*>(C + (long)m * ldc + n) = o;
-      } else {
-        for (int i = 0; i < 4 && n + i < N; ++i) {
-          float x = v[i];
-          if (R) x += (float)R[(long)m * ldr + n + i];
-          C[(long)m * ldc + n + i] = (bf16)x;
-        }
-      }
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
+    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+      const int lim = N - n;
+      if (lim <= 0) return;
+      if (R) add8_bf16(v, R + (long)m * ldr + n, lim);
+      store8_bf16(C + (long)m * ldc + n, v, lim);
     });
   }
 };
@@ -375,16 +434,22 @@ struct EpiF32 {
   int N;
   int accumulate;
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
-                   int, void*) const {
-    for_each_quad(acc, mw, nw, M, lane, [&](int m, int n, float* v) {
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
+    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+      const int lim = N - n;
+      if (lim <= 0) return;
       float* c = C + (long)m * ldc + n;
-      if (n + 3 < N) {
-        f32x4 o = {v[0], v[1], v[2], v[3]};
-        if (accumulate) o += *reinterpret_cast<const f32x4*>(c);
-        *reinterpret_cast<f32x4*>(c) = o;
+      if (lim >= 8 && ((unsigned long)c & 15) == 0) {
+        f32x4 o0 = {v[0], v[1], v[2], v[3]}, o1 = {v[4], v[5], v[6], v[7]};
+        if (accumulate) {
+          o0 += *reinterpret_cast<const f32x4*>(c);
+          o1 += *reinterpret_cast<const f32x4*>(c + 4);
+        }
+        *reinterpret_cast<f32x4*>(c) = o0;
+        *reinterpret_cast<f32x4*>(c + 4) = o1;
       } else {
-        for (int i = 0; i < 4 && n + i < N; ++i) c[i] = accumulate ? c[i] + v[i] : v[i];
+        for (int i = 0; i < 8 && i < lim; ++i) c[i] = accumulate ? c[i] + v[i] : v[i];
       }
     });
   }
@@ -401,24 +466,25 @@ struct EpiSwiGLUBwd {
   long ldg;
   int I;
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
-                   int, void*) const {
-    for_each_quad(acc, mw, nw, M, lane, [&](int m, int n, float* v) {
-      if (n >= I) return;
-      const bf16x4 g4 = *reinterpret_cast<const bf16x4*>(GU + (long)m * ldgu + n);
-      const bf16x4 u4 = *reinterpret_cast<const bf16x4*>(GU + (long)m * ldgu + I + n);
-      bf16x4 og, ou;
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
+    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+      const int lim = I - n;
+      if (lim <= 0) return;
+      float gt[8], up[8], og[8], ou[8];
+      load8_bf16(gt, GU + (long)m * ldgu + n, lim);
+      load8_bf16(up, GU + (long)m * ldgu + I + n, lim);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float g = (float)g4[i], u = (float)u4[i];
+      for (int i = 0; i < 8; ++i) {
+        const float g = gt[i], u = up[i];
         const float sg = 1.f / (1.f + __expf(-g));
         const float silu = g * sg;
         const float dsilu = sg * (1.f + g * (1.f - sg));
-        og[i] = (bf16)(v[i] * u * dsilu);
-        ou[i] = (bf16)(v[i] * silu);
+        og[i] = v[i] * u * dsilu;
+        ou[i] = v[i] * silu;
       }
-      *reinterpret_cast<bf16x4*>(G + (long)m * ldg + n) = og;
-      *reinterpret_cast<bf16x4*>(G + (long)m * ldg + I + n) = ou;
+      store8_bf16(G + (long)m * ldg + n, og, lim);
+      store8_bf16(G + (long)m * ldg + I + n, ou, lim);
     });
   }
 };

@@ -106,28 +106,21 @@ struct EpiCEGrad {
   int Nc;
   int Nc8;
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int,
-                   void*) const {
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
     const float sc = *inv_nvalid;
-    for_each_quad(acc, mw, nw, M, lane, [&](int m, int n, float* v) {
-      if (n >= Nc8) return;
+    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+      const int lim = Nc8 - n;
+      if (lim <= 0) return;
       const int t = labels[m];
       const float l = lse[m];
-      float p[4];
+      float p[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         const float e = __expf(v[i] - l) - ((c0 + n + i) == t ? 1.f : 0.f);
         p[i] = (t >= 0 && n + i < Nc) ? e * sc : 0.f;
       }
-      bf16* d = D + (long)m * ldd + n;
-      if (n + 3 < Nc8) {
-        bf16x4 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (bf16)p[i];
-        *reinterpret_cast<bf16x4*>(d) = o;
-      } else {
-        for (int i = 0; i < 4 && n + i < Nc8; ++i) d[i] = (bf16)p[i];
-      }
+      store8_bf16(D + (long)m * ldd + n, p, lim);
     });
   }
 };
