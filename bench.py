@@ -199,6 +199,7 @@ def main():
     acts = synthetic_activations(cfg, n, n, dev)
     torch.cuda.synchronize()
     log("[bench] state built; warming up")
+    loss = float("nan")
     for _ in range(args.warmup):
         loss, nv = svc.process_backward(acts, seq_lens, n, epoch=0)
     torch.cuda.synchronize()

@@ -9,60 +9,49 @@
 //   attn_forward_core   :20-45   (scale 1/sqrt(Hd), causal mask, fp32 softmax)
 //   attn_backward_core  :48-112  (dS = P∘(dP − rowsum(dP∘P)), GQA group sums)
 // rowsum(dP∘P) is computed as rowsum(dO∘O) with the fp32 O of the forward.
+// The reference fills masked scores with −1e9 before the softmax; exp of that
+// underflows to exactly 0, so skipping masked pairs is the same arithmetic.
 //
-// Register tiles: an MFMA with A = rows of X and B = rows of Y gives
-// lane l the Y-row (l%32) and X-rows 8(r/4)+4(l/32)+r%4. A register tile used
-// again as the B operand of a product that reduces over those X-rows is fed
-// as acc[8c .. 8c+7] for each 16-row chunk c; the matching A operand is read
-// from a transposed LDS tile at rows {16c + 4(l/32) + 0..3, +8..+11}.
+// Data movement. The streamed operand (K and V in the forward and dQ passes,
+// Q and dO in the dK/dV pass) moves in 64-row × 128-column tiles through a
+// two-stage LDS ring filled by direct-to-LDS loads, one tile pair ahead of
+// the MFMAs; rows past the sequence end load as zeros. Tiles keep their
+// natural [row][dim] layout (rows of 256 B, 16-byte chunk c of row r stored
+// in slot c ^ f(r)). Products that reduce over the streamed rows need that
+// operand transposed; it is read with ds_read_b64_tr_b16, which returns, to
+// lane i of each 16-lane group, element i%4 of the 4-element pieces fetched
+// by lanes 4k + i/4 (k = 0..3). Pointing lane j of group g at row
+// base + 4·(g/2) + j/4, column d0 + 16·(g%2) + 4·(j%4) therefore hands lane l
+// rows base + 4·(l/32) + k of column d0 + l%32: the MFMA operand for 8 rows
+// {base + 4·(l/32) + 0..3, base + 8 + 4·(l/32) + 0..3}, which is exactly the
+// row set a 32×32 accumulator fragment holds for its 16-row chunk, so P and
+// dS feed the next product straight from registers.
+//
+// MFMA convention (mfma32(X, Y)): lane l supplies row l%32 of X and of Y with
+// 8 K-values each; the result lane l holds Y-row l%32 against X-rows
+// 8(r/4) + 4(l/32) + r%4, r = 0..15.
 #include "kernels.h"
+#include "tile256.h"
 
 namespace dsb {
 
 namespace {
 constexpr int HD = 128;
-constexpr int SN = 136;  // padded row stride (elements) of [tok][dim] LDS tiles
-constexpr int ST = 72;   // padded row stride of [dim][tok] LDS tiles (64 tokens)
+constexpr int TR = 64;             // rows per streamed tile
+constexpr int TILE = TR * HD;      // elements per tile (16 KB)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kScale = 0.08838834764831845f;  // 1/sqrt(128)
 
-DSB_DEV bf16x8 cat44(bf16x4 lo, bf16x4 hi) {
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+// Rows t0 .. t0+63 (those below L) of a sequence starting at global row st,
+// columns col0 .. col0+127, into a swizzled tile (4 loads per lane).
+DSB_DEV void tile_dma(const bf16* mat, long ld, int st, int t0, int L, int col0, bf16* tile,
+                      int wave, int lane) {
+  const int rows = min(max(L - t0, 0), TR);
+  tile256_dma<TR>(rows > 0 ? mat + (long)(st + t0) * ld + col0 : mat, ld, rows, 128, tile, wave,
+                  lane);
 }
 
-DSB_DEV bf16x8 read_t_frag(const bf16* sT, int row, int col) {
-  const bf16* p = sT + row * ST + col;
-  return cat44(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 8));
-}
-
-DSB_DEV bf16x8 read_n_frag(const bf16* sN, int row, int col) {
-  return *reinterpret_cast<const bf16x8*>(sN + row * SN + col);
-}
-
-// Stage a 64-token × 128-dim tile (rows tok0 .. tok0+63 of a packed sequence
-// starting at global row `st`, valid below `L`) into LDS, normal and/or
-// transposed. Token-fastest thread mapping keeps the transposed b16 writes
-// on consecutive addresses.
-DSB_DEV void stage_tile(const bf16* base, long ld, int col0, int st, int tok0, int L, bf16* sN,
-                        bf16* sT) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + i * 256;
-    const int tok = c & 63, ch = c >> 6;
-    const int t = tok0 + tok;
-    const bool ok = t < L;
-    u32x4 v = ldg128(base + (ok ? (long)(st + t) * ld + col0 + ch * 8 : 0L));
-    if (!ok) v = u32x4{0u, 0u, 0u, 0u};
-    if (sN) *reinterpret_cast<u32x4*>(sN + tok * SN + ch * 8) = v;
-    if (sT) {
-      const bf16x8 b = __builtin_bit_cast(bf16x8, v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sT[(ch * 8 + e) * ST + tok] = b[e];
-    }
-  }
-}
-
+// Row fragments of one global row (lane's row, 8 × 16 columns) straight to registers.
 DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool ok, int lh,
                             bf16x8 (&f)[8]) {
   const bf16* p = base + (ok ? row * ld + col0 : 0L);
@@ -72,19 +61,30 @@ DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool 
     if (!ok) f[kk] = bf16x8{};
   }
 }
+
+DSB_DEV bf16x8 pack_chunk(const f32x16& s, int c) {
+  bf16x8 b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = (bf16)s[8 * c + e];
+  return b;
+}
 }  // namespace
 
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+// ---------------------------------------------------------------- forward
+// Block: 128 queries (4 waves × 32) of q-head h; streams K/V tiles of its
+// kv head. LDS: 2 stages × (K tile + V tile) = 64 KB → 2 blocks per CU.
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int tile = blockIdx.x;
   if (tile >= *a.ntiles_dev) return;
   const int h = blockIdx.y, kvh = h / (a.Hq / a.Hkv);
   const int4 tl = a.tiles[tile];
   const int st = tl.x, L = tl.y, q0 = tl.z;
-  __shared__ __attribute__((aligned(16))) bf16 sK[64 * SN];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[HD * ST];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, lh = lane >> 5;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, lh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qpos = q0 + w * 32 + lr;
   const bool qok = qpos < L;
+  const int wq_last = q0 + w * 32 + 31;  // wave-uniform: last query row of this wave
 
   bf16x8 qf[8];
   load_row_frags(a.q, a.ldq, st + qpos, h * HD, qok, lh, qf);
@@ -97,63 +97,87 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   float m_i = -INFINITY, l_i = 0.f;
   const float sl2 = kScale * kLog2e;
   const int kv_end = min(L, q0 + 128);
+  const int nt = (kv_end + TR - 1) / TR;
 
-  for (int k0 = 0; k0 < kv_end; k0 += 64) {
-    __syncthreads();
-    stage_tile(a.k, a.ldk, kvh * HD, st, k0, L, sK, nullptr);
-    stage_tile(a.v, a.ldv, kvh * HD, st, k0, L, nullptr, sVt);
-    __syncthreads();
+  const FragOffs fo(lane);
+  tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
+  tile_dma(a.v, a.ldv, st, 0, L, kvh * HD, smem + TILE, w, lane);
+  for (int t = 0; t < nt; ++t) {
+    const int k0 = t * TR;
+    const char* sK = reinterpret_cast<const char*>(smem + (t & 1) * 2 * TILE);
+    const char* sV = sK + TILE * 2;
+    wait_vm<0>();
+    lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
+    if (t + 1 < nt) {
+      bf16* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+      tile_dma(a.k, a.ldk, st, k0 + TR, L, kvh * HD, nxt, w, lane);
+      tile_dma(a.v, a.ldv, st, k0 + TR, L, kvh * HD, nxt + TILE, w, lane);
+    }
+    if (k0 > wq_last) continue;  // every key of the tile is after this wave's queries
 
     f32x16 s[2];
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf) {
+      bf16x8 kfr[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[kf][r] = 0.f;
+      for (int kk = 0; kk < 8; ++kk) kfr[kk] = row_frag(sK, fo, kf * 32, kk);
+      s[kf] = mfma32(kfr[0], qf[0], f32x16{});
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        s[kf] = mfma32(read_n_frag(sK, kf * 32 + lr, kk * 16 + lh * 8), qf[kk], s[kf]);
+      for (int kk = 1; kk < 8; ++kk) s[kf] = mfma32(kfr[kk], qf[kk], s[kf]);
+    }
+#pragma unroll
+    for (int kf = 0; kf < 2; ++kf)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kf][r] *= sl2;
+    // causal / length mask, only on tiles that reach past this wave's first
+    // query or past the sequence end (wave-uniform)
+    if (k0 + TR - 1 > q0 + w * 32 || k0 + TR > L) {
+      const int lim = min(qpos, L - 1) - k0 - 4 * lh;  // key offset limit of this lane's rows
+#pragma unroll
+      for (int kf = 0; kf < 2; ++kf)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kf * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kf][r] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + kf * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        float x = s[kf][r] * sl2;
-        if (key > qpos || key >= L) x = -INFINITY;
-        s[kf][r] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kf][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_i, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_i - m_use);
+    // Lazy rescale: the running max m_i only moves when some row's tile max
+    // exceeds it by more than 8 (log2 units); otherwise p = exp2(s − m_i) <= 256,
+    // exact after the final 1/l normalisation.
+    if (__any(mx > m_i + 8.f)) {
+      const float m_new = fmaxf(m_i, mx);
+      const float alpha = m_i == -INFINITY ? 0.f : fast_exp2(m_i - m_new);
+      l_i *= alpha;
+#pragma unroll
+      for (int df = 0; df < 4; ++df)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[df][r] *= alpha;
+      m_i = m_new;
+    }
+    const float m_use = m_i == -INFINITY ? 0.f : m_i;
     float rs = 0.f;
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(s[kf][r] - m_use);
+        const float p = fast_exp2(s[kf][r] - m_use);
         s[kf][r] = p;
         rs += p;
       }
     rs += __shfl_xor(rs, 32, 64);
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-#pragma unroll
-    for (int df = 0; df < 4; ++df)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[df][r] *= alpha;
-
+    l_i += rs;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
-      const int kf = kc >> 1, c = kc & 1;
-      bf16x8 pb;
+      bf16x8 vfr[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = (bf16)s[kf][8 * c + e];
+      for (int df = 0; df < 4; ++df) vfr[df] = tr_frag(sV, fo, kc * 16, df);
+      const bf16x8 pb = pack_chunk(s[kc >> 1], kc & 1);
 #pragma unroll
-      for (int df = 0; df < 4; ++df)
-        o[df] = mfma32(read_t_frag(sVt, df * 32 + lr, kf * 32 + 16 * c + 4 * lh), pb, o[df]);
+      for (int df = 0; df < 4; ++df) o[df] = mfma32(vfr[df], pb, o[df]);
     }
   }
 
@@ -188,23 +212,27 @@ __global__ __launch_bounds__(256) void attn_dsum_kernel(AttnArgs a) {
   const int t = (int)(item / a.Hq), h = (int)(item % a.Hq), l = threadIdx.x & 63;
   const bf16* d = a.dout + (long)t * a.lddo + h * HD;
   const float* o = a.o32 + (long)t * a.ldo32 + h * HD;
-  float v = (float)d[l] * o[l] + (float)d[l + 64] * o[l + 64];
+  const bf16x2 dv = *reinterpret_cast<const bf16x2*>(d + 2 * l);
+  const f32x2 ov = *reinterpret_cast<const f32x2*>(o + 2 * l);
+  float v = (float)dv[0] * ov[0] + (float)dv[1] * ov[1];
   v = wave_sum(v);
   if (l == 0) a.dsum[(long)h * a.ld_stat + t] = v;
 }
 
-__global__ __launch_bounds__(256) void attn_dq_kernel(AttnArgs a) {
+// ---------------------------------------------------------------- dQ
+// Block: 128 queries of q-head h; streams K/V tiles. dQ = scale · dS·K.
+__global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   const int tile = blockIdx.x;
   if (tile >= *a.ntiles_dev) return;
   const int h = blockIdx.y, kvh = h / (a.Hq / a.Hkv);
   const int4 tl = a.tiles[tile];
   const int st = tl.x, L = tl.y, q0 = tl.z;
-  __shared__ __attribute__((aligned(16))) bf16 sK[64 * SN];
-  __shared__ __attribute__((aligned(16))) bf16 sKt[HD * ST];
-  __shared__ __attribute__((aligned(16))) bf16 sV[64 * SN];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, lh = lane >> 5;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, lh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qpos = q0 + w * 32 + lr;
   const bool qok = qpos < L;
+  const int wq_last = q0 + w * 32 + 31;
 
   bf16x8 qf[8], df_[8];
   load_row_frags(a.q, a.ldq, st + qpos, h * HD, qok, lh, qf);
@@ -219,42 +247,66 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
   const float sl2 = kScale * kLog2e;
   const int kv_end = min(L, q0 + 128);
+  const int nt = (kv_end + TR - 1) / TR;
 
-  for (int k0 = 0; k0 < kv_end; k0 += 64) {
-    __syncthreads();
-    stage_tile(a.k, a.ldk, kvh * HD, st, k0, L, sK, sKt);
-    stage_tile(a.v, a.ldv, kvh * HD, st, k0, L, sV, nullptr);
-    __syncthreads();
+  const FragOffs fo(lane);
+  tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
+  tile_dma(a.v, a.ldv, st, 0, L, kvh * HD, smem + TILE, w, lane);
+  for (int t = 0; t < nt; ++t) {
+    const int k0 = t * TR;
+    const char* sK = reinterpret_cast<const char*>(smem + (t & 1) * 2 * TILE);
+    const char* sV = sK + TILE * 2;
+    wait_vm<0>();
+    lds_barrier();
+    if (t + 1 < nt) {
+      bf16* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+      tile_dma(a.k, a.ldk, st, k0 + TR, L, kvh * HD, nxt, w, lane);
+      tile_dma(a.v, a.ldv, st, k0 + TR, L, kvh * HD, nxt + TILE, w, lane);
+    }
+    if (k0 > wq_last) continue;
 
     f32x16 s[2], dp[2];
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) { s[kf][r] = 0.f; dp[kf][r] = 0.f; }
+      bf16x8 kfr[8], vfr[8];
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
-        s[kf] = mfma32(read_n_frag(sK, kf * 32 + lr, kk * 16 + lh * 8), qf[kk], s[kf]);
-        dp[kf] = mfma32(read_n_frag(sV, kf * 32 + lr, kk * 16 + lh * 8), df_[kk], dp[kf]);
+        kfr[kk] = row_frag(sK, fo, kf * 32, kk);
+        vfr[kk] = row_frag(sV, fo, kf * 32, kk);
       }
+      s[kf] = mfma32(kfr[0], qf[0], f32x16{});
+      dp[kf] = mfma32(vfr[0], df_[0], f32x16{});
+#pragma unroll
+      for (int kk = 1; kk < 8; ++kk) {
+        s[kf] = mfma32(kfr[kk], qf[kk], s[kf]);
+        dp[kf] = mfma32(vfr[kk], df_[kk], dp[kf]);
+      }
+    }
+    // P = exp2(S·scale·log2e − lse); dS = P∘(dP − dsum); masked pairs give 0
+#pragma unroll
+    for (int kf = 0; kf < 2; ++kf)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kf][r] = fast_exp2(s[kf][r] * sl2 - lse2);
+    if (k0 + TR - 1 > q0 + w * 32 || k0 + TR > L) {
+      const int lim = min(qpos, L - 1) - k0 - 4 * lh;
+#pragma unroll
+      for (int kf = 0; kf < 2; ++kf)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kf * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kf][r] = 0.f;
     }
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + kf * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        const bool ok = qok && key <= qpos && key < L;
-        const float p = ok ? exp2f(s[kf][r] * sl2 - lse2) : 0.f;
-        s[kf][r] = p * (dp[kf][r] - dsum);
-      }
+      for (int r = 0; r < 16; ++r) s[kf][r] *= dp[kf][r] - dsum;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
-      const int kf = kc >> 1, c = kc & 1;
-      bf16x8 sb;
+      bf16x8 kt[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sb[e] = (bf16)s[kf][8 * c + e];
+      for (int d4 = 0; d4 < 4; ++d4) kt[d4] = tr_frag(sK, fo, kc * 16, d4);
+      const bf16x8 sb = pack_chunk(s[kc >> 1], kc & 1);
 #pragma unroll
-      for (int d4 = 0; d4 < 4; ++d4)
-        dq[d4] = mfma32(read_t_frag(sKt, d4 * 32 + lr, kf * 32 + 16 * c + 4 * lh), sb, dq[d4]);
+      for (int d4 = 0; d4 < 4; ++d4) dq[d4] = mfma32(kt[d4], sb, dq[d4]);
     }
   }
 
@@ -273,20 +325,23 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(AttnArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void attn_dkdv_kernel(AttnArgs a) {
+// ---------------------------------------------------------------- dK / dV
+// Block: 128 keys (4 waves × 32) of kv-head kvh; streams Q/dO tiles of every
+// q head of the group over the queries at or after the block's first key.
+// LDS: 2 stages × (Q tile + dO tile + lse/dsum rows) ≈ 65 KB.
+__global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   const int tile = blockIdx.x;
   if (tile >= *a.ntiles_dev) return;
   const int kvh = blockIdx.y, G = a.Hq / a.Hkv;
   const int4 tl = a.tiles[tile];
   const int st = tl.x, L = tl.y, k0 = tl.z;
-  __shared__ __attribute__((aligned(16))) bf16 sQ[64 * SN];
-  __shared__ __attribute__((aligned(16))) bf16 sQt[HD * ST];
-  __shared__ __attribute__((aligned(16))) bf16 sO[64 * SN];
-  __shared__ __attribute__((aligned(16))) bf16 sOt[HD * ST];
-  __shared__ float sL[64], sD[64];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, lh = lane >> 5;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
+  __shared__ float sLD[2][2][TR];  // [stage][lse | dsum][row]
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, lh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int key = k0 + w * 32 + lr;
   const bool kok = key < L;
+  const int wk_first = k0 + w * 32;  // wave-uniform
 
   bf16x8 kf_[8], vf_[8];
   load_row_frags(a.k, a.ldk, st + key, kvh * HD, kok, lh, kf_);
@@ -298,57 +353,117 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) { dk[i][r] = 0.f; dv[i][r] = 0.f; }
   const float sl2 = kScale * kLog2e;
+  const FragOffs fo(lane);
 
-  for (int hq = kvh * G; hq < kvh * G + G; ++hq) {
-    for (int q0 = k0; q0 < L; q0 += 64) {
-      __syncthreads();
-      stage_tile(a.q, a.ldq, hq * HD, st, q0, L, sQ, sQt);
-      stage_tile(a.dout, a.lddo, hq * HD, st, q0, L, sO, sOt);
-      if (tid < 64) {
-        const bool ok = q0 + tid < L;
-        sL[tid] = ok ? a.lse[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
-        sD[tid] = ok ? a.dsum[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
-      }
-      __syncthreads();
-
+  // (head, q tile) pairs flattened into one pipelined sequence
+  const int qt0 = k0 / TR;                 // first q tile that can see these keys
+  const int nq = (L + TR - 1) / TR - qt0;  // q tiles per head
+  const int nit = G * nq;
+  // lse/dsum rows of pair `it` (threads < 64): loaded into registers one pair
+  // ahead and stored to LDS at the end of the previous pair, so the compiler's
+  // wait on these loads never drains the tile loads issued before them.
+  float nl = 0.f, nd = 0.f;
+  auto load_ld = [&](int it) {
+    const int hq = kvh * G + it / nq;
+    const int q0 = (qt0 + it % nq) * TR;
+    const bool ok = tid < TR && q0 + tid < L;
+    nl = ok ? a.lse[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
+    nd = ok ? a.dsum[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
+  };
+  auto stage = [&](int it, int sidx) {
+    const int hq = kvh * G + it / nq;
+    const int q0 = (qt0 + it % nq) * TR;
+    bf16* d = smem + sidx * 2 * TILE;
+    tile_dma(a.q, a.ldq, st, q0, L, hq * HD, d, w, lane);
+    tile_dma(a.dout, a.lddo, st, q0, L, hq * HD, d + TILE, w, lane);
+  };
+  if (nit > 0) {
+    load_ld(0);
+    if (tid < TR) {
+      sLD[0][0][tid] = nl;
+      sLD[0][1][tid] = nd;
+    }
+    stage(0, 0);
+  }
+  for (int it = 0; it < nit; ++it) {
+    const int sidx = it & 1;
+    const int q0 = (qt0 + it % nq) * TR;
+    const bf16* sQ = smem + sidx * 2 * TILE;
+    const bf16* sO = sQ + TILE;
+    wait_vm<0>();
+    __syncthreads();  // pair `it` (tiles and lse/dsum rows) visible; the other stage is free
+    if (it + 1 < nit) {
+      load_ld(it + 1);
+      stage(it + 1, sidx ^ 1);
+    }
+    if (q0 + TR - 1 >= wk_first) {  // else every query of the tile is before this wave's keys
+      const char* cQ = reinterpret_cast<const char*>(sQ);
+      const char* cO = reinterpret_cast<const char*>(sO);
       f32x16 s[2], dp[2];
 #pragma unroll
       for (int qf = 0; qf < 2; ++qf) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) { s[qf][r] = 0.f; dp[qf][r] = 0.f; }
+        bf16x8 qfr[8], ofr[8];
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-          s[qf] = mfma32(read_n_frag(sQ, qf * 32 + lr, kk * 16 + lh * 8), kf_[kk], s[qf]);
-          dp[qf] = mfma32(read_n_frag(sO, qf * 32 + lr, kk * 16 + lh * 8), vf_[kk], dp[qf]);
+          qfr[kk] = row_frag(cQ, fo, qf * 32, kk);
+          ofr[kk] = row_frag(cO, fo, qf * 32, kk);
+        }
+        s[qf] = mfma32(qfr[0], kf_[0], f32x16{});
+        dp[qf] = mfma32(ofr[0], vf_[0], f32x16{});
+#pragma unroll
+        for (int kk = 1; kk < 8; ++kk) {
+          s[qf] = mfma32(qfr[kk], kf_[kk], s[qf]);
+          dp[qf] = mfma32(ofr[kk], vf_[kk], dp[qf]);
         }
       }
+      // lane: key row; r: queries qf·32 + 8(r/4) + 4·lh + r%4 (4 consecutive per r/4)
 #pragma unroll
       for (int qf = 0; qf < 2; ++qf)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = qf * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          const int query = q0 + qi;
-          const bool ok = kok && query < L && query >= key;
-          const float p = ok ? exp2f(s[qf][r] * sl2 - sL[qi]) : 0.f;
-          s[qf][r] = p;
-          dp[qf][r] = p * (dp[qf][r] - sD[qi]);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int qi = qf * 32 + 8 * r4 + 4 * lh;
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&sLD[sidx][0][qi]);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sLD[sidx][1][qi]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p = fast_exp2(s[qf][4 * r4 + e] * sl2 - l4[e]);
+            s[qf][4 * r4 + e] = p;
+            dp[qf][4 * r4 + e] = p * (dp[qf][4 * r4 + e] - d4[e]);
+          }
         }
+      // mask: query < key or query >= L or key >= L (tiles at the diagonal or the end)
+      if (q0 < wk_first + 31 || q0 + TR > L || wk_first + 31 >= L) {
+#pragma unroll
+        for (int qf = 0; qf < 2; ++qf)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int query = q0 + qf * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (!(kok && query < L && query >= key)) {
+              s[qf][r] = 0.f;
+              dp[qf][r] = 0.f;
+            }
+          }
+      }
 #pragma unroll
       for (int qc = 0; qc < 4; ++qc) {
-        const int qf = qc >> 1, c = qc & 1;
-        bf16x8 pb, sb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pb[e] = (bf16)s[qf][8 * c + e];
-          sb[e] = (bf16)dp[qf][8 * c + e];
-        }
-        const int col = qf * 32 + 16 * c + 4 * lh;
+        bf16x8 ot[4], qt[4];
 #pragma unroll
         for (int d4 = 0; d4 < 4; ++d4) {
-          dv[d4] = mfma32(read_t_frag(sOt, d4 * 32 + lr, col), pb, dv[d4]);
-          dk[d4] = mfma32(read_t_frag(sQt, d4 * 32 + lr, col), sb, dk[d4]);
+          ot[d4] = tr_frag(cO, fo, qc * 16, d4);
+          qt[d4] = tr_frag(cQ, fo, qc * 16, d4);
+        }
+        const bf16x8 pb = pack_chunk(s[qc >> 1], qc & 1);
+        const bf16x8 sb = pack_chunk(dp[qc >> 1], qc & 1);
+#pragma unroll
+        for (int d4 = 0; d4 < 4; ++d4) {
+          dv[d4] = mfma32(ot[d4], pb, dv[d4]);
+          dk[d4] = mfma32(qt[d4], sb, dk[d4]);
         }
       }
+    }
+    if (it + 1 < nit && tid < TR) {
+      sLD[sidx ^ 1][0][tid] = nl;
+      sLD[sidx ^ 1][1][tid] = nd;
     }
   }
 

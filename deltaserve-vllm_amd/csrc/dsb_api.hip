@@ -583,10 +583,9 @@ int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, i
   TnArgs a{};
   a.P = P; a.ldp = ldp; a.X = X; a.ldx = ldx; a.R = R; a.C = C;
   a.n = h->N; a.n_dev = &h->d_hdr->n; a.work = h->tn_work;
-  const int nrb = (R + 31) / 32;
-  const int cb = nrb == 1 ? (C + 1023) / 1024 : (C + 511) / 512;
-  const int zb = (nrb + 1) / 2;
-  int ns = (768 + cb * zb - 1) / (cb * zb);
+  // 128-column blocks × token splits: about two blocks per CU
+  const int cb = (C + 127) / 128;
+  int ns = (512 + cb - 1) / cb;
   ns = std::min(ns, 64);
   ns = std::min<long>(ns, h->tn_work_elems / ((long)R * C));
   ns = std::min(ns, std::max(1, h->N / 64));

@@ -33,6 +33,13 @@ DSB_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// One 16x16x32 bf16 MFMA. Lane l supplies row l%16 of each operand with the
+// 8 K-values 8·(l/16) .. +7; the result lane l holds Y-row l%16 against
+// X-rows 4·(l/16) + i, i = 0..3 (mfma16(X, Y)).
+DSB_DEV f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 DSB_DEV float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -71,6 +78,63 @@ DSB_DEV u32x4 pack8(const float f[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) b[i] = (bf16)f[i];
   return __builtin_bit_cast(u32x4, b);
+}
+
+// ---- direct-to-LDS loads (shared by the GEMM and attention pipelines)
+
+// The direct-to-LDS loads and the waits on them are issued as inline asm:
+// the compiler's wait-count pass then neither tracks them nor inserts its own
+// conservative vmcnt(0) before fragment reads (it loses track of which LDS
+// stage a pending load targets across the loop back edge). Correctness rests
+// on the explicit vmcnt waits below plus the barrier; the "memory" clobbers
+// keep the compiler from moving LDS accesses across them. No compiler-visible
+// global loads are outstanding while the ring runs.
+template <int N>
+DSB_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without a memory fence (a fence would wait for every
+// outstanding load, including the prefetched stages); the empty asm statements
+// keep the compiler from moving memory accesses across it.
+DSB_DEV void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// buffer_load_dwordx4 ... lds: 64 lanes × 16 B land at lds_addr + 16·lane.
+// M0 holds the LDS address (saved and restored around the load: M0 is a
+// reserved register the compiler assumes preserved); one wait state
+// separates the M0 write from the load.
+DSB_DEV void lds_dma16(u32x4 rsrc, int voff, unsigned lds_addr) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(rsrc), "s"(lds_addr)
+      : "memory");
+}
+
+// Buffer descriptor (gfx9): base, stride 0, num_records bytes, raw dword access.
+DSB_DEV u32x4 make_rsrc(const void* base, int bytes) {
+  const unsigned long a = (unsigned long)base;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((unsigned)a);
+  r[1] = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane((unsigned)bytes);
+  r[3] = 0x00020000u;
+  return r;
+}
+
+typedef __attribute__((address_space(3))) bf16 lds_bf16;
+DSB_DEV unsigned lds_addr(bf16* p) {
+  return __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)(lds_bf16*)p);
 }
 
 }  // namespace dsb

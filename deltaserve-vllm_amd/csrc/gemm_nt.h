@@ -159,61 +159,6 @@ DSB_DEV void load8_bf16(float* v, const bf16* r, int lim) {
 
 DSB_DEV int lds_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 
-// The direct-to-LDS loads and the waits on them are issued as inline asm:
-// the compiler's wait-count pass then neither tracks them nor inserts its own
-// conservative vmcnt(0) before fragment reads (it loses track of which LDS
-// stage a pending load targets across the loop back edge). Correctness rests
-// on the explicit vmcnt waits below plus the barrier; the "memory" clobbers
-// keep the compiler from moving LDS accesses across them. No compiler-visible
-// global loads are outstanding while the ring runs.
-template <int N>
-DSB_DEV void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Workgroup barrier without a memory fence (a fence would wait for every
-// outstanding load, including the prefetched stages); the empty asm statements
-// keep the compiler from moving memory accesses across it.
-DSB_DEV void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// buffer_load_dwordx4 ... lds: 64 lanes × 16 B land at lds_addr + 16·lane.
-// M0 holds the LDS address (saved and restored around the load: M0 is a
-// reserved register the compiler assumes preserved); one wait state
-// separates the M0 write from the load.
-DSB_DEV void lds_dma16(u32x4 rsrc, int voff, unsigned lds_addr) {
-  unsigned saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff), "s"(rsrc), "s"(lds_addr)
-      : "memory");
-}
-
-// Buffer descriptor (gfx9): base, stride 0, num_records bytes, raw dword access.
-DSB_DEV u32x4 make_rsrc(const void* base, int bytes) {
-  const unsigned long a = (unsigned long)base;
-  u32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((unsigned)a);
-  r[1] = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32) & 0xffffu);
-  r[2] = __builtin_amdgcn_readfirstlane((unsigned)bytes);
-  r[3] = 0x00020000u;
-  return r;
-}
-
-typedef __attribute__((address_space(3))) bf16 lds_bf16;
-DSB_DEV unsigned lds_addr(bf16* p) {
-  return __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)(lds_bf16*)p);
-}
-
 template <int BM, int BN, int WM, int WN, int NS, class Epi>
 __global__ __launch_bounds__(WM* WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel(GemmProblem p, Epi epi) {

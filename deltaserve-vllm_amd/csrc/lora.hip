@@ -10,13 +10,15 @@
 //      gB = s·Gᵀ·Z  (ops.py:144, grad_B = scaling * (gy.t() @ Z))
 //
 // Both rank-r products are HBM-bound (they stream an [n, width] activation
-// once for a few flops per byte), so neither stages through LDS: lanes load
-// 16-byte row segments straight into MFMA operand registers. For the TN
-// reduction the token dimension is the MFMA K, which the row-major
-// activation does not hold contiguously per column; each lane therefore
-// loads 8 columns × 8 tokens (eight 16-byte loads) and regroups them in
-// registers into 8 operands of 8 tokens each, one per column.
+// once for a few flops per byte). Each streams its activation through a ring
+// of LDS stages filled by direct-to-LDS loads (the tile layout of tile256.h)
+// so that tens of KB per CU are in flight, and multiplies with 16×16×32
+// MFMAs; the TN reduction over tokens reads both operands transposed from
+// LDS with ds_read_b64_tr_b16.
+#include <algorithm>
+
 #include "kernels.h"
+#include "tile256.h"
 
 namespace dsb {
 
@@ -44,154 +46,192 @@ hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunk
 }
 
 // ------------------------------------------------------------------ skinny NT
-// Block: 32 tokens, 4 waves splitting K; wave w covers K-slices of 128
-// (lane half h takes k0 + 64h + 8kk, kk < 8). MFMA rows = tokens, cols =
-// ranks, so each lane ends with 16 tokens × 1 rank per 32-rank block.
+// Z[t, j] = sum_k X[t, k]·B[j, k]. Block: 32 tokens; the X chunk [32 × 128]
+// and the B chunk [16·RB × 128] stream through a 3-stage direct-to-LDS ring
+// (one barrier per chunk); wave w multiplies columns 32w .. 32w+31 of each
+// chunk with 16×16×32 MFMAs (2 token tiles × RB rank tiles) and the four
+// waves' partial sums are added through LDS at the end.
 template <int RB>
-__global__ __launch_bounds__(256) void lora_skinny_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
+  constexpr int NS = 3, XT = 32 * 128, BT = 16 * RB * 128, SE = XT + BT;
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
   const int t0 = blockIdx.x * 32;
   if (t0 >= N) return;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, lh = lane >> 5;
-  const int j0 = blockIdx.y * RB * 32;
-  __shared__ float red[4][RB][32 * 33];
-  f32x16 acc[RB];
+  __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rows = min(N - t0, 32);
+  const bf16* X0 = a.X + (long)t0 * a.ldx;
+  const int nc = (a.K + 127) / 128;
+  // ranks j0 .. j0 + Rg - 1 of this block (groups of 64 on grid.y)
+  const int j0 = blockIdx.y * 64, Rg = min(a.R - j0, 64);
+  const bf16* Bg = a.B + (long)j0 * a.ldb;
+  auto issue = [&](int c, int slot) {
+    const int k0 = c * 128, cv = max(min(a.K - k0, 128), 0);
+    bf16* d = smem + slot * SE;
+    tile256_dma<32>(cv > 0 ? X0 + k0 : X0, a.ldx, rows, cv, d, w, lane);
+    tile256_dma<16 * RB>(cv > 0 ? Bg + k0 : Bg, a.ldb, Rg, cv, d + XT, w, lane);
+  };
+  constexpr int LPS = 2 + RB;  // loads per lane per stage
+  f32x4 acc[2][RB];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[rb][r] = 0.f;
-  const int t = t0 + li;
-  const bool tok = t < N;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  for (int kb = wave * 128; kb < a.K; kb += 4 * 128) {
-    u32x4 xv[8];
+    for (int j = 0; j < RB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // fragment offsets (bytes): row l%16 of a 16-row tile, columns 32w + 8(l/16)
+  const int fr = lane & 15, fc = 32 * w + 8 * (lane >> 4);
+  const int off = toff(fr, fc) * 2;  // tiles start at multiples of 16 rows: f(r) = f(l%16)
+
+  issue(0, 0);
+  issue(1, 1);
+  for (int c = 0; c < nc; ++c) {
+    wait_vm<LPS>();  // own loads of chunk c landed (chunk c+1 may fly)
+    lds_barrier();   // chunk c visible; slot (c+2)%3 = slot of chunk c-1 is free
+    issue(c + 2, (c + 2) % NS);
+    const char* st = reinterpret_cast<const char*>(smem + (c % NS) * SE);
+    bf16x8 xf[2], bfr[RB];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const int k = kb + 64 * lh + 8 * kk;
-      const bool ok = tok && k < a.K;
-      const u32x4 v = ldg128(a.X + (ok ? (long)t * a.ldx + k : 0L));
-      xv[kk] = ok ? v : zero;
-    }
+    for (int i = 0; i < 2; ++i) xf[i] = *reinterpret_cast<const bf16x8*>(st + off + i * 16 * 256);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int j = j0 + rb * 32 + li;
+    for (int j = 0; j < RB; ++j)
+      bfr[j] = *reinterpret_cast<const bf16x8*>(st + XT * 2 + off + j * 16 * 256);
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int k = kb + 64 * lh + 8 * kk;
-        const bool ok = j < a.R && k < a.K;
-        u32x4 bv = ldg128(a.B + (ok ? (long)j * a.ldb + k : 0L));
-        bv = ok ? bv : zero;
-        acc[rb] = mfma32(__builtin_bit_cast(bf16x8, xv[kk]), __builtin_bit_cast(bf16x8, bv),
-                         acc[rb]);
-      }
-    }
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < RB; ++j) acc[i][j] = mfma16(bfr[j], xf[i], acc[i][j]);
   }
-  // acc[rb][r]: token t0 + 8(r/4) + 4lh + r%4, rank j0 + rb*32 + li
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      red[wave][rb][(8 * (r >> 2) + 4 * lh + (r & 3)) * 33 + li] = acc[rb][r];
+  wait_vm<0>();
   __syncthreads();
-  for (int idx = threadIdx.x; idx < RB * 32 * 32; idx += 256) {
-    const int rb = idx / 1024, rem = idx % 1024, tt = rem / 32, jj = rem % 32;
-    const int tk = t0 + tt, j = j0 + rb * 32 + jj;
-    if (tk >= N || j >= a.R) continue;
-    const float v = red[0][rb][tt * 33 + jj] + red[1][rb][tt * 33 + jj] +
-                    red[2][rb][tt * 33 + jj] + red[3][rb][tt * 33 + jj];
-    a.Z[(long)tk * a.ldz + j] = (bf16)v;
+  // acc[i][j]: token 16i + l%16, ranks 16j + 4(l/16) + 0..3 → per-wave partials
+  float* red = reinterpret_cast<float*>(smem);  // [4][32][16·RB + 4]
+  constexpr int RP = 16 * RB + 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+      *reinterpret_cast<f32x4*>(red + (w * 32 + 16 * i + (lane & 15)) * RP + 16 * j +
+                                4 * (lane >> 4)) = acc[i][j];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 32 * 16 * RB; idx += 256) {
+    const int tt = idx / (16 * RB), jj = idx % (16 * RB);
+    if (tt >= rows || jj >= Rg) continue;
+    const float v = red[tt * RP + jj] + red[(32 + tt) * RP + jj] + red[(64 + tt) * RP + jj] +
+                    red[(96 + tt) * RP + jj];
+    a.Z[(long)(t0 + tt) * a.ldz + j0 + jj] = (bf16)v;
   }
 }
 
 hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s) {
   if (a.R <= 0 || a.n <= 0) return hipSuccess;
-  const int nrb = (a.R + 31) / 32;
-  const dim3 grid((a.n + 31) / 32, (nrb + 1) / 2);
-  if (nrb == 1)
-    hipLaunchKernelGGL(lora_skinny_kernel<1>, dim3(grid.x, 1), dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(lora_skinny_kernel<2>, grid, dim3(256), 0, s, a);
+  const dim3 grid((a.n + 31) / 32, (a.R + 63) / 64);
+  switch ((std::min(a.R, 64) + 15) / 16) {
+    case 1: hipLaunchKernelGGL(lora_skinny_kernel<1>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(lora_skinny_kernel<2>, grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(lora_skinny_kernel<3>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(lora_skinny_kernel<4>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ TN
-// Block: 4 waves × (32 lanes × CPL columns); one token split; RB rank blocks.
-// Per 16-token step, lane (li, lh) loads CPL columns c0 + CPL·li .. of tokens
-// t + 8lh + e (e < 8), and MFMA #cc consumes column c0 + CPL·li + cc across
-// those 8 tokens. Output lane: rank j0 + 32rb + li, columns
-// c0 + CPL·(8(r/4) + 4lh + r%4) + cc. Partials go to work[split][C][R].
-template <int RB, int CPL>
-__global__ __launch_bounds__(256) void lora_tn_partial_kernel(TnArgs a) {
+// work[split][c][j] = sum over the split's tokens t of X[t, c]·P[t, j].
+// Block: 128 columns × one token split; token chunks of 32 stream through a
+// 4-stage direct-to-LDS ring: X chunk [32 × 128] (swizzled 256-byte rows) and
+// P chunk [32 × R] (rows of 2R bytes). Both operands reduce over tokens, so
+// both are read transposed with ds_read_b64_tr_b16 (16×16×32 pattern: lane j
+// of group g points at row 8g + j/4 (+4), column c0 + 4(j%4)); wave w owns
+// columns 32w .. 32w+31 (2 column tiles) × RB rank tiles.
+template <int RB>
+__global__ __launch_bounds__(256, 2) void lora_tn_partial_kernel(TnArgs a) {
+  constexpr int NS = 4, XT = 32 * 128, PT = 32 * 16 * RB, SE = XT + PT;
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, lh = lane >> 5;
-  const int c0 = (blockIdx.x * 4 + wave) * 32 * CPL;
-  const int j0 = blockIdx.z * RB * 32;
-  const int sp = blockIdx.y;
+  __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c0 = blockIdx.x * 128, sp = blockIdx.y;
   int per = (N + a.nsplit - 1) / a.nsplit;
-  per = (per + 15) & ~15;
+  per = (per + 31) & ~31;
   const int ta = min(N, sp * per), tb = min(N, ta + per);
-  f32x16 acc[RB][CPL];
+  const int nk = (tb - ta + 31) / 32;
+  const int cv = min(a.C - c0, 128);
+  // ranks j0 .. j0 + R - 1 of this block (groups of 64 on grid.z)
+  const int j0 = blockIdx.z * 64, R = min(a.R - j0, 64);
+  const bf16* Pg = a.P + j0;
+  // P chunk loads: 32 rows × R ranks = 4·RB loads of 1 KB; wave w issues the
+  // ones with index ≡ w (mod 4), so waves 0 .. RB-1 issue one each per stage.
+  const bool pw = w < RB;
+  auto issue = [&](int k, int slot) {
+    const int t = ta + k * 32, rv = max(min(tb - t, 32), 0);
+    bf16* d = smem + slot * SE;
+    tile256_dma<32>(rv > 0 ? a.X + (long)t * a.ldx + c0 : a.X, a.ldx, rv, cv, d, w, lane);
+    if (pw) {
+      // P rows of R ranks: lane q of load w covers row q / (R/8), ranks 8·(q % (R/8))
+      const int q = w * 64 + lane, per_row = R / 8;
+      const int row = q / per_row, ch = q % per_row;
+      const int bytes = rv > 0 ? (int)((((long)(rv - 1) * a.ldp) + R) * 2) : 0;
+      const u32x4 rs = make_rsrc(rv > 0 ? Pg + (long)t * a.ldp : Pg, bytes);
+      const int voff = row < 32 ? (int)(((long)row * a.ldp + ch * 8) * 2) : 0x7ff00000;
+      lds_dma16(rs, voff, lds_addr(d + XT + w * 512));
+    }
+  };
+  f32x4 acc[2][RB];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int cc = 0; cc < CPL; ++cc)
+    for (int j = 0; j < RB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // transposed-read addresses (bytes): X tile row 8g + j/4 (+4), column 32w + 16i + 4(j%4);
+  // P tile row 8g + j/4 (+4), rank 16j' + 4(j%4) at a row pitch of 2R bytes
+  const int g = lane >> 4, jl = lane & 15;
+  const int xr = 8 * g + (jl >> 2);
+  int xo[2][2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[rb][cc][r] = 0.f;
-  const int cl = c0 + CPL * li;
-  const bool cok = cl < a.C;
-  for (int t = ta; t < tb; t += 16) {
-    bf16 xs[8][CPL];
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int tt = t + 8 * lh + e;
-      const bool ok = cok && tt < tb;
-      if constexpr (CPL == 8) {
-        u32x4 v = ldg128(a.X + (ok ? (long)tt * a.ldx + cl : 0L));
-        if (!ok) v = u32x4{0u, 0u, 0u, 0u};
-        const bf16x8 b = __builtin_bit_cast(bf16x8, v);
+    for (int h = 0; h < 2; ++h) xo[i][h] = toff(xr + 4 * h, 32 * w + 16 * i + 4 * (jl & 3)) * 2;
+  const int po = (xr * R + 4 * (jl & 3)) * 2;
+
+  for (int k = 0; k < NS - 1; ++k) issue(k, k);
+  for (int k = 0; k < nk; ++k) {
+    if (pw) wait_vm<(NS - 2) * 3>(); else wait_vm<(NS - 2) * 2>();
+    lds_barrier();
+    issue(k + NS - 1, (k + NS - 1) % NS);
+    const char* st = reinterpret_cast<const char*>(smem + (k % NS) * SE);
+    bf16x8 xf[2], pf[RB];
 #pragma unroll
-        for (int cc = 0; cc < 8; ++cc) xs[e][cc] = b[cc];
-      } else {
-        u32x2 v = *reinterpret_cast<const u32x2*>(a.X + (ok ? (long)tt * a.ldx + cl : 0L));
-        if (!ok) v = u32x2{0u, 0u};
-        const bf16x4 b = __builtin_bit_cast(bf16x4, v);
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) xs[e][cc] = b[cc];
-      }
+    for (int i = 0; i < 2; ++i) {
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + xo[i][0]));
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + xo[i][1]));
+      xf[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int j = j0 + rb * 32 + li;
-      bf16x8 pb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tt = t + 8 * lh + e;
-        const bool ok = j < a.R && tt < tb;
-        const bf16 v = a.P[ok ? (long)tt * a.ldp + j : 0L];
-        pb[e] = ok ? v : (bf16)0.f;
-      }
-#pragma unroll
-      for (int cc = 0; cc < CPL; ++cc) {
-        bf16x8 av;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) av[e] = xs[e][cc];
-        acc[rb][cc] = mfma32(av, pb, acc[rb][cc]);
-      }
+    for (int j = 0; j < RB; ++j) {
+      const char* pp = st + XT * 2 + po + j * 32;
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pp);
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(pp + 4 * R * 2));
+      pf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < RB; ++j) acc[i][j] = mfma16(pf[j], xf[i], acc[i][j]);
   }
+  wait_vm<0>();
+  // acc[i][j]: column c0 + 32w + 16i + l%16, ranks 16j + 4(l/16) + 0..3
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int j = j0 + rb * 32 + li;
-    if (j >= a.R) continue;
+  for (int i = 0; i < 2; ++i) {
+    const int col = c0 + 32 * w + 16 * i + (lane & 15);
+    if (col >= a.C) continue;
 #pragma unroll
-    for (int cc = 0; cc < CPL; ++cc)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int col = c0 + CPL * (8 * (r >> 2) + 4 * lh + (r & 3)) + cc;
-        if (col < a.C) a.work[((long)sp * a.C + col) * a.R + j] = acc[rb][cc][r];
+    for (int j = 0; j < RB; ++j) {
+      const int jr = 16 * j + 4 * (lane >> 4);
+      float* o = a.work + ((long)sp * a.C + col) * a.R + j0 + jr;
+      if (jr + 3 < R) {
+        *reinterpret_cast<f32x4*>(o) = acc[i][j];
+      } else {
+        for (int e = 0; e < 4 && jr + e < R; ++e) o[e] = acc[i][j][e];
       }
+    }
   }
 }
 
@@ -212,17 +252,16 @@ __global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnArgs a) {
 
 hipError_t lora_tn(const TnArgs& a, hipStream_t s) {
   if (a.R <= 0 || a.C <= 0) return hipSuccess;
-  const int nrb = (a.R + 31) / 32;
-  hipError_t e;
-  if (nrb == 1) {
-    const int cb = (a.C + 4 * 256 - 1) / (4 * 256);
-    hipLaunchKernelGGL((lora_tn_partial_kernel<1, 8>), dim3(cb, a.nsplit, 1), dim3(256), 0, s, a);
-  } else {
-    const int cb = (a.C + 4 * 128 - 1) / (4 * 128);
-    hipLaunchKernelGGL((lora_tn_partial_kernel<2, 4>), dim3(cb, a.nsplit, (nrb + 1) / 2),
-                       dim3(256), 0, s, a);
+  const dim3 grid((a.C + 127) / 128, a.nsplit, (a.R + 63) / 64);
+  switch ((std::min(a.R, 64) + 15) / 16) {
+    case 1: hipLaunchKernelGGL(lora_tn_partial_kernel<1>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(lora_tn_partial_kernel<2>, grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(lora_tn_partial_kernel<3>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(lora_tn_partial_kernel<4>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
   }
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   const long tot = (long)a.R * a.C;
   hipLaunchKernelGGL(lora_tn_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
                      s, a);
