@@ -163,6 +163,38 @@ def cpu_baseline(cfg, seq_lens, budget_tokens):
                        f"{t_head:.2f}s), cycle extrapolated as L*layer+head")}
 
 
+def copy_calibration(nbytes=2 << 30, reps=3):
+    """A plain device-to-device copy of `nbytes` (reads and writes `nbytes`
+    once per launch), profiled under the same counters as the bench to turn
+    FETCH_SIZE / WRITE_SIZE into bytes."""
+    import torch
+    torch.cuda.set_device(0)
+    a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"[bench] copy calibration: {reps} copies of {nbytes} bytes")
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm256_bf16.json")
+
+
+def measured_traffic(kernel_class):
+    """HBM bytes per launch of the dominant kernel class, from the committed
+    PMC summary (FETCH_SIZE and WRITE_SIZE passes scaled by a copy of known
+    size); None when no summary for this class exists."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel_class") != kernel_class:
+        return None
+    return t.get("traffic_bytes_per_launch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,7 +204,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--classes-out", default=os.path.join(ROOT, "gpurun_out", "kernel_classes.json"))
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of 2 GiB (3 times) and exit: the "
+                         "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (no collectives, no sharding); "
               f"--gpus {args.gpus} is not supported. Run with --gpus 1.", file=sys.stderr)
@@ -264,7 +302,8 @@ def main():
     if dom:
         roofline = {"bound": dom["bound"], "achieved": round(dom["achieved"], 2),
                     "peak": PEAK_BF16_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBS,
-                    "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": None,
+                    "unit": dom["unit"], "frac": round(dom["frac"], 4),
+                    "traffic": measured_traffic(dom["class"]),
                     "kernel": dom["class"],
                     "avg_launch_us": round(dom["avg_launch_us"], 2),
                     "algorithmic_per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma"
