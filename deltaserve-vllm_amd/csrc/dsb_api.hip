@@ -208,7 +208,7 @@ struct dsb_handle {
   bool finalized = false;
   std::vector<void*> allocs;
   // workspace
-  bf16 *xn1, *qkv_pre, *qk, *ctx, *resid, *xn2, *gu, *hb;
+  bf16 *xn1, *qkv_pre, *qk, *ctx, *resid, *xn2, *gu, *hb, *gh;
   float *o32, *lse, *dsum;
   bf16 *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
   bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
@@ -330,6 +330,7 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->xn2, NN * D));
   CKR(dalloc(h, &h->gu, NN * 2 * I));
   CKR(dalloc(h, &h->hb, NN * I));
+  CKR(dalloc(h, &h->gh, NN * I));
   CKR(dalloc(h, &h->Zqkv_b, NN * 3 * r));
   CKR(dalloc(h, &h->Zo_b, NN * r));
   CKR(dalloc(h, &h->Zgu_b, NN * 2 * r));
@@ -737,10 +738,15 @@ int enqueue(dsb_handle* h, hipStream_t st) {
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
     if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
     {
+      // gh = g·W_down (+ gZ_d·A_d): grad wrt h = silu(gate)·up
       GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
                     hd ? ls.AdT : nullptr, (long)r, N, I, D, hd ? r : 0, nd};
-      EpiSwiGLUBwd e{h->gu, 2L * I, h->Ggu, 2L * I, I};
-      CKR(gemm(h, "swiglu", p, e, st, 4.0, 4.0 * I));
+      EpiBF16 e{h->gh, (long)I, I, nullptr, 0};
+      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
+    }
+    {
+      KScope ks(h, st, "swiglu_bwd", 0, 0, 0, 10.0 * I, 0, 0);
+      LK(swiglu_bwd(h->gh, I, h->gu, 2L * I, h->Ggu, 2L * I, N, nd, I, st));
     }
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];

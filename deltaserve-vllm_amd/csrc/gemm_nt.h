@@ -151,11 +151,6 @@ DSB_DEV void add8_bf16(float* v, const bf16* r, int lim) {
     for (int i = 0; i < 8 && i < lim; ++i) v[i] += (float)r[i];
   }
 }
-DSB_DEV void load8_bf16(float* v, const bf16* r, int lim) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = 0.f;
-  add8_bf16(v, r, lim);
-}
 
 DSB_DEV int lds_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 
@@ -396,40 +391,6 @@ struct EpiF32 {
       } else {
         for (int i = 0; i < 8 && i < lim; ++i) c[i] = accumulate ? c[i] + v[i] : v[i];
       }
-    });
-  }
-};
-
-// SwiGLU backward fused into the down-projection dX product:
-//   gh = acc (grad wrt h = silu(gate)·up), gate = GU[m, n], up = GU[m, I + n]
-//   G[m, n] = gh·up·silu'(gate), G[m, I + n] = gh·silu(gate)
-// with silu'(g) = σ(g)·(1 + g·(1 − σ(g))).
-struct EpiSwiGLUBwd {
-  const bf16* GU;
-  long ldgu;
-  bf16* G;
-  long ldg;
-  int I;
-  template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
-                   void* smem) const {
-    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
-      const int lim = I - n;
-      if (lim <= 0) return;
-      float gt[8], up[8], og[8], ou[8];
-      load8_bf16(gt, GU + (long)m * ldgu + n, lim);
-      load8_bf16(up, GU + (long)m * ldgu + I + n, lim);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float g = gt[i], u = up[i];
-        const float sg = 1.f / (1.f + __expf(-g));
-        const float silu = g * sg;
-        const float dsilu = sg * (1.f + g * (1.f - sg));
-        og[i] = v[i] * u * dsilu;
-        ou[i] = v[i] * silu;
-      }
-      store8_bf16(G + (long)m * ldg + n, og, lim);
-      store8_bf16(G + (long)m * ldg + I + n, ou, lim);
     });
   }
 };
