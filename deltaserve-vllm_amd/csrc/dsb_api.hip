@@ -17,6 +17,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <array>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -246,10 +247,30 @@ struct dsb_handle {
   std::vector<KRec> krec;
   size_t kpos = 0, kcount = 0;
   std::vector<KClass> kcls;
+  // publish into the served LoRA slots (trainer.py:760-802)
+  struct Served {
+    void* a = nullptr;
+    long lda = 0;
+    void* b = nullptr;
+    long ldb = 0;
+  };
+  std::vector<std::array<Served, DSB_NUM_PROJ>> served;
+  CastJob* d_pub_jobs = nullptr;
+  int2* d_pub_chunks = nullptr;
+  int npub_chunks = 0;
+  long pub_elems = 0;
   // graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
   bool graph_failed = false;
+  // pause-point path: one graph per segment, run-ahead event ring
+  std::vector<hipGraphExec_t> seg_exec;
+  std::vector<hipGraph_t> seg_graph;
+  std::vector<hipEvent_t> ring;
+  bool in_step = false;
+  int seg_next = 0;
+  int step_nseq = 0;
+  std::vector<int32_t> step_lens;
   std::mutex mu;
   std::string err;
 };
@@ -388,7 +409,7 @@ int finalize(dsb_handle* h) {
   std::vector<int2> opt_chunks;
   const float s = h->s;
   auto job = [&](const float* src, int rows, int cols, int lds, bf16* dst, int ldd, int tr,
-                 float sc) { jobs.push_back(CastJob{src, dst, rows, cols, lds, ldd, tr, sc}); };
+                 float sc) { jobs.push_back(CastJob{src, dst, rows, cols, lds, ldd, tr, sc, 0.f}); };
   for (int i = 0; i < h->L; ++i) {
     LayerState& ls = h->layers[i];
     if (ls.has[DSB_PROJ_Q]) {
@@ -598,85 +619,93 @@ int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, i
   return 0;
 }
 
-// The whole cycle on stream s (captured once into a graph).
-int enqueue(dsb_handle* h, hipStream_t st) {
+// One segment of the cycle on stream st. Segments: 0 = RoPE table, LoRA
+// operand casts and the LM head (head.py:42-100); 1 .. L = decoder layer
+// L - seg, forward recompute + backward; L + 1 = per-layer clip, AdamW and the
+// publish into the served LoRA slots. The cycle is the segments in order
+// (captured as one graph); the pause-point path (reference base.py:148-208,
+// _maybe_pause per layer) launches them one graph per segment.
+int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
   const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
   const int* nd = &h->d_hdr->n;
   const float eps = h->d.rms_eps;
   const double Hq = h->Hq;
-  h->kpos = 0;
-  {
-    KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
-    LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
-  }
-  {
-    KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
-    LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
-  }
-
-  // ---- head: loss and grad wrt final_in (head.py:42-100)
-  {
-    KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
-    LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
-  }
-  {
-    KScope ks(h, st, "labels", 0, 0, 0, 16, 0, 0);
-    LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
-  }
-  HeadArgs ha{};
-  ha.normed = h->normed; ha.ldh = D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.ldwt = h->ldwt;
-  ha.labels = h->labels;
-  ha.n = N; ha.n_dev = nd; ha.D = D; ha.V = h->V; ha.stats = h->stats; ha.ntn = h->ntn;
-  ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
-  ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
-  ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH;
-  {
-    // logits recompute in the LSE pass is not algorithmic work (6·M·D·V vs 4·M·D·V)
-    KScope ks(h, st, "gemm256_ce_stats", 0, 0, 0, 2.0 * D + 8.0 * h->ntn, 0, 2.0 * h->V * D);
-    LK(head_stats(ha, st));
-  }
-  {
-    KScope ks(h, st, "ce_reduce", 0, 0, 0, 8.0 * h->ntn + 16, 0, 0);
-    LK(head_reduce(ha, st));
-  }
-  for (int c0 = 0; c0 < h->V; c0 += h->vchunk) {
-    const int Nc = std::min(h->vchunk, h->V - c0);
+  if (seg == 0) {
+    h->kpos = 0;  // kernel-timing records restart with every cycle
     {
-      KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, Nc))) + "_ce_grad", 2.0 * Nc * D, 0,
-                0, 2.0 * D + 2.0 * Nc, 0, 2.0 * Nc * D);
-      LK(head_chunk_grad(ha, c0, st));
+      KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
+      LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
     }
     {
-      KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, D))) + "_f32", 2.0 * Nc * D, 0, 0,
-                2.0 * Nc + 8.0 * D, 0, 2.0 * Nc * D);
-      LK(head_chunk_dh(ha, c0, st));
+      KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
+      LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
     }
-  }
-  bf16* g = h->g0;
-  bf16* gnext = h->g1;
-  {
-    KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
-    LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, g, D, N, nd, D,
-                   eps, st));
-  }
 
-  AttnArgs at{};
-  at.q = h->qk; at.ldq = q + kv;
-  at.k = h->qk + q; at.ldk = q + kv;
-  at.v = h->qkv_pre + q + kv; at.ldv = W3;
-  at.ctx = h->ctx; at.ldc = q; at.o32 = h->o32; at.ldo32 = q;
-  at.lse = h->lse; at.dsum = h->dsum; at.ld_stat = N + 1;
-  at.dout = h->gctx; at.lddo = q;
-  at.dq = h->gqkv; at.lddq = W3;
-  at.dk = h->gqkv + q; at.lddk = W3;
-  at.dv = h->gqkv + q + kv; at.lddv = W3;
-  at.tiles = h->d_tiles; at.ntiles_dev = &h->d_hdr->ntiles; at.max_tiles = h->max_tiles;
-  at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
-  // one causal attention matmul = Hq·Hd·S flops (S = sum L(L+1), unmasked pairs ×2)
-  const double au = Hq * 128.0;
-  const double arow = 2.0 * (q + 2.0 * kv);
-
-  for (int li = h->L - 1; li >= 0; --li) {
+    // ---- head: loss and grad wrt final_in (head.py:42-100)
+    {
+      KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
+    }
+    {
+      KScope ks(h, st, "labels", 0, 0, 0, 16, 0, 0);
+      LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
+    }
+    HeadArgs ha{};
+    ha.normed = h->normed; ha.ldh = D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.ldwt = h->ldwt;
+    ha.labels = h->labels;
+    ha.n = N; ha.n_dev = nd; ha.D = D; ha.V = h->V; ha.stats = h->stats; ha.ntn = h->ntn;
+    ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
+    ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
+    ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH;
+    {
+      // logits recompute in the LSE pass is not algorithmic work (6·M·D·V vs 4·M·D·V)
+      KScope ks(h, st, "gemm256_ce_stats", 0, 0, 0, 2.0 * D + 8.0 * h->ntn, 0, 2.0 * h->V * D);
+      LK(head_stats(ha, st));
+    }
+    {
+      KScope ks(h, st, "ce_reduce", 0, 0, 0, 8.0 * h->ntn + 16, 0, 0);
+      LK(head_reduce(ha, st));
+    }
+    for (int c0 = 0; c0 < h->V; c0 += h->vchunk) {
+      const int Nc = std::min(h->vchunk, h->V - c0);
+      {
+        KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, Nc))) + "_ce_grad", 2.0 * Nc * D, 0,
+                  0, 2.0 * D + 2.0 * Nc, 0, 2.0 * Nc * D);
+        LK(head_chunk_grad(ha, c0, st));
+      }
+      {
+        KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, D))) + "_f32", 2.0 * Nc * D, 0, 0,
+                  2.0 * Nc + 8.0 * D, 0, 2.0 * Nc * D);
+        LK(head_chunk_dh(ha, c0, st));
+      }
+    }
+    {
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, h->g0, D, N, nd, D,
+                     eps, st));
+    }
+    return 0;
+  }
+  if (seg <= h->L) {
+    const int li = h->L - seg;
+    // the incoming gradient alternates between the two g buffers layer by layer
+    bf16* g = ((seg - 1) & 1) ? h->g1 : h->g0;
+    bf16* gnext = ((seg - 1) & 1) ? h->g0 : h->g1;
+    AttnArgs at{};
+    at.q = h->qk; at.ldq = q + kv;
+    at.k = h->qk + q; at.ldk = q + kv;
+    at.v = h->qkv_pre + q + kv; at.ldv = W3;
+    at.ctx = h->ctx; at.ldc = q; at.o32 = h->o32; at.ldo32 = q;
+    at.lse = h->lse; at.dsum = h->dsum; at.ld_stat = N + 1;
+    at.dout = h->gctx; at.lddo = q;
+    at.dq = h->gqkv; at.lddq = W3;
+    at.dk = h->gqkv + q; at.lddk = W3;
+    at.dv = h->gqkv + q + kv; at.lddv = W3;
+    at.tiles = h->d_tiles; at.ntiles_dev = &h->d_hdr->ntiles; at.max_tiles = h->max_tiles;
+    at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
+    // one causal attention matmul = Hq·Hd·S flops (S = sum L(L+1), unmasked pairs ×2)
+    const double au = Hq * 128.0;
+    const double arow = 2.0 * (q + 2.0 * kv);
     LayerState& ls = h->layers[li];
     const bf16* x = h->layer_in[li];
     const long ldx = h->act_ld;
@@ -830,9 +859,8 @@ int enqueue(dsb_handle* h, hipStream_t st) {
       LK(rmsnorm_bwd(x, ldx, h->gxn1, true, D, (const bf16*)ls.w.in_ln, h->grm, D, gnext, D, N,
                      nd, D, eps, st));
     }
-    std::swap(g, gnext);
+    return 0;
   }
-
   // ---- per-layer clip + AdamW (trainer.py:624-636, :668)
   {
     KScope ks(h, st, "clip_adamw", 0, 0, 0, 0, 0, (double)h->opt_elems * 28.0);
@@ -840,7 +868,183 @@ int enqueue(dsb_handle* h, hipStream_t st) {
                   h->d_opt_partial, h->d_sq, &h->d_hdr->hyper,
                   (h->d.flags & DSB_FLAG_NO_CLIP) ? 0 : 1, st));
   }
+  if (h->npub_chunks > 0) {
+    KScope ks(h, st, "lora_publish", 0, 0, 0, 0, 0, (double)h->pub_elems * 6.0);
+    LK(lora_cast(h->d_pub_jobs, h->d_pub_chunks, h->npub_chunks, st));
+  }
   h->kcount = h->kpos;
+  return 0;
+}
+
+int num_segments(const dsb_handle* h) { return h->L + 2; }
+
+// The whole cycle on stream st.
+int enqueue(dsb_handle* h, hipStream_t st) {
+  for (int sgi = 0; sgi < num_segments(h); ++sgi) CKR(enqueue_segment(h, sgi, st));
+  return 0;
+}
+
+// Drops every captured graph (pointers baked into them changed).
+void drop_graphs(dsb_handle* h) {
+  if (h->gexec) (void)hipGraphExecDestroy(h->gexec);
+  if (h->graph) (void)hipGraphDestroy(h->graph);
+  h->gexec = nullptr;
+  h->graph = nullptr;
+  for (auto& e : h->seg_exec)
+    if (e) (void)hipGraphExecDestroy(e);
+  for (auto& g : h->seg_graph)
+    if (g) (void)hipGraphDestroy(g);
+  h->seg_exec.assign(h->seg_exec.size(), nullptr);
+  h->seg_graph.assign(h->seg_graph.size(), nullptr);
+}
+
+// Publish jobs (trainer.py:760-802): A -> a_slot[:r, :in] and s·B ->
+// b_slot[:out, :r], both clamped to ±6.5e4 and cast to bf16, for every
+// projection with a bound served slot. Rebuilt whenever a slot is bound.
+int rebuild_publish(dsb_handle* h) {
+  const int D = h->D, q = h->q, kv = h->kv, I = h->I, r = h->r;
+  const int ins[7] = {D, D, D, q, D, D, I}, outs[7] = {q, kv, kv, D, I, I, D};
+  std::vector<CastJob> jobs;
+  for (int i = 0; i < h->L; ++i)
+    for (int p = 0; p < DSB_NUM_PROJ; ++p) {
+      const auto& sv = h->served[i][p];
+      if (!sv.a || !h->layers[i].has[p]) continue;
+      const dsb_lora_tensors& t = h->layers[i].lora[p];
+      jobs.push_back(CastJob{t.A, (bf16*)sv.a, r, ins[p], ins[p], (int)sv.lda, 0, 1.f, 6.5e4f});
+      jobs.push_back(CastJob{t.B, (bf16*)sv.b, outs[p], r, r, (int)sv.ldb, 0, h->s, 6.5e4f});
+    }
+  std::vector<int2> chunks;
+  long elems = 0;
+  for (int j = 0; j < (int)jobs.size(); ++j) {
+    const long tot = (long)jobs[j].rows * jobs[j].cols;
+    elems += tot;
+    for (long st = 0; st < tot; st += 1024) chunks.push_back(int2{j, (int)st});
+  }
+  CK(hipStreamSynchronize(h->hs));
+  if (h->d_pub_jobs) CK(hipFree(h->d_pub_jobs));
+  if (h->d_pub_chunks) CK(hipFree(h->d_pub_chunks));
+  h->d_pub_jobs = nullptr;
+  h->d_pub_chunks = nullptr;
+  h->npub_chunks = 0;
+  h->pub_elems = elems;
+  if (!jobs.empty()) {
+    CK(hipMalloc(&h->d_pub_jobs, jobs.size() * sizeof(CastJob)));
+    CK(hipMemcpy(h->d_pub_jobs, jobs.data(), jobs.size() * sizeof(CastJob), hipMemcpyHostToDevice));
+    CK(hipMalloc(&h->d_pub_chunks, chunks.size() * sizeof(int2)));
+    CK(hipMemcpy(h->d_pub_chunks, chunks.data(), chunks.size() * sizeof(int2),
+                 hipMemcpyHostToDevice));
+    h->npub_chunks = (int)chunks.size();
+  }
+  drop_graphs(h);
+  return 0;
+}
+
+// Validates and packs a cycle, stages its device block (one H2D copy on the
+// library stream, ordered after the caller's stream) and records the start.
+int step_prepare(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, int64_t step,
+                 hipStream_t cs) {
+  h->err.clear();
+  if (n <= 0 || n > h->N) return fail(h, "dsb_step: n must be in [1, s_max]");
+  if (nseq <= 0 || nseq > h->d.max_seqs) return fail(h, "dsb_step: nseq out of range");
+  if (step < 1) return fail(h, "dsb_step: step must be >= 1");
+  if (!seq_lens) return fail(h, "dsb_step: null seq_lens");
+  if (finalize(h)) return -1;
+  const size_t off_pos = 64, off_pred = off_pos + ((size_t)h->N * 4 + 63) / 64 * 64;
+  const size_t off_tiles = off_pred + ((size_t)h->N * 4 + 63) / 64 * 64;
+  char* hs = (char*)h->h_stage;
+  std::vector<int4> tiles;
+  const int nv = pack_cycle(seq_lens, nseq, n, (int32_t*)(hs + off_pos), (int32_t*)(hs + off_pred),
+                            &tiles);
+  if (nv < 0) return fail(h, "dsb_step: seq_lens must be non-negative and sum to n");
+  if ((int)tiles.size() > h->max_tiles) return fail(h, "dsb_step: too many attention tiles");
+  memcpy(hs + off_tiles, tiles.data(), tiles.size() * sizeof(int4));
+  StepHdr hdr{};
+  hdr.n = n;
+  hdr.ntiles = (int)tiles.size();
+  hdr.n_valid = nv;
+  hdr.inv_nvalid = nv > 0 ? 1.f / (float)nv : 0.f;
+  hdr.hyper.lr = lr;
+  hdr.hyper.beta1 = h->d.beta1;
+  hdr.hyper.beta2 = h->d.beta2;
+  hdr.hyper.eps = h->d.adam_eps;
+  hdr.hyper.wd = h->d.weight_decay;
+  hdr.hyper.bc1 = (float)(1.0 - pow((double)h->d.beta1, (double)step));
+  hdr.hyper.bc2 = (float)(1.0 - pow((double)h->d.beta2, (double)step));
+  hdr.hyper.max_norm = h->d.max_grad_norm;
+  memcpy(hs, &hdr, sizeof(hdr));
+  h->step_lens.assign(seq_lens, seq_lens + nseq);
+  h->step_nseq = nseq;
+  CK(hipEventRecord(h->ev_in, cs));
+  CK(hipStreamWaitEvent(h->hs, h->ev_in, 0));
+  CK(hipMemcpyAsync(h->d_stage, h->h_stage, h->stage_bytes, hipMemcpyHostToDevice, h->hs));
+  CK(hipEventRecord(h->ev_t0, h->hs));
+  return 0;
+}
+
+// Copies the 64-byte result header back, orders the caller's stream after
+// the cycle, waits for it and reports loss / n_valid / timing.
+int step_finish(dsb_handle* h, hipStream_t cs, bool used_graph, float* loss, int* n_valid,
+                dsb_cycle_info* info) {
+  CK(hipEventRecord(h->ev_t1, h->hs));
+  CK(hipMemcpyAsync(h->h_stage, h->d_stage, sizeof(StepHdr), hipMemcpyDeviceToHost, h->hs));
+  CK(hipEventRecord(h->ev_out, h->hs));
+  CK(hipStreamWaitEvent(cs, h->ev_out, 0));
+  CK(hipEventSynchronize(h->ev_out));
+  StepHdr back;
+  memcpy(&back, h->h_stage, sizeof(back));
+  if (h->ktiming) {
+    double S = 0;
+    for (int i = 0; i < h->step_nseq; ++i)
+      S += (double)h->step_lens[i] * (h->step_lens[i] + 1);
+    const int n = back.n;
+    for (size_t i = 0; i < h->kcount && i < h->krec.size(); ++i) {
+      const KRec& rr = h->krec[i];
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, rr.e0, rr.e1) != hipSuccess) continue;
+      KClass& c = h->kcls[rr.cls];
+      c.calls += 1;
+      c.ms += ms;
+      c.flops += rr.fa * n + rr.fb * S + rr.fc;
+      c.bytes += rr.ba * n + rr.bb * S + rr.bc;
+    }
+  }
+  if (back.err & 1) return fail(h, "dsb_step: a target token id is outside [0, vocab)");
+  if (loss) *loss = back.loss;
+  if (n_valid) *n_valid = back.n_valid;
+  if (info) {
+    float ms = 0.f;
+    CK(hipEventElapsedTime(&ms, h->ev_t0, h->ev_t1));
+    info->gpu_ms = ms;
+    info->graph = used_graph ? 1 : 0;
+    info->n_valid = back.n_valid;
+  }
+  return 0;
+}
+
+// Captures the kernel sequence `fn` issues on the library stream into an
+// executable graph; returns 0 and sets *out, or marks capture as failed.
+template <class F>
+int capture(dsb_handle* h, F&& fn, hipGraph_t* g_out, hipGraphExec_t* x_out) {
+  hipError_t e = hipStreamBeginCapture(h->hs, hipStreamCaptureModeThreadLocal);
+  if (e == hipSuccess) {
+    const int rc = fn();
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(h->hs, &g);
+    if (rc != 0) {
+      if (g) (void)hipGraphDestroy(g);
+      return -1;
+    }
+    if (e == hipSuccess) {
+      e = hipGraphInstantiate(x_out, g, nullptr, nullptr, 0);
+      *g_out = g;
+    }
+  }
+  if (e != hipSuccess) {
+    h->graph_failed = true;
+    (void)hipGetLastError();
+    fprintf(stderr, "[dsb] hipGraph capture failed (%s); running the cycle eagerly\n",
+            hipGetErrorString(e));
+  }
   return 0;
 }
 
@@ -901,8 +1105,10 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
 void dsb_destroy(dsb_handle* h) {
   if (!h) return;
   if (h->hs) (void)hipStreamSynchronize(h->hs);
-  if (h->gexec) (void)hipGraphExecDestroy(h->gexec);
-  if (h->graph) (void)hipGraphDestroy(h->graph);
+  drop_graphs(h);
+  for (hipEvent_t e : h->ring) (void)hipEventDestroy(e);
+  if (h->d_pub_jobs) (void)hipFree(h->d_pub_jobs);
+  if (h->d_pub_chunks) (void)hipFree(h->d_pub_chunks);
   for (KRec& r : h->krec) {
     (void)hipEventDestroy(r.e0);
     (void)hipEventDestroy(r.e1);
@@ -992,15 +1198,8 @@ int dsb_bind_activations(dsb_handle* h, const dsb_activations* a) {
   h->final_in = (const bf16*)a->final_in;
   h->ids = a->input_ids;
   h->act_ld = a->ld;
-  // Rebinding activations after capture changes baked pointers: drop the graph.
-  if (h->gexec) {
-    (void)hipGraphExecDestroy(h->gexec);
-    h->gexec = nullptr;
-  }
-  if (h->graph) {
-    (void)hipGraphDestroy(h->graph);
-    h->graph = nullptr;
-  }
+  // Rebinding activations after capture changes baked pointers: drop the graphs.
+  drop_graphs(h);
   return 0;
 }
 
@@ -1069,103 +1268,121 @@ int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, 
              void* stream, float* loss, int* n_valid, dsb_cycle_info* info) {
   if (!h) return fail(nullptr, "dsb_step: null handle");
   std::lock_guard<std::mutex> lk(h->mu);
-  h->err.clear();
-  if (n <= 0 || n > h->N) return fail(h, "dsb_step: n must be in [1, s_max]");
-  if (nseq <= 0 || nseq > h->d.max_seqs) return fail(h, "dsb_step: nseq out of range");
-  if (step < 1) return fail(h, "dsb_step: step must be >= 1");
-  if (finalize(h)) return -1;
-  const size_t off_pos = 64, off_pred = off_pos + ((size_t)h->N * 4 + 63) / 64 * 64;
-  const size_t off_tiles = off_pred + ((size_t)h->N * 4 + 63) / 64 * 64;
-  char* hs = (char*)h->h_stage;
-  std::vector<int4> tiles;
-  const int nv = pack_cycle(seq_lens, nseq, n, (int32_t*)(hs + off_pos), (int32_t*)(hs + off_pred),
-                            &tiles);
-  if (nv < 0) return fail(h, "dsb_step: seq_lens must be non-negative and sum to n");
-  if ((int)tiles.size() > h->max_tiles) return fail(h, "dsb_step: too many attention tiles");
-  memcpy(hs + off_tiles, tiles.data(), tiles.size() * sizeof(int4));
-  StepHdr hdr{};
-  hdr.n = n;
-  hdr.ntiles = (int)tiles.size();
-  hdr.n_valid = nv;
-  hdr.inv_nvalid = nv > 0 ? 1.f / (float)nv : 0.f;
-  hdr.hyper.lr = lr;
-  hdr.hyper.beta1 = h->d.beta1;
-  hdr.hyper.beta2 = h->d.beta2;
-  hdr.hyper.eps = h->d.adam_eps;
-  hdr.hyper.wd = h->d.weight_decay;
-  hdr.hyper.bc1 = (float)(1.0 - pow((double)h->d.beta1, (double)step));
-  hdr.hyper.bc2 = (float)(1.0 - pow((double)h->d.beta2, (double)step));
-  hdr.hyper.max_norm = h->d.max_grad_norm;
-  memcpy(hs, &hdr, sizeof(hdr));
+  if (h->in_step) return fail(h, "dsb_step: a segmented cycle is in progress");
   hipStream_t cs = (hipStream_t)stream;
-  CK(hipEventRecord(h->ev_in, cs));
-  CK(hipStreamWaitEvent(h->hs, h->ev_in, 0));
-  CK(hipMemcpyAsync(h->d_stage, h->h_stage, h->stage_bytes, hipMemcpyHostToDevice, h->hs));
-  CK(hipEventRecord(h->ev_t0, h->hs));
+  CKR(step_prepare(h, seq_lens, nseq, n, lr, step, cs));
   bool used_graph = false;
   // Kernel timing needs an elapsed time per kernel: HIP reports none for
   // event pairs recorded inside a captured graph, so timed cycles replay the
   // same kernel sequence eagerly on the same stream.
   if ((h->d.flags & DSB_FLAG_GRAPH) && !h->graph_failed && !h->ktiming) {
-    if (!h->gexec) {
-      hipError_t e = hipStreamBeginCapture(h->hs, hipStreamCaptureModeThreadLocal);
-      if (e == hipSuccess) {
-        const int rc = enqueue(h, h->hs);
-        hipGraph_t g = nullptr;
-        e = hipStreamEndCapture(h->hs, &g);
-        if (rc != 0) {
-          if (g) (void)hipGraphDestroy(g);
-          return -1;
-        }
-        if (e == hipSuccess) {
-          e = hipGraphInstantiate(&h->gexec, g, nullptr, nullptr, 0);
-          h->graph = g;
-        }
-      }
-      if (e != hipSuccess) {
-        h->graph_failed = true;
-        (void)hipGetLastError();
-        fprintf(stderr, "[dsb] hipGraph capture failed (%s); running the cycle eagerly\n",
-                hipGetErrorString(e));
-      }
-    }
+    if (!h->gexec) CKR(capture(h, [&] { return enqueue(h, h->hs); }, &h->graph, &h->gexec));
     if (h->gexec) {
       CK(hipGraphLaunch(h->gexec, h->hs));
       used_graph = true;
     }
   }
   if (!used_graph && enqueue(h, h->hs)) return -1;
-  CK(hipEventRecord(h->ev_t1, h->hs));
-  CK(hipMemcpyAsync(h->h_stage, h->d_stage, sizeof(StepHdr), hipMemcpyDeviceToHost, h->hs));
+  return step_finish(h, cs, used_graph, loss, n_valid, info);
+}
+
+int dsb_num_segments(const dsb_handle* h) {
+  if (!h) return fail(nullptr, "dsb_num_segments: null handle");
+  return num_segments(h);
+}
+
+int dsb_step_begin(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr,
+                   int64_t step, void* stream) {
+  if (!h) return fail(nullptr, "dsb_step_begin: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (h->in_step) return fail(h, "dsb_step_begin: a segmented cycle is already in progress");
+  CKR(step_prepare(h, seq_lens, nseq, n, lr, step, (hipStream_t)stream));
+  h->in_step = true;
+  h->seg_next = 0;
+  return 0;
+}
+
+int dsb_step_segment(dsb_handle* h, int seg, int run_ahead) {
+  if (!h) return fail(nullptr, "dsb_step_segment: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (!h->in_step) return fail(h, "dsb_step_segment: no cycle begun (dsb_step_begin)");
+  if (seg != h->seg_next) return fail(h, "dsb_step_segment: segments must run in order");
+  if (run_ahead < 0 || run_ahead > 64) return fail(h, "dsb_step_segment: run_ahead must be in [0, 64]");
+  const int ns = num_segments(h);
+  if ((int)h->seg_exec.size() != ns) {
+    h->seg_exec.assign(ns, nullptr);
+    h->seg_graph.assign(ns, nullptr);
+  }
+  bool launched = false;
+  if ((h->d.flags & DSB_FLAG_GRAPH) && !h->graph_failed && !h->ktiming) {
+    if (!h->seg_exec[seg])
+      CKR(capture(h, [&] { return enqueue_segment(h, seg, h->hs); }, &h->seg_graph[seg],
+                  &h->seg_exec[seg]));
+    if (h->seg_exec[seg]) {
+      CK(hipGraphLaunch(h->seg_exec[seg], h->hs));
+      launched = true;
+    }
+  }
+  if (!launched && enqueue_segment(h, seg, h->hs)) return -1;
+  h->seg_next = seg + 1;
+  // Run-ahead bound (base.py:155-183): record this boundary and wait for the
+  // one recorded run_ahead boundaries ago, so the host stays at most
+  // run_ahead segments ahead of the GPU.
+  if (run_ahead > 0) {
+    if ((int)h->ring.size() != run_ahead + 1) {
+      for (hipEvent_t e : h->ring) (void)hipEventDestroy(e);
+      h->ring.assign(run_ahead + 1, nullptr);
+      for (auto& e : h->ring) CK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    const int R = run_ahead + 1;
+    CK(hipEventRecord(h->ring[seg % R], h->hs));
+    if (seg >= run_ahead) CK(hipEventSynchronize(h->ring[(seg - run_ahead) % R]));
+  }
+  return 0;
+}
+
+int dsb_step_end(dsb_handle* h, void* stream, float* loss, int* n_valid, dsb_cycle_info* info) {
+  if (!h) return fail(nullptr, "dsb_step_end: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (!h->in_step) return fail(h, "dsb_step_end: no cycle begun");
+  h->in_step = false;
+  if (h->seg_next != num_segments(h))
+    return fail(h, "dsb_step_end: not every segment ran; the cycle's results are incomplete");
+  const bool graph = !h->seg_exec.empty() && h->seg_exec[0] != nullptr;
+  return step_finish(h, (hipStream_t)stream, graph, loss, n_valid, info);
+}
+
+int dsb_bind_served(dsb_handle* h, int layer, int proj, void* a_slot, int64_t lda, void* b_slot,
+                    int64_t ldb) {
+  if (!h) return fail(nullptr, "dsb_bind_served: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (layer < 0 || layer >= h->L || proj < 0 || proj >= DSB_NUM_PROJ)
+    return fail(h, "dsb_bind_served: layer/proj out of range");
+  if (h->in_step) return fail(h, "dsb_bind_served: a segmented cycle is in progress");
+  if (!h->layers[layer].has[proj]) return fail(h, "dsb_bind_served: projection has no LoRA bound");
+  const int D = h->D, q = h->q, r = h->r, I = h->I;
+  const int ins[7] = {D, D, D, q, D, D, I};
+  if ((a_slot == nullptr) != (b_slot == nullptr))
+    return fail(h, "dsb_bind_served: bind both slots or neither");
+  if (a_slot && (lda < ins[proj] || ldb < r))
+    return fail(h, "dsb_bind_served: slot row stride smaller than the row");
+  if ((int)h->served.size() != h->L) h->served.assign(h->L, {});
+  h->served[layer][proj] = dsb_handle::Served{a_slot, (long)lda, b_slot, (long)ldb};
+  return rebuild_publish(h);
+}
+
+int dsb_publish(dsb_handle* h, void* stream) {
+  if (!h) return fail(nullptr, "dsb_publish: null handle");
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (h->in_step) return fail(h, "dsb_publish: a segmented cycle is in progress");
+  if (h->npub_chunks <= 0) return 0;
+  hipStream_t cs = (hipStream_t)stream;
+  CK(hipEventRecord(h->ev_in, cs));
+  CK(hipStreamWaitEvent(h->hs, h->ev_in, 0));
+  LK(lora_cast(h->d_pub_jobs, h->d_pub_chunks, h->npub_chunks, h->hs));
   CK(hipEventRecord(h->ev_out, h->hs));
   CK(hipStreamWaitEvent(cs, h->ev_out, 0));
   CK(hipEventSynchronize(h->ev_out));
-  StepHdr back;
-  memcpy(&back, hs, sizeof(back));
-  if (h->ktiming) {
-    double S = 0;
-    for (int i = 0; i < nseq; ++i) S += (double)seq_lens[i] * (seq_lens[i] + 1);
-    for (size_t i = 0; i < h->kcount && i < h->krec.size(); ++i) {
-      const KRec& rr = h->krec[i];
-      float ms = 0.f;
-      if (hipEventElapsedTime(&ms, rr.e0, rr.e1) != hipSuccess) continue;
-      KClass& c = h->kcls[rr.cls];
-      c.calls += 1;
-      c.ms += ms;
-      c.flops += rr.fa * n + rr.fb * S + rr.fc;
-      c.bytes += rr.ba * n + rr.bb * S + rr.bc;
-    }
-  }
-  if (back.err & 1) return fail(h, "dsb_step: a target token id is outside [0, vocab)");
-  if (loss) *loss = back.loss;
-  if (n_valid) *n_valid = nv;
-  if (info) {
-    float ms = 0.f;
-    CK(hipEventElapsedTime(&ms, h->ev_t0, h->ev_t1));
-    info->gpu_ms = ms;
-    info->graph = used_graph ? 1 : 0;
-    info->n_valid = nv;
-  }
   return 0;
 }
 

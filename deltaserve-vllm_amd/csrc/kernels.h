@@ -63,6 +63,7 @@ struct CastJob {
   int ld_src, ld_dst;
   int transpose;    // dst[c, r] = src[r, c]
   float scale;
+  float clamp;      // > 0: clamp the scaled value to [-clamp, clamp] before the cast
 };
 hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunks,
                      hipStream_t s);

@@ -32,7 +32,9 @@ __global__ __launch_bounds__(256) void lora_cast_kernel(const CastJob* __restric
     const long idx = (long)ck.y + threadIdx.x + e * 256;
     if (idx >= tot) break;
     const int r = (int)(idx / j.cols), c = (int)(idx % j.cols);
-    const float v = j.src[(long)r * j.ld_src + c] * j.scale;
+    float v = j.src[(long)r * j.ld_src + c] * j.scale;
+    // clamp like torch.clamp: NaN stays NaN (comparisons with NaN are false)
+    if (j.clamp > 0.f) v = v > j.clamp ? j.clamp : (v < -j.clamp ? -j.clamp : v);
     const long d = j.transpose ? (long)c * j.ld_dst + r : (long)r * j.ld_dst + c;
     j.dst[d] = (bf16)v;
   }

@@ -71,6 +71,14 @@ _SIGS = {
     "dsb_step": (c_int, [c_void_p, POINTER(c_int32), c_int, c_int, c_float, c_int64,
                          c_void_p, POINTER(c_float), POINTER(c_int),
                          POINTER(DsbCycleInfo)]),
+    "dsb_num_segments": (c_int, [c_void_p]),
+    "dsb_step_begin": (c_int, [c_void_p, POINTER(c_int32), c_int, c_int, c_float, c_int64,
+                               c_void_p]),
+    "dsb_step_segment": (c_int, [c_void_p, c_int, c_int]),
+    "dsb_step_end": (c_int, [c_void_p, c_void_p, POINTER(c_float), POINTER(c_int),
+                             POINTER(DsbCycleInfo)]),
+    "dsb_bind_served": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p, c_int64]),
+    "dsb_publish": (c_int, [c_void_p, c_void_p]),
     "dsb_reset_optimizer": (c_int, [c_void_p, c_float]),
     "dsb_kernel_stats": (c_int, [c_void_p, c_int, c_char_p, c_int, POINTER(c_int64),
                                  POINTER(c_double), POINTER(c_double), POINTER(c_double)]),

@@ -59,12 +59,24 @@ class BackwardService:
         self._last_loss = None
         self._last_mode = "graph"
 
-    # -- GPU-yield contract (base.py:148-208): wait while the grant is cleared.
+    # -- GPU-yield contract (base.py:148-208): at a segment boundary, block
+    # (bounded, 5 s) while the grant is cleared. The run-ahead bound of the
+    # reference's event ring is applied by libdsb between segment launches
+    # (dsb_step_segment's run_ahead, from meta backward_run_ahead_boundaries).
     def _maybe_pause(self) -> None:
         grant = self._gpu_grant
         if grant is None or grant.is_set():
             return
-        grant.wait(timeout=5.0)
+        deadline = time.monotonic() + 5.0
+        while not grant.is_set() and time.monotonic() < deadline:
+            grant.wait(timeout=0.002)
+
+    def _run_ahead(self) -> int:
+        meta = (self.shared or {}).get("meta") or {}
+        return max(0, int(meta.get("backward_run_ahead_boundaries", 0) or 0))
+
+    def _on_lora_buffers(self) -> None:  # trainer overrides
+        pass
 
     # -- pipe loop (base.py:297-408)
     def run(self, conn) -> None:
@@ -86,6 +98,7 @@ class BackwardService:
                 self._handle_share_activations(conn, msg)
             elif cmd == "share_lora_buffers":
                 self.lora_buffers = msg.get("buffers")
+                self._on_lora_buffers()
                 conn.send({"event": "lora_buffers_received"})
             elif cmd == "set_corpus_meta":
                 self._total_tokens_per_epoch = int(msg.get("total_tokens_per_epoch", 0))

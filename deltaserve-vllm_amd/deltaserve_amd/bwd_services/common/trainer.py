@@ -55,6 +55,7 @@ class LoraSftTrainerService(BackwardService):
         self._pending_epoch_save = None
         self._h = None
         self._act_key = None
+        self._served_key = None
         self._opt_step = 0
         self._keep: list = []
         self.lr = 0.0
@@ -245,24 +246,60 @@ class LoraSftTrainerService(BackwardService):
         if n > self._s_max:
             raise ValueError(f"n={n} exceeds the backward capacity s_max={self._s_max}")
         self._bind_activations(activations)
+        self._bind_served_buffers()
         self._opt_step += 1
         loss = c_float(0.0)
         nv = c_int(0)
         info = L.DsbCycleInfo()
         stream = c_void_p(torch.cuda.current_stream().cuda_stream)
-        rc = L.load().dsb_step(self._h, L.i32_array(seq_lens), len(seq_lens), n, float(self.lr),
-                               int(self._opt_step), stream, byref(loss), byref(nv), byref(info))
+        lib = L.load()
+        if self._use_segments():
+            rc = self._run_segmented(lib, seq_lens, n, stream, loss, nv, info)
+            what = "segmented cycle"
+        else:
+            rc = lib.dsb_step(self._h, L.i32_array(seq_lens), len(seq_lens), n, float(self.lr),
+                              int(self._opt_step), stream, byref(loss), byref(nv), byref(info))
+            what = "dsb_step"
         if rc != 0:
             self._opt_step -= 1
-            L.check(rc, self._h, "dsb_step")
+            L.check(rc, self._h, what)
         self.last_cycle_info = {"gpu_ms": info.gpu_ms, "graph": bool(info.graph),
                                 "n_valid": info.n_valid}
-        self._last_mode = "graph" if info.graph else "eager"
+        self._last_mode = ("graph" if info.graph else "eager") + (
+            "/segments" if what != "dsb_step" else "")
         if epoch > self.current_epoch:
             self.lr *= self.gamma  # StepLR(step_size=1, gamma) stepped per epoch advance
             self.current_epoch = epoch
-        self._publish_to_served()
+        # the served LoRA slots were written inside the cycle, after AdamW
         return float(loss.value), int(nv.value)
+
+    def _use_segments(self) -> bool:
+        """Pause points (one graph per segment) when a GPU grant is wired in
+        (co-located with serving) or meta asks for them; otherwise the whole
+        cycle is one graph."""
+        meta = self.shared.get("meta") or {}
+        if meta.get("backward_single_graph"):
+            return False
+        return self._gpu_grant is not None or bool(meta.get("backward_pause_boundaries"))
+
+    def _run_segmented(self, lib, seq_lens, n, stream, loss, nv, info) -> int:
+        """trainer.py:503-678 with _maybe_pause before the cycle (:504) and at
+        every layer boundary (:577-581): segment 0 is the LM head, 1 .. L the
+        layers from the last, L + 1 the optimizer and publish."""
+        rc = lib.dsb_step_begin(self._h, L.i32_array(seq_lens), len(seq_lens), n,
+                                float(self.lr), int(self._opt_step), stream)
+        if rc != 0:
+            return rc
+        run_ahead = self._run_ahead()
+        nseg = lib.dsb_num_segments(self._h)
+        for seg in range(nseg):
+            if seg <= self.L:
+                self._maybe_pause()
+            rc = lib.dsb_step_segment(self._h, seg, run_ahead)
+            if rc != 0:
+                break
+        rc_end = lib.dsb_step_end(self._h, stream, byref(loss), byref(nv), byref(info))
+        return rc if rc != 0 else rc_end
 
     # ------------------------------------------------------------ checkpoints
     @torch.no_grad()
@@ -399,26 +436,52 @@ class LoraSftTrainerService(BackwardService):
                f"lr={self.lr}, wd={self.weight_decay}, gamma={self.gamma}")
         return {"tensors": len(have)}
 
-    @torch.no_grad()
-    def _publish_to_served(self) -> None:
-        """trainer.py:760-802: clamp ±6.5e4, bake α/r into B, cast, copy into the
-        served slot of vLLM's stacked LoRA buffers (every trained projection)."""
-        if not self.lora_buffers:
+    def _on_lora_buffers(self) -> None:
+        self._served_key = None
+        if self._h is not None:
+            self._bind_served_buffers()
+
+    def _bind_served_buffers(self) -> None:
+        """Registers vLLM's stacked LoRA slot rows with libdsb (trainer.py:760-802:
+        a_buf[slot, 0, :r, :in] = clamp(A), b_buf[slot, 0, :out, :r] = clamp(s·B),
+        bf16) so every cycle publishes inside its graph, after AdamW."""
+        bufs = self.lora_buffers
+        if not bufs or self._h is None:
             return
-        slot = int(self.lora_buffers["slot"])
-        for i, projd in self.lora_buffers["layers"].items():
-            ld = self.lora.get(int(i), {})
+        slot = int(bufs["slot"])
+        key = (slot, tuple((int(i), p, buf["a"].data_ptr(), buf["b"].data_ptr())
+                           for i, projd in sorted(bufs["layers"].items(), key=lambda kv: int(kv[0]))
+                           for p, buf in sorted(projd.items())))
+        if key == self._served_key:
+            return
+        lib = L.load()
+        for i, projd in bufs["layers"].items():
+            i = int(i)
             for proj, buf in projd.items():
-                pa = ld.get(proj, {}).get("A")
-                pb = ld.get(proj, {}).get("B")
-                if pa is None:
+                if proj not in self.lora.get(i, {}):
                     continue
-                a_buf, b_buf = buf["a"], buf["b"]
-                r, in_dim = pa.shape
-                out_dim = pb.shape[0]
-                a_buf[slot, 0, :r, :in_dim].copy_(pa.clamp(-6.5e4, 6.5e4).to(a_buf.dtype))
-                b_buf[slot, 0, :out_dim, :r].copy_(
-                    (pb * self.scaling).clamp(-6.5e4, 6.5e4).to(b_buf.dtype))
+                a, b = buf["a"][slot, 0], buf["b"][slot, 0]
+                for t in (a, b):
+                    if t.dtype != torch.bfloat16 or not t.is_cuda or t.stride(1) != 1:
+                        raise TypeError("served LoRA buffers must be bf16 CUDA tensors with "
+                                        "contiguous rows")
+                pa, pb = self.lora[i][proj]["A"], self.lora[i][proj]["B"]
+                if a.shape[0] < pa.shape[0] or a.shape[1] < pa.shape[1] or \
+                        b.shape[0] < pb.shape[0] or b.shape[1] < pb.shape[1]:
+                    raise ValueError(f"served slot of layer {i} {proj} is smaller than the adapter")
+                L.check(lib.dsb_bind_served(self._h, i, L.PROJ_INDEX[proj], a.data_ptr(),
+                                            a.stride(0), b.data_ptr(), b.stride(0)),
+                        self._h, "dsb_bind_served")
+        self._served_key = key
+
+    def _publish_to_served(self) -> None:
+        """Publishes the current masters into the served slots now, outside a
+        cycle (the switch_adapter path; cycles publish inside their graph)."""
+        if not self.lora_buffers or self._h is None:
+            return
+        self._bind_served_buffers()
+        stream = c_void_p(torch.cuda.current_stream().cuda_stream)
+        L.check(L.load().dsb_publish(self._h, stream), self._h, "dsb_publish")
 
     def kernel_stats(self) -> list[dict]:
         """Per-kernel-class timing (meta ``backward_kernel_timing``): calls,

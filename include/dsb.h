@@ -111,13 +111,44 @@ int dsb_bind_lora(dsb_handle* h, int layer, int proj, const dsb_lora_tensors* t)
 /* Binds the shared activation buffers (base.py:438-461 share_activations). */
 int dsb_bind_activations(dsb_handle* h, const dsb_activations* a);
 
-/* One backward cycle + AdamW step: trainer.py:503-678 without the publish.
+/* One backward cycle + AdamW step (+ the served-slot publish when slots are
+ * bound, dsb_bind_served): trainer.py:503-678.
  * seq_lens: host int32[nseq] in request order, summing to n <= s_max.
  * lr: this cycle's learning rate; step: the optimizer step count t >= 1.
  * stream: the caller's hipStream_t (work is ordered after it and it waits
  * for the cycle). Writes the mean loss and the number of predicting rows. */
 int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, int64_t step,
              void* stream, float* loss, int* n_valid, dsb_cycle_info* info);
+
+/* The same cycle in segments, for the GPU-yield contract of the reference's
+ * BackwardService._maybe_pause (bwd_services/base.py:148-208), which the
+ * reference calls at every layer boundary (llama3.py:342-344): segment 0 is
+ * the LM head, segments 1 .. L the decoder layers from the last to the
+ * first, segment L + 1 the clip, AdamW and publish. dsb_step_begin stages the
+ * cycle (like dsb_step's first half); dsb_step_segment launches segment `seg`
+ * (in order, each its own captured graph) and, when run_ahead > 0, keeps the
+ * host at most run_ahead segments ahead of the GPU: the reference's
+ * backward_run_ahead_boundaries event ring (base.py:155-183). dsb_step_end
+ * waits for the cycle and reports like dsb_step. The caller's pause check
+ * runs between dsb_step_segment calls, outside any captured region. Results
+ * equal dsb_step's bit for bit (same kernels, same order). */
+int dsb_num_segments(const dsb_handle* h);
+int dsb_step_begin(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr,
+                   int64_t step, void* stream);
+int dsb_step_segment(dsb_handle* h, int seg, int run_ahead);
+int dsb_step_end(dsb_handle* h, void* stream, float* loss, int* n_valid, dsb_cycle_info* info);
+
+/* Served-slot publish, replacing LoraSftTrainerService._publish_to_served
+ * (trainer.py:760-802): binds the bf16 rows of vLLM's stacked LoRA buffers
+ * for one projection, a_slot = lora_a_stacked[slot, 0] ([r, in], row stride
+ * lda) and b_slot = lora_b_stacked[slot, 0] ([out, r], row stride ldb).
+ * Every cycle then ends by writing clamp(A, ±6.5e4) and clamp(s·B, ±6.5e4),
+ * cast to bf16, into every bound slot, inside its graph after AdamW. NULL
+ * slots unbind. dsb_publish writes them once outside a cycle (the
+ * switch_adapter path, trainer.py:721-724). */
+int dsb_bind_served(dsb_handle* h, int layer, int proj, void* a_slot, int64_t lda, void* b_slot,
+                    int64_t ldb);
+int dsb_publish(dsb_handle* h, void* stream);
 
 /* Per-kernel-class timing. While enabled (DSB_FLAG_KTIMING at create, or
  * dsb_set_kernel_timing), each cycle replays the captured kernel sequence
