@@ -1397,6 +1397,41 @@ int dsb_publish(dsb_handle* h, void* stream) {
     }                                                                                \
   } while (0)
 
+// ------------------------------------------------------------ capture
+
+int dsb_capture_index(const int64_t* positions, int num_ft, int offset, int max_saved,
+                      int64_t* src, int64_t* dst) {
+  if (max_saved <= 0 || offset < 0 || num_ft < 0 || !src || !dst || (num_ft > 0 && !positions))
+    return fail(nullptr, "dsb_capture_index: bad arguments");
+  const int n = std::max(0, std::min(num_ft, max_saved - offset));
+  for (int i = 0; i < max_saved; ++i) {
+    src[i] = i < n ? positions[i] : 0;
+    dst[i] = i < n ? (int64_t)offset + i : (int64_t)max_saved;
+  }
+  return n;
+}
+
+int dsb_save_rows(const void* x, int64_t ldx, const void* r, int64_t ldr, int64_t x_rows,
+                  int x_dtype, const int64_t* src, const int64_t* dst, int count, int width,
+                  void* buf, int64_t ldbuf, int64_t buf_rows, void* stream) {
+  if (!x || !src || !dst || !buf || count < 0 || width <= 0 || ldx < width || ldbuf < width ||
+      (r && ldr < width) || buf_rows < 1 || x_rows < 0)
+    return fail(nullptr, "dsb_save_rows: bad arguments");
+  if (x_dtype != DSB_DT_BF16 && x_dtype != DSB_DT_F16 && x_dtype != DSB_DT_F32)
+    return fail(nullptr, "dsb_save_rows: x_dtype must be DSB_DT_BF16, DSB_DT_F16 or DSB_DT_F32");
+  OPCK(save_rows(x, ldx, r, ldr, x_rows, x_dtype, src, dst, count, width, (bf16*)buf, ldbuf, buf_rows,
+                 (hipStream_t)stream));
+  return 0;
+}
+
+int dsb_save_ids(const int64_t* ids, int64_t ids_len, const int64_t* src, const int64_t* dst,
+                 int count, int64_t* out, int64_t out_len, void* stream) {
+  if (!ids || !src || !dst || !out || count < 0 || out_len < 0 || ids_len < 0)
+    return fail(nullptr, "dsb_save_ids: bad arguments");
+  OPCK(save_ids(ids, ids_len, src, dst, count, out, out_len, (hipStream_t)stream));
+  return 0;
+}
+
 int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
                 int64_t lda2, const void* B2, int64_t ldb2, int M, int N, int K1, int K2, void* C,
                 int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr, int cfg,

@@ -1,6 +1,7 @@
 // Internal launch API of the backward's HIP kernels (not part of the C-ABI).
 #pragma once
 
+#include "../../include/dsb.h"
 #include "dsb_common.h"
 
 namespace dsb {
@@ -132,6 +133,13 @@ struct OptHyper {
 hipError_t clip_adamw(const OptTensor* tensors_dev, const int2* chunks_dev, int nchunks,
                       const int2* layer_chunks_dev, int nlayers, float* partial,
                       float* sq_layer, const OptHyper* hyper_dev, int do_clip, hipStream_t s);
+
+// ---- capture.hip (forward-side save into the activation store)
+hipError_t save_rows(const void* x, long ldx, const void* r, long ldr, long x_rows, int dtype,
+                     const int64_t* src, const int64_t* dst, int count, int width, bf16* buf,
+                     long ldbuf, long buf_rows, hipStream_t s);
+hipError_t save_ids(const int64_t* ids, long ids_len, const int64_t* src, const int64_t* dst, int count,
+                    int64_t* out, long out_len, hipStream_t s);
 
 // ---- misc (dsb_api.hip)
 hipError_t build_labels(const int64_t* ids, const int* pred_flag, int* labels, int n,

@@ -22,6 +22,7 @@ ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
 PROJ_INDEX = {p: i for i, p in enumerate(PROJS)}
 FLAG_GRAPH, FLAG_NO_CLIP, FLAG_KTIMING = 1, 2, 4
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 
 
 class DsbDesc(Structure):
@@ -79,6 +80,11 @@ _SIGS = {
                              POINTER(DsbCycleInfo)]),
     "dsb_bind_served": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p, c_int64]),
     "dsb_publish": (c_int, [c_void_p, c_void_p]),
+    "dsb_capture_index": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "dsb_save_rows": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int, c_void_p,
+                              c_void_p, c_int, c_int, c_void_p, c_int64, c_int64, c_void_p]),
+    "dsb_save_ids": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_void_p, c_int64,
+                             c_void_p]),
     "dsb_reset_optimizer": (c_int, [c_void_p, c_float]),
     "dsb_kernel_stats": (c_int, [c_void_p, c_int, c_char_p, c_int, POINTER(c_int64),
                                  POINTER(c_double), POINTER(c_double), POINTER(c_double)]),

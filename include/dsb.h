@@ -30,6 +30,8 @@ enum {
   DSB_PROJ_Q = 0, DSB_PROJ_K = 1, DSB_PROJ_V = 2, DSB_PROJ_O = 3,
   DSB_PROJ_GATE = 4, DSB_PROJ_UP = 5, DSB_PROJ_DOWN = 6, DSB_NUM_PROJ = 7
 };
+/* element types of the capture entry points */
+enum { DSB_DT_BF16 = 0, DSB_DT_F16 = 1, DSB_DT_F32 = 2 };
 /* dsb_desc.flags */
 enum { DSB_FLAG_GRAPH = 1u, DSB_FLAG_NO_CLIP = 2u, DSB_FLAG_KTIMING = 4u };
 
@@ -175,6 +177,36 @@ int dsb_pack(const int32_t* seq_lens, int nseq, int n, int32_t* positions, int32
 /* RoPE inverse frequencies [head_dim/2] (ops.py:26-57), host only. */
 int dsb_rope_inv_freq(int head_dim, float theta, int rope_type, float factor, float low,
                       float high, float orig_max, float* out);
+
+/* ---- the forward-side capture (the serving worker's half of the handoff) ----
+ *
+ * dsb_capture_index replaces ActivationAccumulator.arm_op_step
+ * (accumulate.py:324-343), host only: for a step whose finetuning rows sit at
+ * `positions` [num_ft] of the flat batch, fills the fixed-length index pair
+ * src/dst [max_saved] (n = min(num_ft, max_saved - offset) rows: src[i] =
+ * positions[i], dst[i] = offset + i; the rest src 0, dst max_saved, the
+ * scratch row). Returns n, or -1 on bad arguments.
+ *
+ * dsb_save_rows replaces the save op torch.ops.vllm.dserve_save_rows
+ * (ft_save_op.py:72-93): buf[dst[i]] = bf16(x[src[i]] (+ r[src[i]], added in
+ * x's dtype)) for i < count, x/r of element type x_dtype (DSB_DT_*), rows of
+ * `width` elements; buf is a bf16 store [buf_rows = max_saved + 1, ldbuf].
+ * Slots pointing at the scratch row (dst == buf_rows - 1), and slots whose
+ * src lies outside x's x_rows rows (where the reference's index_select would
+ * raise a device-side assert), are skipped. Only
+ * enqueues on `stream` (no host synchronisation), so it can be captured in a
+ * graph and replayed with refreshed device indices.
+ *
+ * dsb_save_ids: the final save point's token ids (accumulate.py:598-622):
+ * out[dst[i]] = ids[src[i]] for dst[i] < out_len and src[i] < ids_len;
+ * stream-ordered likewise. */
+int dsb_capture_index(const int64_t* positions, int num_ft, int offset, int max_saved,
+                      int64_t* src, int64_t* dst);
+int dsb_save_rows(const void* x, int64_t ldx, const void* r, int64_t ldr, int64_t x_rows,
+                  int x_dtype, const int64_t* src, const int64_t* dst, int count, int width,
+                  void* buf, int64_t ldbuf, int64_t buf_rows, void* stream);
+int dsb_save_ids(const int64_t* ids, int64_t ids_len, const int64_t* src, const int64_t* dst,
+                 int count, int64_t* out, int64_t out_len, void* stream);
 
 /* ---- single-op entry points (parity tests; synchronous on `stream`) ---- */
 

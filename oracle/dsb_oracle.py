@@ -56,6 +56,36 @@ def pack(seq_lens):
 
 
 # --------------------------------------------------------------------------- #
+# Forward-side capture (accumulate.py:325-343, ft_save_op.py:72-89)
+# --------------------------------------------------------------------------- #
+
+def capture_index(positions, num_ft: int, offset: int, max_saved: int):
+    """``arm_op_step``'s index pair (accumulate.py:332-340): the first
+    n = min(num_ft, max_saved - offset) slots gather ``positions[:n]`` into
+    buffer rows offset..offset+n-1; the rest gather row 0 into the scratch row
+    ``max_saved``. Returns (src, dst) int64 [max_saved] and max(n, 0)."""
+    n = min(int(num_ft), max_saved - int(offset))
+    src = torch.zeros(max_saved, dtype=torch.int64)
+    dst = torch.full((max_saved,), max_saved, dtype=torch.int64)
+    if n > 0:
+        src[:n] = torch.as_tensor(list(positions)[:n], dtype=torch.int64)
+        dst[:n] = torch.arange(offset, offset + n, dtype=torch.int64)
+    return src, dst, max(n, 0)
+
+
+def save_rows_(x, r, buf, src, dst):
+    """The save op on CPU tensors (ft_save_op.py:84-89): rows of ``x`` (+ ``r``,
+    added in x's dtype) at ``src``, cast to the buffer's dtype, copied into
+    ``buf`` at ``dst``. In place; the scratch row receives whatever the
+    unused slots gather."""
+    rows = x.index_select(0, src)
+    if r is not None:
+        rows = rows + r.index_select(0, src)
+    buf.index_copy_(0, dst, rows.to(buf.dtype))
+    return buf
+
+
+# --------------------------------------------------------------------------- #
 # common/ops.py
 # --------------------------------------------------------------------------- #
 

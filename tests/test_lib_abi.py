@@ -134,3 +134,41 @@ def test_product_ops_refuse_cpu_tensors():
         ops.rmsnorm(x, torch.ones(8, dtype=torch.bfloat16), 1e-5)
     with pytest.raises(ValueError):
         ops.gemm_nt(x, x)
+
+
+@pytest.mark.parametrize("max_saved", [1, 7, 16, 257])
+def test_host_capture_index_bit_exact_vs_oracle(max_saved):
+    """dsb_capture_index (arm_op_step's index build) against the oracle, over
+    every offset / count at the buffer's edges, with interleaved positions."""
+    from deltaserve_amd import capture
+
+    g = torch.Generator().manual_seed(max_saved)
+    offsets = sorted({0, 1, max_saved // 2, max_saved - 1, max_saved, max_saved + 3})
+    counts = sorted({0, 1, max_saved // 3, max_saved - 1, max_saved, max_saved + 5})
+    for off in offsets:
+        for nft in counts:
+            pos = torch.randperm(4 * max_saved + 8, generator=g)[:nft]
+            src, dst, n = capture.capture_index(pos, nft, off, max_saved)
+            osrc, odst, on = O.capture_index(pos.tolist(), nft, off, max_saved)
+            assert n == on and torch.equal(src, osrc) and torch.equal(dst, odst), (off, nft)
+
+
+def test_capture_entry_points_reject_bad_input():
+    from deltaserve_amd import capture
+
+    L, lib = _lib()
+    with pytest.raises(ValueError):
+        capture.capture_index([1, 2], 3, 0, 8)  # fewer positions than rows
+    src = (ctypes.c_int64 * 4)()
+    assert lib.dsb_capture_index(None, 0, 0, 0, src, src) < 0  # empty buffer
+    assert lib.dsb_capture_index(None, 0, -1, 4, src, src) < 0  # negative offset
+    assert lib.dsb_capture_index(None, 2, 0, 4, src, src) < 0  # rows without positions
+    # argument checks run before any device work
+    assert lib.dsb_save_rows(None, 8, None, 0, 4, 0, src, src, 4, 8, src, 8, 5, None) < 0
+    assert lib.dsb_save_rows(src, 8, None, 0, 4, 7, src, src, 4, 8, src, 8, 5, None) < 0
+    assert lib.dsb_save_rows(src, 4, None, 0, 4, 0, src, src, 4, 8, src, 8, 5, None) < 0
+    assert lib.dsb_save_ids(None, 4, src, src, 4, src, 4, None) < 0
+    with pytest.raises(ValueError):  # host tensors: no fallback
+        x = torch.zeros(4, 8, dtype=torch.bfloat16)
+        i = torch.zeros(4, dtype=torch.int64)
+        capture.save_rows(x, None, torch.zeros(5, 8, dtype=torch.bfloat16), i, i)

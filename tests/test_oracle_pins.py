@@ -21,6 +21,11 @@ Reference behaviour each pin stands for (paths under
   head_backward     head.py:42-100
   clip_, adamw_     trainer.py:252-256, :624-636, :668 (torch AdamW / clip)
   process_backward  trainer.py:503-678 vs transformers *ForCausalLM autograd
+  capture_index     accumulate.py:325-343 (brute-force set semantics, and the
+                    cases of tests/test_ft_save_op.py:230-262)
+  save_rows_        ft_save_op.py:72-89 (per-row loop with an independent
+                    round-to-nearest-even bf16, and the expectations of
+                    tests/test_ft_save_op.py:40-90)
 """
 
 from __future__ import annotations
@@ -571,6 +576,90 @@ def test_cycle_clip_and_update_compose():
 
 
 # --------------------------------------------------------------------------- #
+# Forward-side capture
+# --------------------------------------------------------------------------- #
+
+def check_capture_index(fn, M=9):
+    """Against the set definition: the non-scratch (src, dst) pairs are exactly
+    {(positions[i], offset + i) : i < num_ft, offset + i < M}, every other
+    slot gathers row 0 into row M, and the count is the number of such i."""
+    rng = random.Random(11)
+    for offset in range(0, M + 2):
+        for num_ft in range(0, M + 2):
+            pos = [rng.randrange(0, 40) for _ in range(num_ft)]
+            src, dst, n = fn(pos, num_ft, offset, M)
+            want = {(pos[i], offset + i) for i in range(num_ft) if offset + i < M}
+            got = {(int(a), int(b)) for a, b in zip(src, dst) if int(b) != M}
+            assert got == want, (offset, num_ft)
+            assert n == len(want)
+            assert all(int(a) == 0 for a, b in zip(src, dst) if int(b) == M)
+            assert len(src) == len(dst) == M
+    # tests/test_ft_save_op.py:230 and :252 (S_MAX 16): rows 4..8, then 9..10
+    src, dst, n = fn([2, 9, 10, 17, 23], 5, 4, 16)
+    assert n == 5 and dst[:5].tolist() == [4, 5, 6, 7, 8] and src[:5].tolist() == [2, 9, 10, 17, 23]
+    src, dst, n = fn([0, 5], 2, 9, 16)
+    assert n == 2 and dst[:2].tolist() == [9, 10] and (dst[2:] == 16).all()
+
+
+def _bf16_rne(a):
+    """float32 -> bf16 round-to-nearest-even on the bit pattern (numpy)."""
+    import numpy as np
+    b = np.asarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (b & 0x7FFFFFFF) > 0x7F800000
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, (b >> 16) | 0x40, r)
+    return torch.from_numpy((r.astype(np.uint32) << 16).view(np.float32).copy())
+
+
+def check_save_rows(fn):
+    """Per row and element: buf[dst[i]] = rne_bf16(x[src[i]] + r[src[i]]) with
+    the add done in x's dtype; rows no slot names keep their contents; the
+    cases of the reference's own capture test (test_ft_save_op.py:59-75)."""
+    import numpy as np
+    g = torch.Generator().manual_seed(4)
+    M, W, T = 16, 8, 32
+    for xdt in (torch.bfloat16, torch.float16, torch.float32):
+        x = (torch.randn(T, W, generator=g) * 3).to(xdt)
+        r = (torch.randn(T, W, generator=g) * 3).to(xdt)
+        for rr in (r, None):
+            buf = torch.full((M + 1, W), 5.0, dtype=torch.bfloat16)
+            pos = [3, 7, 20, 31, 0]
+            src, dst, n = O.capture_index(pos, len(pos), 9, M)
+            fn(x, rr, buf, src, dst)
+            for i in range(M):
+                if i < 9 or i >= 9 + n:
+                    assert (buf[i] == 5.0).all(), (xdt, i)
+            for i in range(n):
+                xs = x[pos[i]].numpy() if xdt != torch.bfloat16 else x[pos[i]].float().numpy()
+                if rr is None:
+                    v = np.asarray(xs, dtype=np.float32)
+                elif xdt == torch.float32:
+                    v = xs.astype(np.float32) + r[pos[i]].numpy()
+                elif xdt == torch.float16:
+                    v = (xs.astype(np.float16) + r[pos[i]].numpy().astype(np.float16)).astype(np.float32)
+                else:  # bf16 add: exact float sum rounded once to bf16
+                    v = _bf16_rne(xs + r[pos[i]].float().numpy()).numpy()
+                assert torch.equal(buf[9 + i].float(), _bf16_rne(v)), (xdt, rr is None, i)
+    # test_ft_save_op.py:59-66: positions 3, 7, 20 -> rows 5..7, others untouched
+    x = torch.randn(32, 8, generator=g).to(torch.bfloat16)
+    r = torch.randn(32, 8, generator=g).to(torch.bfloat16)
+    buf = torch.zeros(17, 8, dtype=torch.bfloat16)
+    src = torch.tensor([3, 7, 20] + [0] * 13)
+    dst = torch.tensor([5, 6, 7] + [16] * 13)
+    fn(x, r, buf, src, dst)
+    assert torch.equal(buf[5:8], (x[[3, 7, 20]].float() + r[[3, 7, 20]].float()).to(torch.bfloat16))
+    assert buf[:5].abs().sum() == 0 and buf[8:16].abs().sum() == 0
+
+
+def test_capture_index():
+    check_capture_index(O.capture_index)
+
+
+def test_save_rows():
+    check_save_rows(O.save_rows_)
+
+
+# --------------------------------------------------------------------------- #
 # Negative controls: each check must reject a planted mistake.
 # --------------------------------------------------------------------------- #
 
@@ -617,7 +706,24 @@ def _bad_cycle(model, acts, seq_lens, n, **kw):  # per-layer gradient scaled by 
     return loss, nv, grads
 
 
+def _bad_capture_index(pos, num_ft, offset, M):  # n not clipped at the buffer end
+    src, dst, n = O.capture_index(pos, num_ft, 0, M + num_ft)
+    src, dst = src[:M], dst[:M]
+    dst = torch.where(dst < M + num_ft, dst + offset, torch.full_like(dst, M))
+    return src, dst, min(num_ft, M)
+
+
+def _bad_save_rows(x, r, buf, src, dst):  # residual added after the bf16 cast
+    rows = x.index_select(0, src).to(buf.dtype)
+    if r is not None:
+        rows = rows + r.index_select(0, src).to(buf.dtype)
+    buf.index_copy_(0, dst, rows)
+    return buf
+
+
 PLANTED = {
+    "capture_index_clip": lambda: check_capture_index(_bad_capture_index),
+    "save_rows_cast_order": lambda: check_save_rows(_bad_save_rows),
     "pack": lambda: check_pack(_bad_pack, [3, 4]),
     "rope_inv_freq": lambda: check_rope_inv_freq(_bad_inv_freq, *ROPE_CASES[3]),
     "rope_backward": lambda: check_rope_backward(_bad_rope_backward),
