@@ -4,10 +4,10 @@
 #include "gemm_nt.h"
 
 namespace dsb {
-template __global__ void gemm_nt_kernel<256, 256, 2, 2, GEMM_STAGES, EpiBF16>(GemmProblem, EpiBF16);
-template __global__ void gemm_nt_kernel<128, 128, 2, 2, GEMM_STAGES, EpiBF16>(GemmProblem, EpiBF16);
-template __global__ void gemm_nt_kernel<64, 64, 2, 2, GEMM_STAGES, EpiBF16>(GemmProblem, EpiBF16);
-template __global__ void gemm_nt_kernel<256, 256, 2, 2, GEMM_STAGES, EpiF32>(GemmProblem, EpiF32);
-template __global__ void gemm_nt_kernel<128, 128, 2, 2, GEMM_STAGES, EpiF32>(GemmProblem, EpiF32);
-template __global__ void gemm_nt_kernel<64, 64, 2, 2, GEMM_STAGES, EpiF32>(GemmProblem, EpiF32);
+template __global__ void gemm_nt_kernel<256, 256, 2, 2, EpiBF16>(GemmProblem, EpiBF16);
+template __global__ void gemm_nt_kernel<128, 128, 2, 2, EpiBF16>(GemmProblem, EpiBF16);
+template __global__ void gemm_nt_kernel<64, 64, 2, 2, EpiBF16>(GemmProblem, EpiBF16);
+template __global__ void gemm_nt_kernel<256, 256, 2, 2, EpiF32>(GemmProblem, EpiF32);
+template __global__ void gemm_nt_kernel<128, 128, 2, 2, EpiF32>(GemmProblem, EpiF32);
+template __global__ void gemm_nt_kernel<64, 64, 2, 2, EpiF32>(GemmProblem, EpiF32);
 }  // namespace dsb

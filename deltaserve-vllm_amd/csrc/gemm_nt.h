@@ -7,28 +7,26 @@
 // LoRA factor rides along as a second K segment (K-concatenation), so
 // y = x·Wᵀ + (x·Aᵀ)·(s·B)ᵀ is one kernel with K = in + r.
 //
-// Main loop. BK = 32; the K tiles stream through a ring of NS LDS stages that
-// are filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): no
-// VGPR staging and no ds_write instructions, so up to NS-2 stages are in
-// flight while the waves run MFMAs. Each wave owns a (BM/WM)×(BN/WN) sub-tile
-// of v_mfma_f32_32x32x16_bf16 accumulators. Per K step (two 16-deep slices):
-//   read slice-1 fragments → MFMAs of slice 0 → wait for the own loads of the
-//   next stage → barrier → issue the loads of stage kt+NS-1 into the slot
-//   freed by stage kt-1 → read slice-0 fragments of the next stage → MFMAs of
-//   slice 1.
-// The single barrier per step both publishes stage kt+1 (every wave's loads
-// landed) and retires stage kt-1 (every wave is past its reads), and the
-// next stage's first fragments are read under the current stage's last MFMAs.
-// One loop iteration per K step with a rotating stage slot; the ring always
-// issues one stage per step (zero-filled past K), so the vmcnt waits are
-// constants.
+// Main loop. BK = 64: each K tile is a 128-byte run of every operand row,
+// fetched by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds; 8 lanes
+// cover one row, so every request is a whole 128-byte line) into one of two
+// LDS stages. Each wave owns a (BM/WM)×(BN/WN) sub-tile of
+// v_mfma_f32_32x32x16_bf16 accumulators. Per K step (four 16-deep slices):
+//   read slices 0-1 → MFMAs of slice 0 (+ half of the next stage's loads) →
+//   read slice 2 → MFMAs of slice 1 (+ the other half) → read slice 3 →
+//   MFMAs of slices 2, 3 → wait for the own loads → barrier.
+// The one barrier per step publishes stage kt+1 (every wave's loads landed)
+// and retires stage kt (every wave's reads of it were consumed by its
+// MFMAs), so the next step can fill that slot. Loads issue one at a time
+// between MFMAs; past the end of K they zero-fill the slot without touching
+// memory, so the waits are constants.
 //
-// LDS layout per stage and operand: rows of 64 B (32 bf16) as four 16-byte
-// chunks; chunk c of row r sits in slot c ^ g(r), g(r) = ((r>>1)&3) ^ ((r>>3)&1),
+// LDS layout per stage and operand: rows of 128 B (64 bf16) as eight 16-byte
+// chunks; chunk c of row r sits in slot c ^ f(r), f(r) = ((r>>1)&7) ^ ((r&1)<<2),
 // which makes the 32-row fragment reads conflict-free for both 128-byte and
 // 256-byte bank windows. The loads write LDS linearly (lane i of a load lands
-// at byte 16·i of its 1 KB segment = 16 rows), so the swizzle is applied on
-// the global side: the lane filling slot s of row r fetches chunk s ^ g(r).
+// at byte 16·i of its 1 KB segment = 8 rows), so the swizzle is applied on
+// the global side: the lane filling slot s of row r fetches chunk s ^ f(r).
 // Out-of-range rows (past M or N) and chunks past K are fetched from an offset
 // outside the buffer descriptor and land as zeros.
 //
@@ -152,22 +150,27 @@ DSB_DEV void add8_bf16(float* v, const bf16* r, int lim) {
   }
 }
 
-DSB_DEV int lds_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+// Slot of 16-byte chunk c of LDS row r (rows of 128 B = 8 chunks): c ^ f(r).
+// Any 8 consecutive rows (one 128-byte bank window per row) and any 16
+// consecutive rows (256-byte windows, rows r and r^1 in different halves)
+// hit distinct banks for a fixed logical chunk.
+DSB_DEV int lds_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
-template <int BM, int BN, int WM, int WN, int NS, class Epi>
+template <int BM, int BN, int WM, int WN, class Epi>
 __global__ __launch_bounds__(WM* WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel(GemmProblem p, Epi epi) {
-  constexpr int BK = 32;
+  constexpr int BK = 64;
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
-  // direct-to-LDS loads per lane per stage: one load = 64 lanes × 16 B = 16 rows
-  constexpr int IA = BM / (16 * NW), IB = BN / (16 * NW), IAB = IA + IB;
+  // direct-to-LDS loads per lane per stage: one load = 64 lanes × 16 B = 8 rows
+  constexpr int IA = BM / (8 * NW), IB = BN / (8 * NW), IAB = IA + IB;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be 32-aligned");
-  static_assert(IA >= 1 && IB >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "loader split");
-  static_assert(NS >= 3 && (NS - 2) * IAB < 64, "stage ring / vmcnt range");
+  static_assert(IA >= 1 && IB >= 1 && BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "loader split");
+  static_assert(NW % 2 == 0, "row-block parity is the wave's");
+  static_assert(IAB < 64, "vmcnt range");
   constexpr int SA = BM * BK, SE = (BM + BN) * BK;  // elements
-  __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * SE];
 
   int M = p.M;
   if (p.M_dev) M = min(M, *p.M_dev);
@@ -184,11 +187,11 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   const int nk2 = p.K2 > 0 ? (p.K2 + BK - 1) / BK : 0;
   const int nk = nk1 + nk2;
 
-  // Loader geometry: lane fills slot (lane & 3) of row (lane >> 2) of its
-  // 16-row segment; every segment starts at a multiple of 16 rows, so the
-  // fetched chunk (lane & 3) ^ g(lane >> 2) is the same for every load.
-  const int lrow = lane >> 2;
-  const int lch = (lane & 3) ^ lds_swz(lrow);
+  // Loader geometry: lane fills slot (lane & 7) of row (lane >> 3) of its
+  // 8-row block; block b = wave + j·NW starts at row 8b, whose bit 3 is the
+  // wave's parity (NW even), so the fetched chunk is the same for every load.
+  const int lrow = lane >> 3;
+  const int lch = (lane & 7) ^ lds_swz(lrow + 8 * (wave & 1));
   const int rowsA = min(M - m0, BM), rowsB = min(p.N - n0, BN);
   // One descriptor per operand and K segment, over the tile's rows that
   // exist: rows past M (N) and chunks past K (offset OR-ed with OOB) fall
@@ -202,21 +205,20 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   const u32x4 dB1 = rsrc(p.B + (long)n0 * p.ldb, p.ldb, rowsB, p.K1);
   const u32x4 dA2 = rsrc(nk2 ? p.A2 + (long)m0 * p.lda2 : p.A, p.lda2, rowsA, K2);
   const u32x4 dB2 = rsrc(nk2 ? p.B2 + (long)n0 * p.ldb2 : p.B, p.ldb2, rowsB, K2);
-  // lane byte offset of its first row; load i adds i·16·NW rows
-  const int rw = 16 * wave + lrow;
+  // lane byte offset of its first row; load j adds j·8·NW rows
+  const int rw = 8 * wave + lrow;
   const int voA1 = (rw * (int)p.lda + lch * 8) * 2, voB1 = (rw * (int)p.ldb + lch * 8) * 2;
   const int voA2 = (rw * (int)p.lda2 + lch * 8) * 2, voB2 = (rw * (int)p.ldb2 + lch * 8) * 2;
-  const int stA1 = 32 * NW * (int)p.lda, stB1 = 32 * NW * (int)p.ldb;   // bytes per 16·NW rows
-  const int stA2 = 32 * NW * (int)p.lda2, stB2 = 32 * NW * (int)p.ldb2;
+  const int stA1 = 16 * NW * (int)p.lda, stB1 = 16 * NW * (int)p.ldb;  // bytes per 8·NW rows
+  const int stA2 = 16 * NW * (int)p.lda2, stB2 = 16 * NW * (int)p.ldb2;
   // OR-ed into the offset of chunks past K: beyond any descriptor, loads zero
   constexpr int OOB = 0x7ff00000;
   const unsigned lds0 = lds_addr(smem);
 
-  // Loads of K tile kt into stage slot `slot`: IAB loads per lane, issued one
-  // at a time by issue_one(j) so they can be spread over a run of MFMAs.
-  // Tiles past the end (kt >= nk) fall past K of the second segment and fill
-  // the slot with zeros without touching memory, so every step issues the
-  // same number of loads and the vmcnt arithmetic never changes.
+  // Loads of K tile kt into stage slot `slot`, issued one at a time by
+  // issue_one(j) so they can be spread over a run of MFMAs. Tiles past the
+  // end (kt >= nk) fall past K of the second segment and fill the slot with
+  // zeros without touching memory.
   struct Fill {
     u32x4 dA, dB;
     int voA, voB, stA, stB;
@@ -234,14 +236,14 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     f.voB = (s1 ? voB1 : voB2) + kb;
     f.stA = s1 ? stA1 : stA2;
     f.stB = s1 ? stB1 : stB2;
-    f.dst = lds0 + (unsigned)(slot * SE * 2) + (unsigned)(16 * wave * BK * 2);
+    f.dst = lds0 + (unsigned)(slot * SE * 2) + (unsigned)(8 * wave * BK * 2);
     return f;
   };
   auto issue_one = [&](const Fill& f, int j) {
     if (j < IA)
-      lds_dma16(f.dA, f.voA + j * f.stA, f.dst + j * 16 * NW * BK * 2);
+      lds_dma16(f.dA, f.voA + j * f.stA, f.dst + j * 8 * NW * BK * 2);
     else
-      lds_dma16(f.dB, f.voB + (j - IA) * f.stB, f.dst + (SA + (j - IA) * 16 * NW * BK) * 2);
+      lds_dma16(f.dB, f.voB + (j - IA) * f.stB, f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
   };
 
   f32x16 acc[FM][FN];
@@ -253,95 +255,76 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int lr = lane & 31, lh = lane >> 5;
-  // Fragment addresses (elements) inside a stage for slice kk: row r, chunk
-  // 2·kk + lh. Fragments are 32 rows apart, a multiple of 16, so g depends
-  // on lr only.
+  // Fragment rows are 32 apart, so the swizzle depends on lr only. Slice s
+  // of the stage (K 16s .. 16s+15) is chunk 2s + lh of the lane's row.
   const int g = lds_swz(lr);
-  const int fa0 = (wm * TM + lr) * BK + (((0 + lh) ^ g) << 3);
-  const int fa1 = (wm * TM + lr) * BK + (((2 + lh) ^ g) << 3);
-  const int fb0 = SA + (wn * TN + lr) * BK + (((0 + lh) ^ g) << 3);
-  const int fb1 = SA + (wn * TN + lr) * BK + (((2 + lh) ^ g) << 3);
-  bf16x8 af0[FM], bf0[FN], af1[FM], bf1[FN];
-  auto read0 = [&](const bf16* b) {
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) af0[fm] = *reinterpret_cast<const bf16x8*>(b + fa0 + fm * 32 * BK);
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) bf0[fn] = *reinterpret_cast<const bf16x8*>(b + fb0 + fn * 32 * BK);
-  };
-  auto read1 = [&](const bf16* b) {
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) af1[fm] = *reinterpret_cast<const bf16x8*>(b + fa1 + fm * 32 * BK);
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) bf1[fn] = *reinterpret_cast<const bf16x8*>(b + fb1 + fn * 32 * BK);
-  };
-  auto mma0 = [&]() {
+  const int arow = (wm * TM + lr) * BK, brow = SA + (wn * TN + lr) * BK;
+  bf16x8 af[2][FM], bfr[2][FN];
+  auto read = [&](const bf16* b, int s, int buf) {
+    const int ch = ((2 * s + lh) ^ g) << 3;
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
+      af[buf][fm] = *reinterpret_cast<const bf16x8*>(b + arow + ch + fm * 32 * BK);
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = mfma32(bf0[fn], af0[fm], acc[fm][fn]);
+    for (int fn = 0; fn < FN; ++fn)
+      bfr[buf][fn] = *reinterpret_cast<const bf16x8*>(b + brow + ch + fn * 32 * BK);
   };
-  // Slice-1 MFMAs with the next stage's loads spread among them: the loads'
-  // scalar set-up and issue run in the MFMA shadow instead of stalling it.
-  // The next stage's slice-0 fragment reads go out after the first MFMA so
-  // the MFMA pipe restarts right after the barrier.
-  auto mma1_interleaved = [&](const Fill& f, const bf16* next) {
+  // MFMAs of one slice, with loads j0 .. j0+nj-1 of `f` spread among them:
+  // their scalar set-up and issue run in the MFMA shadow.
+  auto mma = [&](int buf, const Fill& f, int j0, int nj) {
     constexpr int NM = FM * FN;
-    constexpr int EVERY = NM / IAB > 0 ? NM / IAB : 1;
-    int j = 0;
-    __builtin_amdgcn_sched_barrier(0);
+    const int every = nj > 0 ? (NM / nj > 0 ? NM / nj : 1) : NM + 1;
+    int j = j0;
 #pragma unroll
     for (int t = 0; t < NM; ++t) {
       const int fm = t / FN, fn = t % FN;
-      acc[fm][fn] = mfma32(bf1[fn], af1[fm], acc[fm][fn]);
-      if (t == 0) {
-        __builtin_amdgcn_sched_barrier(0);
-        read0(next);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (t % EVERY == EVERY - 1 && j < IAB) {
+      acc[fm][fn] = mfma32(bfr[buf][fn], af[buf][fm], acc[fm][fn]);
+      if (t % every == every - 1 && j < j0 + nj) {
         __builtin_amdgcn_sched_barrier(0);
         issue_one(f, j++);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
-    for (; j < IAB; ++j) issue_one(f, j);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int jj = 0; jj < IAB; ++jj)
+      if (jj >= j && jj < j0 + nj) issue_one(f, jj);
   };
 
-  // Prologue: stages 0 .. NS-2 in flight; wait for stage 0, read its slice 0.
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s) {
-    const Fill f = make_fill(s, s);
+  // Two stages of BK = 64. Step kt computes on slot kt&1 while the loads of
+  // stage kt+1 fill the other slot; the step ends with the wave's own loads
+  // landed and one barrier, which both publishes stage kt+1 and retires
+  // stage kt (every wave's fragment reads of it were consumed by its MFMAs).
+  {
+    const Fill f = make_fill(0, 0);
 #pragma unroll
     for (int j = 0; j < IAB; ++j) issue_one(f, j);
   }
-  wait_vm<(NS - 2) * IAB>();
+  wait_vm<0>();
   lds_barrier();
-  read0(smem);
 
-  int cur = 0;  // slot of stage kt
   for (int kt = 0; kt < nk; ++kt) {
-    const int nxt = cur + 1 == NS ? 0 : cur + 1;
-    const int fill = cur == 0 ? NS - 1 : cur - 1;  // slot of stage kt-1 = kt+NS-1
-    // slice-0 fragments (read one half-step ago) are complete; the compiler
-    // then waits only on the slice-1 reads where they are used.
-    __builtin_amdgcn_s_waitcnt((0 << 8) | (7 << 4) | 15 | (3 << 14));  // lgkmcnt(0)
-    read1(smem + cur * SE);
+    const int cur = kt & 1;
+    const bf16* b = smem + cur * SE;
+    const Fill f = make_fill(kt + 1, cur ^ 1);
+    read(b, 0, 0);
+    read(b, 1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mma0();
+    mma(0, f, 0, IAB / 2);
     __builtin_amdgcn_sched_barrier(0);
-    // own loads of stage kt+1 landed (stages kt+2 .. kt+NS-2 may fly) → the
-    // barrier publishes stage kt+1 and retires stage kt-1's slot.
-    const Fill f = make_fill(kt + NS - 1, fill);  // scalar set-up before the barrier
-    wait_vm<(NS - 3) * IAB>();
+    read(b, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, f, IAB / 2, IAB - IAB / 2);
+    __builtin_amdgcn_sched_barrier(0);
+    read(b, 3, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0, f, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, f, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm<0>();
     lds_barrier();
-    mma1_interleaved(f, smem + nxt * SE);
-    cur = nxt;
   }
 
-  wait_vm<0>();
-  __syncthreads();  // every wave is done with the stages before the epilogue reuses them
   epi.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
                                    (void*)smem);
 }
@@ -419,13 +402,12 @@ struct EpiLoraZ {
 // Tile configurations. Big: 256×256, 4 waves of 128×128 (256 accumulators per
 // lane). Mid: 128×128, 4 waves of 64×64. Skinny: 64×64, 4 waves of 32×32.
 enum GemmCfg { GEMM_BIG = 0, GEMM_MID = 1, GEMM_SKINNY = 2 };
-constexpr int GEMM_STAGES = 4;
 
 template <int BM, int BN, int WM, int WN, class Epi>
 hipError_t launch_gemm_cfg(const GemmProblem& p, const Epi& e, hipStream_t s) {
   const int nbm = (p.M + BM - 1) / BM, nbn = (p.N + BN - 1) / BN;
   if (nbm == 0 || nbn == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WM, WN, GEMM_STAGES, Epi>), dim3(nbm * nbn),
+  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WM, WN, Epi>), dim3(nbm * nbn),
                      dim3(WM * WN * 64), 0, s, p, e);
   return hipGetLastError();
 }
