@@ -132,6 +132,16 @@ DSB_DEV u32x4 make_rsrc(const void* base, int bytes) {
   return r;
 }
 
+// Buffer descriptor for plain (register-destination) buffer loads: same
+// fields as make_rsrc; loads at or beyond `bytes` return zeros.
+DSB_DEV __amdgpu_buffer_rsrc_t make_brsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+// 16 bytes per lane at byte offset `off` of the descriptor's range.
+DSB_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 typedef __attribute__((address_space(3))) bf16 lds_bf16;
 DSB_DEV unsigned lds_addr(bf16* p) {
   return __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)(lds_bf16*)p);

@@ -49,13 +49,15 @@ hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunk
 
 // ------------------------------------------------------------------ skinny NT
 // Z[t, j] = sum_k X[t, k]·B[j, k]. Block: 32 tokens; the X chunk [32 × 128]
-// and the B chunk [16·RB × 128] stream through a 3-stage direct-to-LDS ring
-// (one barrier per chunk); wave w multiplies columns 32w .. 32w+31 of each
+// and the B chunk [16·RB × 128] stream through a direct-to-LDS ring of up to
+// 96 KB (8 stages at RB = 1, so ~84 KB per CU stay in flight; one barrier per
+// chunk); wave w multiplies columns 32w .. 32w+31 of each
 // chunk with 16×16×32 MFMAs (2 token tiles × RB rank tiles) and the four
 // waves' partial sums are added through LDS at the end.
 template <int RB>
 __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
-  constexpr int NS = 3, XT = 32 * 128, BT = 16 * RB * 128, SE = XT + BT;
+  constexpr int XT = 32 * 128, BT = 16 * RB * 128, SE = XT + BT;
+  constexpr int NS = (48 * 1024) / SE < 8 ? (48 * 1024) / SE : 8;  // SE elements = 2·SE bytes
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
   const int t0 = blockIdx.x * 32;
@@ -84,12 +86,12 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   const int fr = lane & 15, fc = 32 * w + 8 * (lane >> 4);
   const int off = toff(fr, fc) * 2;  // tiles start at multiples of 16 rows: f(r) = f(l%16)
 
-  issue(0, 0);
-  issue(1, 1);
+#pragma unroll
+  for (int c = 0; c < NS - 1; ++c) issue(c, c);
   for (int c = 0; c < nc; ++c) {
-    wait_vm<LPS>();  // own loads of chunk c landed (chunk c+1 may fly)
-    lds_barrier();   // chunk c visible; slot (c+2)%3 = slot of chunk c-1 is free
-    issue(c + 2, (c + 2) % NS);
+    wait_vm<(NS - 2) * LPS>();  // own loads of chunk c landed (c+1 .. c+NS-2 may fly)
+    lds_barrier();               // chunk c visible; the slot of chunk c-1 is free
+    issue(c + NS - 1, (c + NS - 1) % NS);
     const char* st = reinterpret_cast<const char*>(smem + (c % NS) * SE);
     bf16x8 xf[2], bfr[RB];
 #pragma unroll
@@ -139,14 +141,15 @@ hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s) {
 // ------------------------------------------------------------------ TN
 // work[split][c][j] = sum over the split's tokens t of X[t, c]·P[t, j].
 // Block: 128 columns × one token split; token chunks of 32 stream through a
-// 4-stage direct-to-LDS ring: X chunk [32 × 128] (swizzled 256-byte rows) and
-// P chunk [32 × R] (rows of 2R bytes). Both operands reduce over tokens, so
+// direct-to-LDS ring of up to 80 KB (two blocks per CU, 6-8 stages): X chunk
+// [32 × 128] (swizzled 256-byte rows) and P chunk [32 × R] (rows of 2R bytes). Both operands reduce over tokens, so
 // both are read transposed with ds_read_b64_tr_b16 (16×16×32 pattern: lane j
 // of group g points at row 8g + j/4 (+4), column c0 + 4(j%4)); wave w owns
 // columns 32w .. 32w+31 (2 column tiles) × RB rank tiles.
 template <int RB>
 __global__ __launch_bounds__(256, 2) void lora_tn_partial_kernel(TnArgs a) {
-  constexpr int NS = 4, XT = 32 * 128, PT = 32 * 16 * RB, SE = XT + PT;
+  constexpr int XT = 32 * 128, PT = 32 * 16 * RB, SE = XT + PT;
+  constexpr int NS = (40 * 1024) / SE < 8 ? (40 * 1024) / SE : 8;  // SE elements = 2·SE bytes
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
   __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
@@ -242,6 +245,7 @@ __global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnArgs a) {
   if (idx >= (long)a.R * a.C) return;
   const int c = (int)(idx / a.R), j = (int)(idx % a.R);
   float s = 0.f;
+#pragma unroll 8
   for (int sp = 0; sp < a.nsplit; ++sp) s += a.work[((long)sp * a.C + c) * a.R + j];
   s *= a.scale;
   const int grp = j / a.rg, jj = j % a.rg;
