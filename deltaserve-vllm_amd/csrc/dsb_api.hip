@@ -190,6 +190,14 @@ struct LayerState {
 
 }  // namespace
 
+// Every non-null pointer 16-byte aligned (the vectorized kernels' contract).
+template <class... P>
+bool aligned16(const P*... ps) {
+  bool ok = true;
+  ((ok = ok && ((reinterpret_cast<uintptr_t>(ps) & 15) == 0)), ...);
+  return ok;
+}
+
 struct dsb_handle {
   dsb_desc d{};
   int D, Hq, Hkv, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk;
@@ -1484,6 +1492,8 @@ int dsb_op_rope_table(const int32_t* pos, int n, const float* inv_freq, int half
 int dsb_op_rope(const void* qkv_pre, int64_t ldin, void* qk_out, int64_t ldout, const float* cos_t,
                 const float* sin_t, int n, int Hq, int Hkv, const void* q_norm, const void* k_norm,
                 float eps, void* stream) {
+  if (ldin % 8 || ldout % 8 || !aligned16(qkv_pre, qk_out, q_norm, k_norm, cos_t, sin_t))
+    return fail(nullptr, "dsb_op_rope: row strides must be multiples of 8, pointers 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   OPCK(rope_fwd((const bf16*)qkv_pre, ldin, (bf16*)qk_out, ldout, cos_t, sin_t, n, nullptr, Hq,
                 Hkv, (const bf16*)q_norm, (const bf16*)k_norm, eps, s));
@@ -1494,6 +1504,8 @@ int dsb_op_rope(const void* qkv_pre, int64_t ldin, void* qk_out, int64_t ldout, 
 int dsb_op_rope_bwd(void* g, int64_t ldg, const void* qkv_pre, int64_t ldp, const float* cos_t,
                     const float* sin_t, int n, int Hq, int Hkv, const void* q_norm,
                     const void* k_norm, float eps, void* stream) {
+  if (ldg % 8 || ldp % 8 || !aligned16(g, qkv_pre, q_norm, k_norm, cos_t, sin_t))
+    return fail(nullptr, "dsb_op_rope_bwd: row strides must be multiples of 8, pointers 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   OPCK(rope_bwd((bf16*)g, ldg, (const bf16*)qkv_pre, ldp, cos_t, sin_t, n, nullptr, Hq, Hkv,
                 (const bf16*)q_norm, (const bf16*)k_norm, eps, s));

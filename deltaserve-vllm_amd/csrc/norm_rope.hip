@@ -141,10 +141,19 @@ __global__ void rope_table_kernel(const int* __restrict__ pos, int n, const int*
   sinb[idx] = s;
 }
 
-// One wave per (token, head) over the q heads then the k heads; head_dim 128:
-// lane l owns the rotate-half pair (l, l + 64).
+// Eight lanes per head (head_dim 128): lane i of a head's group owns the
+// rotate-half pairs (8i + e, 64 + 8i + e), e = 0..7, moved as 16-byte
+// vectors; one wave covers 8 heads of one token (q heads, then k heads), and
+// per-head sums reduce over the group's 8 lanes.
 //   in : qkv_pre row [q | k | v] (pre-norm, pre-RoPE projection output)
 //   out: qk row [q | k] after (optional per-head RMSNorm, rounded to bf16) + RoPE
+DSB_DEV float group8_sum(float v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  return v;
+}
+
 __global__ __launch_bounds__(256) void rope_fwd_kernel(
     const bf16* __restrict__ in, long ldin, bf16* __restrict__ out, long ldout,
     const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
@@ -152,27 +161,53 @@ __global__ __launch_bounds__(256) void rope_fwd_kernel(
     const bf16* __restrict__ kn_w, float eps) {
   int N = n;
   if (n_dev) N = min(N, *n_dev);
-  const int H = Hq + Hkv;
+  const int H = Hq + Hkv, HG = (H + 7) / 8;
   const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= (long)N * H) return;
-  const int t = (int)(item / H), hh = (int)(item % H), l = threadIdx.x & 63;
-  const bf16* src = in + (long)t * ldin + hh * 128;
-  float x1 = (float)src[l], x2 = (float)src[l + 64];
-  const bf16* nw = hh < Hq ? qn_w : kn_w;
+  if (item >= (long)N * HG) return;
+  const int t = (int)(item / HG), l = threadIdx.x & 63, i = l & 7;
+  const int hh = (int)(item % HG) * 8 + (l >> 3);
+  const bool live = hh < H;
+  const int h = live ? hh : H - 1;
+  const bf16* src = in + (long)t * ldin + h * 128 + 8 * i;
+  float x1[8], x2[8];
+  unpack8(ldg128(src), x1);
+  unpack8(ldg128(src + 64), x2);
+  const bf16* nw = h < Hq ? qn_w : kn_w;
   if (nw) {
-    const float ss = wave_sum(x1 * x1 + x2 * x2);
-    const float inv = rsqrtf(ss / 128.f + eps);
-    x1 = (float)(bf16)((x1 * inv) * (float)nw[l]);
-    x2 = (float)(bf16)((x2 * inv) * (float)nw[l + 64]);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
+    const float inv = rsqrtf(group8_sum(ss) / 128.f + eps);
+    float w1[8], w2[8];
+    unpack8(ldg128(nw + 8 * i), w1);
+    unpack8(ldg128(nw + 64 + 8 * i), w2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x1[e] = (float)(bf16)((x1[e] * inv) * w1[e]);
+      x2[e] = (float)(bf16)((x2[e] * inv) * w2[e]);
+    }
   }
-  const float c = cosb[(long)t * 64 + l], s = sinb[(long)t * 64 + l];
-  bf16* dst = out + (long)t * ldout + hh * 128;
-  dst[l] = (bf16)(x1 * c - x2 * s);
-  dst[l + 64] = (bf16)(x2 * c + x1 * s);
+  const f32x4* cp = reinterpret_cast<const f32x4*>(cosb + (long)t * 64 + 8 * i);
+  const f32x4* sp = reinterpret_cast<const f32x4*>(sinb + (long)t * 64 + 8 * i);
+  const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  float o1[8], o2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    o1[e] = x1[e] * c[e] - x2[e] * sn[e];
+    o2[e] = x2[e] * c[e] + x1[e] * sn[e];
+  }
+  if (live) {
+    bf16* dst = out + (long)t * ldout + h * 128 + 8 * i;
+    stg128(dst, pack8(o1));
+    stg128(dst + 64, pack8(o2));
+  }
 }
 
 // In-place RoPE backward on g[:, :(Hq+Hkv)*128] (then the per-head RMSNorm
-// backward against the pre-norm projection output when norm weights are given).
+// backward against the pre-norm projection output when norm weights are given);
+// same lane layout as the forward.
 __global__ __launch_bounds__(256) void rope_bwd_kernel(
     bf16* __restrict__ g, long ldg, const bf16* __restrict__ pre, long ldp,
     const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
@@ -180,28 +215,58 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(
     const bf16* __restrict__ kn_w, float eps) {
   int N = n;
   if (n_dev) N = min(N, *n_dev);
-  const int H = Hq + Hkv;
+  const int H = Hq + Hkv, HG = (H + 7) / 8;
   const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= (long)N * H) return;
-  const int t = (int)(item / H), hh = (int)(item % H), l = threadIdx.x & 63;
-  bf16* gp = g + (long)t * ldg + hh * 128;
-  const float g1 = (float)gp[l], g2 = (float)gp[l + 64];
-  const float c = cosb[(long)t * 64 + l], s = sinb[(long)t * 64 + l];
-  float r1 = g1 * c + g2 * s;
-  float r2 = -g1 * s + g2 * c;
-  const bf16* nw = hh < Hq ? qn_w : kn_w;
-  if (nw) {
-    const bf16* xp = pre + (long)t * ldp + hh * 128;
-    const float x1 = (float)xp[l], x2 = (float)xp[l + 64];
-    const float inv = rsqrtf(wave_sum(x1 * x1 + x2 * x2) / 128.f + eps);
-    const float a1 = r1 * (float)nw[l], a2 = r2 * (float)nw[l + 64];
-    const float dot = wave_sum(a1 * (x1 * inv) + a2 * (x2 * inv));
-    const float k = dot / 128.f;
-    r1 = (a1 - (x1 * inv) * k) * inv;
-    r2 = (a2 - (x2 * inv) * k) * inv;
+  if (item >= (long)N * HG) return;
+  const int t = (int)(item / HG), l = threadIdx.x & 63, i = l & 7;
+  const int hh = (int)(item % HG) * 8 + (l >> 3);
+  const bool live = hh < H;
+  const int h = live ? hh : H - 1;
+  bf16* gp = g + (long)t * ldg + h * 128 + 8 * i;
+  float g1[8], g2[8];
+  unpack8(ldg128(gp), g1);
+  unpack8(ldg128(gp + 64), g2);
+  const f32x4* cp = reinterpret_cast<const f32x4*>(cosb + (long)t * 64 + 8 * i);
+  const f32x4* sp = reinterpret_cast<const f32x4*>(sinb + (long)t * 64 + 8 * i);
+  const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  float r1[8], r2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    r1[e] = g1[e] * c[e] + g2[e] * sn[e];
+    r2[e] = -g1[e] * sn[e] + g2[e] * c[e];
   }
-  gp[l] = (bf16)r1;
-  gp[l + 64] = (bf16)r2;
+  const bf16* nw = h < Hq ? qn_w : kn_w;
+  if (nw) {
+    const bf16* xp = pre + (long)t * ldp + h * 128 + 8 * i;
+    float x1[8], x2[8], w1[8], w2[8];
+    unpack8(ldg128(xp), x1);
+    unpack8(ldg128(xp + 64), x2);
+    unpack8(ldg128(nw + 8 * i), w1);
+    unpack8(ldg128(nw + 64 + 8 * i), w2);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
+    const float inv = rsqrtf(group8_sum(ss) / 128.f + eps);
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      r1[e] *= w1[e];
+      r2[e] *= w2[e];
+      dot += r1[e] * (x1[e] * inv) + r2[e] * (x2[e] * inv);
+    }
+    const float k = group8_sum(dot) / 128.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      r1[e] = (r1[e] - (x1[e] * inv) * k) * inv;
+      r2[e] = (r2[e] - (x2[e] * inv) * k) * inv;
+    }
+  }
+  if (live) {
+    stg128(gp, pack8(r1));
+    stg128(gp + 64, pack8(r2));
+  }
 }
 
 // h[m, j] = bf16(silu(gate) * up) with gate = GU[m, j], up = GU[m, I + j].
@@ -284,7 +349,7 @@ hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_
 hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
                     const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
                     const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s) {
-  const long items = (long)n * (Hq + Hkv);
+  const long items = (long)n * ((Hq + Hkv + 7) / 8);
   if (items <= 0) return hipSuccess;
   hipLaunchKernelGGL(rope_fwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, in,
                      ldin, out, ldout, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
@@ -294,7 +359,7 @@ hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const floa
 hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* cosb,
                     const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
                     const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s) {
-  const long items = (long)n * (Hq + Hkv);
+  const long items = (long)n * ((Hq + Hkv + 7) / 8);
   if (items <= 0) return hipSuccess;
   hipLaunchKernelGGL(rope_bwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, g,
                      ldg, pre, ldp, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
