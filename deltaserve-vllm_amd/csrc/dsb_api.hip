@@ -226,6 +226,7 @@ struct dsb_handle {
   bf16 *normed, *dlog;
   float2* stats;
   float *tgt_logit, *lse_h, *loss_row, *dH;
+  float* logits = nullptr;  // [N + 1, ldwt] fp32 head logits (stats pass → grad pass)
   float* tn_work;
   long tn_work_elems;
   float *cosb, *sinb, *inv_freq;
@@ -382,6 +383,7 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->lse_h, NN));
   CKR(dalloc(h, &h->loss_row, NN));
   CKR(dalloc(h, &h->dlog, NN * h->vchunk));
+  CKR(dalloc(h, &h->logits, NN * h->ldwt));
   CKR(dalloc(h, &h->dH, NN * D));
   h->tn_work_elems = 32L << 20;
   CKR(dalloc(h, &h->tn_work, h->tn_work_elems));
@@ -666,9 +668,11 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
     ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
     ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH;
+    ha.logits = h->logits; ha.ldl = h->ldwt;
     {
-      // logits recompute in the LSE pass is not algorithmic work (6·M·D·V vs 4·M·D·V)
-      KScope ks(h, st, "gemm256_ce_stats", 0, 0, 0, 2.0 * D + 8.0 * h->ntn, 0, 2.0 * h->V * D);
+      // the logits product: 2·M·D·V of the head's 4·M·D·V (the dH product is the rest)
+      KScope ks(h, st, "gemm256_ce_stats", 2.0 * h->V * D, 0, 0,
+                2.0 * D + 8.0 * h->ntn + 4.0 * h->V, 0, 2.0 * h->V * D);
       LK(head_stats(ha, st));
     }
     {
@@ -678,8 +682,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     for (int c0 = 0; c0 < h->V; c0 += h->vchunk) {
       const int Nc = std::min(h->vchunk, h->V - c0);
       {
-        KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, Nc))) + "_ce_grad", 2.0 * Nc * D, 0,
-                  0, 2.0 * D + 2.0 * Nc, 0, 2.0 * Nc * D);
+        KScope ks(h, st, "ce_grad", 0, 0, 0, 4.0 * Nc + 2.0 * ((Nc + 7) / 8 * 8) + 8.0, 0, 0);
         LK(head_chunk_grad(ha, c0, st));
       }
       {
@@ -1619,7 +1622,8 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   float* scal = tmp.alloc<float>(4);
   int* err = tmp.alloc<int>(1);
   bf16* dlog = tmp.alloc<bf16>((size_t)(n + 1) * vchunk);
-  if (!WT || !dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog)
+  float* logits = tmp.alloc<float>((size_t)(n + 1) * ldwt);
+  if (!WT || !dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog || !logits)
     return fail(nullptr, "dsb_op_head: hipMalloc failed");
   float hsc[4] = {nv > 0 ? 1.f / nv : 0.f, 0.f, 0.f, 0.f};
   OPCK(hipMemcpy(scal, hsc, sizeof(hsc), hipMemcpyHostToDevice));
@@ -1632,7 +1636,7 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w; a.WT = WT; a.ldwt = ldwt;
   a.labels = labels; a.n = n; a.n_dev = nullptr; a.D = D; a.V = V; a.stats = stats; a.ntn = ntn;
   a.tgt_logit = tl; a.lse = lse; a.loss_row = lr; a.loss_out = scal + 1; a.inv_nvalid = scal;
-  a.dlog = dlog; a.vchunk = vchunk; a.dH = dH;
+  a.dlog = dlog; a.vchunk = vchunk; a.dH = dH; a.logits = logits; a.ldl = ldwt;
   OPCK(head_fwd_bwd(a, s));
   OPCK(hipStreamSynchronize(s));
   int herr = 0;

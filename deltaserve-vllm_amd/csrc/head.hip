@@ -6,13 +6,17 @@
 //   grad_rows = dlogits · W. Rows that predict nothing (the last token of each
 //   sequence) carry label -1 and contribute neither loss nor gradient.
 //
-// Pass 1 (LSE): one vocab-tiled MFMA GEMM whose epilogue reduces each 256-wide
-//   vocab tile to (max, sum exp) per row and picks out the target logit.
+// Pass 1 (LSE): one vocab-tiled MFMA GEMM whose epilogue stores the fp32
+//   logits (row-contiguous, [n, round_up(V, 8)]), reduces each 256-wide vocab
+//   tile to (max, sum exp) per row and picks out the target logit.
 // Reduce: combine the per-tile statistics into the row LSE and the row loss;
 //   a single-block deterministic sum gives the cycle loss.
-// Pass 2, per vocab chunk: recompute the logits with an epilogue writing
-//   bf16 dlogits for the chunk only, then dH += dlogits_chunk · W_chunk with
-//   the transposed head copy (fp32 accumulate in the epilogue).
+// Pass 2, per vocab chunk: an elementwise kernel turns the stored logits into
+//   bf16 dlogits for the chunk, then dH += dlogits_chunk · W_chunk with the
+//   transposed head copy (fp32 accumulate in the epilogue). The logits are
+//   the same fp32 values the reference computes once per chunk; keeping them
+//   (4.2 GB at 8192 rows × 128256 vocab) costs one write and one read instead
+//   of a second vocab-wide GEMM.
 #include "gemm_nt.h"
 #include "kernels.h"
 
@@ -27,15 +31,32 @@ struct EpiCEStats {
   int ntn;
   float* tgt_logit;
   int V;
+  float* logits;
+  long ldl;
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
     constexpr int TM = FM * 32, TN = FN * 32, BMl = WM * TM;
+    static_assert(WM * WN * 32 * (TN + 4) * 4 + WN * BMl * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2,
+                  "row staging + reduction scratch fit in the stage buffers");
+    // the logits, row-contiguous through the per-wave staging of the LDS
+    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+      const int lim = V - n;
+      if (lim <= 0) return;
+      float* d = logits + (long)m * ldl + n;
+      if (lim >= 8) {
+        *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      } else {
+        for (int i = 0; i < lim; ++i) d[i] = v[i];
+      }
+    });
     const int wn = wave % WN, wm = wave / WN;
     const int n0 = nw - wn * TN;
     const int pn = n0 / (WN * TN);
     const int lr = lane & 31, lh = lane >> 5;
-    float* red = reinterpret_cast<float*>(smem);  // [WN][BMl]
+    // [WN][BMl], past the staging rows of all waves
+    float* red = reinterpret_cast<float*>(smem) + WM * WN * 32 * (TN + 4);
     float mx[FM];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
@@ -94,36 +115,45 @@ struct EpiCEStats {
   }
 };
 
-// Columns [Nc, Nc8) of the chunk (Nc8 = round_up(Nc, 8)) are written as zero
-// so the dH product can run its K loop over whole 16-byte chunks.
-struct EpiCEGrad {
-  const int* labels;
-  const float* lse;
-  const float* inv_nvalid;
-  bf16* D;
-  long ldd;
-  int c0;
-  int Nc;
-  int Nc8;
-  template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
-                   void* smem) const {
-    const float sc = *inv_nvalid;
-    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
-      const int lim = Nc8 - n;
-      if (lim <= 0) return;
-      const int t = labels[m];
-      const float l = lse[m];
-      float p[8];
+// dlog[m, j] = bf16((exp(logit[m, c0 + j] - lse[m]) - [c0 + j == t_m]) / n_valid)
+// for the chunk's columns j < Nc (0 for rows without a target); columns
+// [Nc, Nc8) (Nc8 = round_up(Nc, 8)) are written as zero so the dH product
+// runs its K loop over whole 16-byte chunks. Eight columns per thread.
+__global__ __launch_bounds__(256) void ce_grad_kernel(const float* __restrict__ logits, long ldl,
+                                                      const int* __restrict__ labels,
+                                                      const float* __restrict__ lse,
+                                                      const float* __restrict__ inv_nvalid,
+                                                      bf16* __restrict__ D, long ldd, int c0,
+                                                      int Nc, int Nc8, int n, const int* n_dev) {
+  int N = n;
+  if (n_dev) N = min(N, *n_dev);
+  const int G = Nc8 / 8;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const int m = (int)(idx / G), g = (int)(idx % G);
+  if (m >= N) return;
+  const int t = labels[m];
+  const float l = lse[m], sc = *inv_nvalid;
+  const int j0 = 8 * g;
+  const float* src = logits + (long)m * ldl + c0 + j0;
+  float x[8];
+  if (j0 + 8 <= Nc) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+  } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float e = __expf(v[i] - l) - ((c0 + n + i) == t ? 1.f : 0.f);
-        p[i] = (t >= 0 && n + i < Nc) ? e * sc : 0.f;
-      }
-      store8_bf16(D + (long)m * ldd + n, p, lim);
-    });
+    for (int i = 0; i < 8; ++i) x[i] = j0 + i < Nc ? src[i] : 0.f;
   }
-};
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float e = __expf(x[i] - l) - ((c0 + j0 + i) == t ? 1.f : 0.f);
+    p[i] = (t >= 0 && j0 + i < Nc) ? e * sc : 0.f;
+  }
+  stg128(D + (long)m * ldd + j0, pack8(p));
+}
+
 }  // namespace
 
 // One wave per row: combine the per-tile (max, sumexp) pairs.
@@ -169,7 +199,7 @@ hipError_t head_stats(const HeadArgs& a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   GemmProblem p{a.normed, a.ldh, a.W, (long)a.D, nullptr, 0, nullptr, 0,
                 a.n, a.V, a.D, 0, a.n_dev};
-  EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.V};
+  EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.V, a.logits, a.ldl};
   return launch_gemm_cfg<256, CE_BN, 2, 2>(p, epi, s);
 }
 
@@ -185,11 +215,13 @@ hipError_t head_reduce(const HeadArgs& a, hipStream_t s) {
 }
 
 hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s) {
-  const int Nc = min(a.vchunk, a.V - c0);
-  GemmProblem p{a.normed, a.ldh, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
-                a.n, Nc, a.D, 0, a.n_dev};
-  EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Nc, (Nc + 7) / 8 * 8};
-  return launch_gemm(p, epi, s);
+  const int Nc = min(a.vchunk, a.V - c0), Nc8 = (Nc + 7) / 8 * 8;
+  const long items = (long)a.n * (Nc8 / 8);
+  if (items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ce_grad_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
+                     a.logits, a.ldl, a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0,
+                     Nc, Nc8, a.n, a.n_dev);
+  return hipGetLastError();
 }
 
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {

@@ -109,6 +109,7 @@ struct HeadArgs {
   float* loss_row;                // [n_cap]
   float* loss_out;                // scalar: sum(loss_row)/n_valid
   const float* inv_nvalid;        // device scalar 1/n_valid (0 when none)
+  float* logits; long ldl;        // [n_cap, ldl] fp32, ldl = round_up(V, 8)
   bf16* dlog; int vchunk;         // [n_cap, vchunk] bf16 scratch
   float* dH;                      // [n, D] fp32
 };
