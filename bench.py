@@ -178,7 +178,7 @@ def copy_calibration(nbytes=2 << 30, reps=3):
     log(f"[bench] copy calibration: {reps} copies of {nbytes} bytes")
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm256_bf16.json")
+TRAFFIC_DIR = os.path.join(ROOT, "profiles")
 
 
 def measured_traffic(kernel_class):
@@ -186,7 +186,7 @@ def measured_traffic(kernel_class):
     PMC summary (FETCH_SIZE and WRITE_SIZE passes scaled by a copy of known
     size); None when no summary for this class exists."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(os.path.join(TRAFFIC_DIR, f"traffic_{kernel_class}.json")) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None

@@ -763,18 +763,25 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     if (hg) CKR(skinny(h, h->xn2, D, ls.Agu, 2 * r, D, h->Zgu_b, 2 * r, st));
     {
+      // gate‖up (ffn.py:25-26) with h = silu(gate)·up in the epilogue; h is the
+      // down projection's input and only feeds its LoRA terms. The fused form
+      // needs I to be a multiple of 64 (whole 32-column fragments per half).
       GemmProblem p{h->xn2, (long)D, wgu, (long)D, hg ? h->Zgu_b : nullptr, 2L * r,
                     hg ? ls.B2gu : nullptr, 2L * r, N, 2 * I, D, hg ? 2 * r : 0, nd};
-      EpiBF16 e{h->gu, 2L * I, 2 * I, nullptr, 0};
-      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
-    }
-    if (hd) {
-      {
-        KScope ks(h, st, "swiglu_h", 0, 0, 0, 6.0 * I, 0, 0);
-        LK(swiglu_h(h->gu, 2L * I, h->hb, I, N, nd, I, st));
+      if (I % 64 == 0) {
+        p.glu_half = I;
+        EpiGLU e{h->gu, 2L * I, hd ? h->hb : nullptr, (long)I, I};
+        CKR(gemm(h, "glu", p, e, st, 2.0, hd ? 2.0 * I : 0.0));
+      } else {
+        EpiBF16 e{h->gu, 2L * I, 2 * I, nullptr, 0};
+        CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
+        if (hd) {
+          KScope ks(h, st, "swiglu_h", 0, 0, 0, 6.0 * I, 0, 0);
+          LK(swiglu_h(h->gu, 2L * I, h->hb, I, N, nd, I, st));
+        }
       }
-      CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
     }
+    if (hd) CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
 
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
     if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
@@ -1460,6 +1467,23 @@ int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const vo
     EpiBF16 e{(bf16*)C, ldc, N, (const bf16*)R, ldr};
     OPCK(launch_gemm(p, e, s, cfg));
   }
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_gemm_glu(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
+                    int64_t lda2, const void* B2, int64_t ldb2, int M, int I, int K1, int K2,
+                    void* GU, int64_t ldgu, void* H, int64_t ldh, void* stream) {
+  if (K1 % 8 || K2 % 8 || lda % 8 || ldb % 8 || (K2 && (lda2 % 8 || ldb2 % 8)) || ldgu % 8 ||
+      (H && ldh % 8) || I % 64 || I <= 0 || M < 0 ||
+      !aligned16(A, B, A2, B2, GU, H))
+    return fail(nullptr, "dsb_op_gemm_glu: I a multiple of 64; K, leading dims multiples of 8");
+  GemmProblem p{(const bf16*)A, lda, (const bf16*)B, ldb, (const bf16*)A2, lda2,
+                (const bf16*)B2, ldb2, M, 2 * I, K1, K2, nullptr};
+  p.glu_half = I;
+  EpiGLU e{(bf16*)GU, ldgu, (bf16*)H, ldh, I};
+  hipStream_t s = (hipStream_t)stream;
+  OPCK(launch_gemm(p, e, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
 }

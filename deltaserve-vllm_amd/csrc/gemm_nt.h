@@ -51,6 +51,12 @@ struct GemmProblem {
   long ldb2;
   int M, N, K1, K2;
   const int* M_dev;  // optional device-resident row count (min with M)
+  // Gated-unit layout (0 = off): B (and B2) hold 2·glu_half rows, gate rows
+  // then up rows. The tile's output columns are fed so that each wave's
+  // first TN/2 columns are gate features f .. f+TN/2-1 and its last TN/2 the
+  // up features of the same f, so an epilogue sees both halves of a feature
+  // (EpiGLU). N = 2·glu_half; glu_half a multiple of BN/2.
+  int glu_half = 0;
 };
 
 DSB_DEV void tile_map(int bid, int nbm, int nbn, int& pm, int& pn) {
@@ -201,16 +207,36 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     return make_rsrc(base, bytes);
   };
   const int K2 = nk2 ? p.K2 : 0;
+  const bool glu = p.glu_half > 0;
+  // B rows of the tile: rows n0 .. n0+BN-1, or for the gated layout the
+  // gate/up row runs of the tile's BN/2 features (descriptor over all rows)
+  const long bbase = glu ? 0 : n0;
+  const int brows = glu ? p.N : rowsB;
   const u32x4 dA1 = rsrc(p.A + (long)m0 * p.lda, p.lda, rowsA, p.K1);
-  const u32x4 dB1 = rsrc(p.B + (long)n0 * p.ldb, p.ldb, rowsB, p.K1);
+  const u32x4 dB1 = rsrc(p.B + bbase * p.ldb, p.ldb, brows, p.K1);
   const u32x4 dA2 = rsrc(nk2 ? p.A2 + (long)m0 * p.lda2 : p.A, p.lda2, rowsA, K2);
-  const u32x4 dB2 = rsrc(nk2 ? p.B2 + (long)n0 * p.ldb2 : p.B, p.ldb2, rowsB, K2);
-  // lane byte offset of its first row; load j adds j·8·NW rows
+  const u32x4 dB2 = rsrc(nk2 ? p.B2 + bbase * p.ldb2 : p.B, p.ldb2, brows, K2);
+  // lane byte offset of its first row; A load j adds j·8·NW rows, B load j
+  // starts at row brow0(j) of the descriptor (uniform)
   const int rw = 8 * wave + lrow;
-  const int voA1 = (rw * (int)p.lda + lch * 8) * 2, voB1 = (rw * (int)p.ldb + lch * 8) * 2;
-  const int voA2 = (rw * (int)p.lda2 + lch * 8) * 2, voB2 = (rw * (int)p.ldb2 + lch * 8) * 2;
-  const int stA1 = 16 * NW * (int)p.lda, stB1 = 16 * NW * (int)p.ldb;  // bytes per 8·NW rows
-  const int stA2 = 16 * NW * (int)p.lda2, stB2 = 16 * NW * (int)p.ldb2;
+  const int voA1 = (rw * (int)p.lda + lch * 8) * 2, voB1 = (lrow * (int)p.ldb + lch * 8) * 2;
+  const int voA2 = (rw * (int)p.lda2 + lch * 8) * 2, voB2 = (lrow * (int)p.ldb2 + lch * 8) * 2;
+  const int stA1 = 16 * NW * (int)p.lda;  // bytes per 8·NW rows
+  const int stA2 = 16 * NW * (int)p.lda2;
+  auto brow0 = [&](int jb) {
+    const int r = 8 * (wave + jb * NW);  // LDS row of the block
+    if (!glu) return r;
+    constexpr int HF = TN / 2;                // features per wave column
+    const int wcol = r / TN, c = r % TN;      // wave column, column within it
+    const int f = pn * (BN / 2) + wcol * HF + (c % HF);
+    return c < HF ? f : p.glu_half + f;
+  };
+  int boff1[IB], boff2[IB];
+#pragma unroll
+  for (int jb = 0; jb < IB; ++jb) {
+    boff1[jb] = brow0(jb) * (int)p.ldb * 2;
+    boff2[jb] = brow0(jb) * (int)p.ldb2 * 2;
+  }
   // OR-ed into the offset of chunks past K: beyond any descriptor, loads zero
   constexpr int OOB = 0x7ff00000;
   const unsigned lds0 = lds_addr(smem);
@@ -221,7 +247,8 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   // zeros without touching memory.
   struct Fill {
     u32x4 dA, dB;
-    int voA, voB, stA, stB;
+    int voA, voB, stA;
+    bool s1;
     unsigned dst;
   };
   auto make_fill = [&](int kt, int slot) {
@@ -235,7 +262,7 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     f.voA = (s1 ? voA1 : voA2) + kb;
     f.voB = (s1 ? voB1 : voB2) + kb;
     f.stA = s1 ? stA1 : stA2;
-    f.stB = s1 ? stB1 : stB2;
+    f.s1 = s1;
     f.dst = lds0 + (unsigned)(slot * SE * 2) + (unsigned)(8 * wave * BK * 2);
     return f;
   };
@@ -243,7 +270,8 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     if (j < IA)
       lds_dma16(f.dA, f.voA + j * f.stA, f.dst + j * 8 * NW * BK * 2);
     else
-      lds_dma16(f.dB, f.voB + (j - IA) * f.stB, f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+      lds_dma16(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]),
+                f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
   };
 
   f32x16 acc[FM][FN];
@@ -350,6 +378,67 @@ struct EpiBF16 {
   }
 };
 
+// Gated unit (GemmProblem::glu_half = I): the wave's first TN/2 columns are
+// gate features f .. f+TN/2-1, the last TN/2 the up features of the same f.
+// Writes gate and up (bf16, as EpiBF16 would: GU[m, f] and GU[m, I + f]) and,
+// when H is set, H[m, f] = bf16(silu(gate)·up) from the bf16-rounded halves.
+struct EpiGLU {
+  bf16* GU;
+  long ldgu;
+  bf16* H;
+  long ldh;
+  int I;
+  template <int FM, int FN, int WM, int WN>
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
+    constexpr int TN = FN * 32, HF = TN / 2, PITCH = TN + 4, CG = HF / 8, RPI = 64 / CG;
+    static_assert(FN % 2 == 0 && 64 % CG == 0, "gate/up halves of 32-column fragments");
+    float* buf = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int rsub = lane / CG, cg = lane % CG;
+    // nw = n0 + wn·TN is the tile's output column base; the features start at
+    // (n0 / BN)·(BN / 2) + wn·HF, i.e. nw / 2
+    const int f0 = nw / 2;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      if (mw + fm * 32 >= M) break;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                           acc[fm][fn][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(buf + lr * PITCH + fn * 32 + 8 * g + 4 * lh) = v;
+        }
+#pragma unroll
+      for (int it = 0; it < 32 / RPI; ++it) {
+        const int row = it * RPI + rsub;
+        const int m = mw + fm * 32 + row;
+        const float* gp = buf + row * PITCH + cg * 8;
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(gp);
+        const f32x4 g1 = *reinterpret_cast<const f32x4*>(gp + 4);
+        const f32x4 u0 = *reinterpret_cast<const f32x4*>(gp + HF);
+        const f32x4 u1 = *reinterpret_cast<const f32x4*>(gp + HF + 4);
+        if (m >= M) continue;
+        float gv[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+        float uv[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+        const int f = f0 + cg * 8;
+        const u32x4 gb = pack8(gv), ub = pack8(uv);
+        stg128(GU + (long)m * ldgu + f, gb);
+        stg128(GU + (long)m * ldgu + I + f, ub);
+        if (H) {
+          float gr[8], ur[8], o[8];
+          unpack8(gb, gr);
+          unpack8(ub, ur);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = gr[e] / (1.f + __expf(-gr[e])) * ur[e];
+          stg128(H + (long)m * ldh + f, pack8(o));
+        }
+      }
+    }
+  }
+};
+
 // C (+)= acc, fp32 out.
 struct EpiF32 {
   float* C;
@@ -422,10 +511,17 @@ inline GemmCfg pick_gemm_cfg(int M, int N) {
 template <class Epi>
 hipError_t launch_gemm(const GemmProblem& p, const Epi& e, hipStream_t s, int cfg = -1) {
   if (cfg < 0) cfg = pick_gemm_cfg(p.M, p.N);
-  switch (cfg) {
-    case GEMM_BIG: return launch_gemm_cfg<256, 256, 2, 2>(p, e, s);
-    case GEMM_MID: return launch_gemm_cfg<128, 128, 2, 2>(p, e, s);
-    default: return launch_gemm_cfg<64, 64, 2, 2>(p, e, s);
+  if constexpr (std::is_same<Epi, EpiGLU>::value) {
+    // the gated layout needs two 32-column fragments per wave half
+    if (cfg == GEMM_BIG && p.glu_half % 128 == 0) return launch_gemm_cfg<256, 256, 2, 2>(p, e, s);
+    if (p.glu_half % 64 != 0) return hipErrorInvalidValue;
+    return launch_gemm_cfg<128, 128, 2, 2>(p, e, s);
+  } else {
+    switch (cfg) {
+      case GEMM_BIG: return launch_gemm_cfg<256, 256, 2, 2>(p, e, s);
+      case GEMM_MID: return launch_gemm_cfg<128, 128, 2, 2>(p, e, s);
+      default: return launch_gemm_cfg<64, 64, 2, 2>(p, e, s);
+    }
   }
 }
 

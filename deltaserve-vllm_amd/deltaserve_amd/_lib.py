@@ -14,7 +14,9 @@ from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int, c_in
                     c_int64, c_uint32, c_void_p)
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
-LIB_PATH = os.path.join(LIB_DIR, "libdsb.so")
+# DSB_LIB overrides the library file (e.g. a build kept elsewhere for an A/B
+# timing); the in-tree build is the default.
+LIB_PATH = os.environ.get("DSB_LIB") or os.path.join(LIB_DIR, "libdsb.so")
 
 ABI_VERSION = 1
 FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
@@ -97,6 +99,9 @@ _SIGS = {
     "dsb_op_gemm": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                             c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p,
                             c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p]),
+    "dsb_op_gemm_glu": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int64,
+                                c_void_p, c_int64, c_void_p]),
     "dsb_op_rmsnorm": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int,
                                c_int, c_float, c_void_p]),
     "dsb_op_rmsnorm_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int64, c_void_p,

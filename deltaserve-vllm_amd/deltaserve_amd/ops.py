@@ -88,6 +88,24 @@ def gemm_nt(A, B, A2=None, B2=None, out_dtype=BF16, R=None, out=None, accumulate
     return out
 
 
+def gemm_glu(A, B, A2=None, B2=None, with_h=True):
+    """Gate‖up product with the SwiGLU forward fused (ffn.py:25-26, silu as
+    ffn.py:40-41): returns (GU [M, 2I] = bf16(A·Bᵀ (+ A2·B2ᵀ)) with B = gate
+    rows then up rows, H [M, I] = bf16(silu(gate)·up) or None)."""
+    _dev(A, B, A2, B2)
+    M, K1 = A.shape
+    I = B.shape[0] // 2
+    K2 = 0 if A2 is None else A2.shape[1]
+    GU = torch.empty(M, 2 * I, dtype=BF16, device=A.device)
+    H = torch.empty(M, I, dtype=BF16, device=A.device) if with_h else None
+    L.check(L.load().dsb_op_gemm_glu(_p(A), _ld(A), _p(B), _ld(B), _p(A2),
+                                     0 if A2 is None else _ld(A2), _p(B2),
+                                     0 if B2 is None else _ld(B2), M, I, K1, K2, _p(GU), _ld(GU),
+                                     _p(H), 0 if H is None else _ld(H), _stream()),
+            what="dsb_op_gemm_glu")
+    return GU, H
+
+
 # ---------------------------------------------------------------- norms / rope
 
 def rmsnorm(x, w, eps):

@@ -215,6 +215,14 @@ int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const vo
                 int64_t lda2, const void* B2, int64_t ldb2, int M, int N, int K1, int K2,
                 void* C, int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr,
                 int cfg, void* stream);
+/* Gate‖up product with the SwiGLU forward in its epilogue (the recompute of
+ * ffn.py:25-26, frozen gate_up_proj plus its LoRA term; silu as ffn.py:40-41): GU[m, :] = bf16(A·Bᵀ + A2·B2ᵀ)
+ * with B [2I, K1] = gate rows then up rows (GU = [gate | up], ld ldgu), and,
+ * when H is non-null, H[m, f] = bf16(silu(gate)·up) of the bf16-rounded
+ * halves. I a multiple of 64. */
+int dsb_op_gemm_glu(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
+                    int64_t lda2, const void* B2, int64_t ldb2, int M, int I, int K1, int K2,
+                    void* GU, int64_t ldgu, void* H, int64_t ldh, void* stream);
 /* ops.py:84-88 */
 int dsb_op_rmsnorm(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int rows,
                    int D, float eps, void* stream);

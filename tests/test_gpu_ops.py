@@ -72,6 +72,32 @@ def test_gemm_strided_views():
     assert max_rel(out, A.float().cpu() @ B.float().cpu().t()) < 1e-5
 
 
+@pytest.mark.parametrize("M,I,K,K2", [(700, 512, 256, 16), (8192, 1536, 512, 32),
+                                      (333, 192, 128, 0), (64, 128, 1024, 48)])
+def test_gemm_glu(M, I, K, K2):
+    """Gate‖up with the SwiGLU forward in the epilogue (256- and 128-wide tiles):
+    GU against an fp32 product, H exactly silu(gate)·up of the returned halves."""
+    from deltaserve_amd import ops
+    A = _bf(_rnd(M, K, seed=21))
+    B = _bf(_rnd(2 * I, K, seed=22))
+    A2 = _bf(_rnd(M, K2, seed=23)) if K2 else None
+    B2 = _bf(_rnd(2 * I, K2, seed=24)) if K2 else None
+    ref = A.float() @ B.float().t()
+    if K2:
+        ref += A2.float() @ B2.float().t()
+    GU, H = ops.gemm_glu(A.to(DEV), B.to(DEV), None if A2 is None else A2.to(DEV),
+                         None if B2 is None else B2.to(DEV))
+    assert max_rel(GU, ref) < 8e-3
+    g, u = GU[:, :I].float(), GU[:, I:].float()
+    want = (g * torch.sigmoid(g) * u).to(torch.bfloat16)
+    assert max_rel(H, want) < 8e-3
+    # bf16 rounding of the same fp32 value: at most one ulp apart
+    assert ((H.float() - want.float()).abs() <= want.float().abs() * 2 ** -7 + 1e-30).all()
+    GU2, H2 = ops.gemm_glu(A.to(DEV), B.to(DEV), None if A2 is None else A2.to(DEV),
+                           None if B2 is None else B2.to(DEV), with_h=False)
+    assert H2 is None and torch.equal(GU2, GU)
+
+
 def test_rmsnorm_fwd_bwd():
     from deltaserve_amd import ops
     x = _bf(_rnd(77, 1024, seed=11) * 3)
