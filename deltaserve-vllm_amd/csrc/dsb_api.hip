@@ -222,7 +222,7 @@ struct dsb_handle {
   bf16 *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
   bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
   bf16 *g0, *g1, *Ggu, *grm, *gctx, *gqkv;
-  float *gxn2, *gxn1;
+  bf16 *gxn2, *gxn1;  // the FFN / attention input gradients, bf16 as the reference's cdt
   bf16 *normed, *dlog;
   float2* stats;
   float *tgt_logit, *lse_h, *loss_row, *dH;
@@ -808,8 +808,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     {
       GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
                     hg ? ls.AguT : nullptr, 2L * r, N, D, 2 * I, hg ? 2 * r : 0, nd};
-      EpiF32 e{h->gxn2, (long)D, D, 0};
-      CKR(gemm(h, "f32", p, e, st, 4.0, 0.0));
+      EpiBF16 e{h->gxn2, (long)D, D, nullptr, 0};
+      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
     if (hg) {
       const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
@@ -819,8 +819,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       CKR(tn(h, h->Zgu_b + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 10.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(h->resid, D, h->gxn2, true, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(h->resid, D, h->gxn2, false, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
                      nd, D, eps, st));
     }
     if (ho) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_b, r, st));
@@ -860,8 +860,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     {
       GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
                     hq ? ls.AqkvT : nullptr, 3L * r, N, D, W3, hq ? 3 * r : 0, nd};
-      EpiF32 e{h->gxn1, (long)D, D, 0};
-      CKR(gemm(h, "f32", p, e, st, 4.0, 0.0));
+      EpiBF16 e{h->gxn1, (long)D, D, nullptr, 0};
+      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
     if (hq) {
       const dsb_lora_tensors& tq = ls.lora[DSB_PROJ_Q];
@@ -874,8 +874,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
              h->s, st));
     }
     {
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 10.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(x, ldx, h->gxn1, true, D, (const bf16*)ls.w.in_ln, h->grm, D, gnext, D, N,
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(x, ldx, h->gxn1, false, D, (const bf16*)ls.w.in_ln, h->grm, D, gnext, D, N,
                      nd, D, eps, st));
     }
     return 0;
