@@ -615,10 +615,10 @@ int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, i
   TnArgs a{};
   a.P = P; a.ldp = ldp; a.X = X; a.ldx = ldx; a.R = R; a.C = C;
   a.n = h->N; a.n_dev = &h->d_hdr->n; a.work = h->tn_work;
-  // 128-column blocks × token splits: at most two blocks per CU, so the grid
-  // runs in one round
+  // 128-column blocks × token splits: about one block per CU (measured best
+  // at C3 shapes; the grid runs in one round)
   const int cb = (C + 127) / 128;
-  int ns = std::max(1, 512 / cb);
+  int ns = std::max(1, 256 / cb);
   ns = std::min(ns, 32);
   ns = std::min<long>(ns, h->tn_work_elems / ((long)R * C));
   ns = std::min(ns, std::max(1, h->N / 64));

@@ -48,23 +48,25 @@ hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunk
 }
 
 // ------------------------------------------------------------------ skinny NT
-// Z[t, j] = sum_k X[t, k]·B[j, k]. Block: 32 tokens; the X chunk [32 × 128]
-// and the B chunk [16·RB × 128] stream through a direct-to-LDS ring of up to
-// 96 KB (8 stages at RB = 1, so ~84 KB per CU stay in flight; one barrier per
-// chunk); wave w multiplies columns 32w .. 32w+31 of each
-// chunk with 16×16×32 MFMAs (2 token tiles × RB rank tiles) and the four
-// waves' partial sums are added through LDS at the end.
-template <int RB>
+// Z[t, j] = sum_k X[t, k]·B[j, k]. Block: 16·TT tokens (TT = 1 for short
+// rows, so more blocks share each CU and hide each other's ramp-up; TT = 2
+// for long ones); the X chunk [16·TT × 128] and the B chunk [16·RB × 128]
+// stream through a direct-to-LDS ring of up to 96 KB (up to 8 stages; one
+// barrier per chunk); wave w multiplies columns 32w .. 32w+31 of each chunk
+// with 16×16×32 MFMAs (TT token tiles × RB rank tiles) and the four waves'
+// partial sums are added through LDS at the end.
+template <int TT, int RB>
 __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
-  constexpr int XT = 32 * 128, BT = 16 * RB * 128, SE = XT + BT;
+  constexpr int TR = 16 * TT;  // tokens per block
+  constexpr int XT = TR * 128, BT = 16 * RB * 128, SE = XT + BT;
   constexpr int NS = (48 * 1024) / SE < 8 ? (48 * 1024) / SE : 8;  // SE elements = 2·SE bytes
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
-  const int t0 = blockIdx.x * 32;
+  const int t0 = blockIdx.x * TR;
   if (t0 >= N) return;
   __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rows = min(N - t0, 32);
+  const int rows = min(N - t0, TR);
   const bf16* X0 = a.X + (long)t0 * a.ldx;
   const int nc = (a.K + 127) / 128;
   // ranks j0 .. j0 + Rg - 1 of this block (groups of 64 on grid.y)
@@ -73,13 +75,13 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   auto issue = [&](int c, int slot) {
     const int k0 = c * 128, cv = max(min(a.K - k0, 128), 0);
     bf16* d = smem + slot * SE;
-    tile256_dma<32>(cv > 0 ? X0 + k0 : X0, a.ldx, rows, cv, d, w, lane);
+    tile256_dma<TR>(cv > 0 ? X0 + k0 : X0, a.ldx, rows, cv, d, w, lane);
     tile256_dma<16 * RB>(cv > 0 ? Bg + k0 : Bg, a.ldb, Rg, cv, d + XT, w, lane);
   };
-  constexpr int LPS = 2 + RB;  // loads per lane per stage
-  f32x4 acc[2][RB];
+  constexpr int LPS = TT + RB;  // loads per lane per stage
+  f32x4 acc[TT][RB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TT; ++i)
 #pragma unroll
     for (int j = 0; j < RB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   // fragment offsets (bytes): row l%16 of a 16-row tile, columns 32w + 8(l/16)
@@ -93,49 +95,57 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
     lds_barrier();               // chunk c visible; the slot of chunk c-1 is free
     issue(c + NS - 1, (c + NS - 1) % NS);
     const char* st = reinterpret_cast<const char*>(smem + (c % NS) * SE);
-    bf16x8 xf[2], bfr[RB];
+    bf16x8 xf[TT], bfr[RB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) xf[i] = *reinterpret_cast<const bf16x8*>(st + off + i * 16 * 256);
+    for (int i = 0; i < TT; ++i) xf[i] = *reinterpret_cast<const bf16x8*>(st + off + i * 16 * 256);
 #pragma unroll
     for (int j = 0; j < RB; ++j)
       bfr[j] = *reinterpret_cast<const bf16x8*>(st + XT * 2 + off + j * 16 * 256);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TT; ++i)
 #pragma unroll
       for (int j = 0; j < RB; ++j) acc[i][j] = mfma16(bfr[j], xf[i], acc[i][j]);
   }
   wait_vm<0>();
   __syncthreads();
   // acc[i][j]: token 16i + l%16, ranks 16j + 4(l/16) + 0..3 → per-wave partials
-  float* red = reinterpret_cast<float*>(smem);  // [4][32][16·RB + 4]
+  float* red = reinterpret_cast<float*>(smem);  // [4][TR][16·RB + 4]
   constexpr int RP = 16 * RB + 4;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TT; ++i)
 #pragma unroll
     for (int j = 0; j < RB; ++j)
-      *reinterpret_cast<f32x4*>(red + (w * 32 + 16 * i + (lane & 15)) * RP + 16 * j +
+      *reinterpret_cast<f32x4*>(red + (w * TR + 16 * i + (lane & 15)) * RP + 16 * j +
                                 4 * (lane >> 4)) = acc[i][j];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 32 * 16 * RB; idx += 256) {
+  for (int idx = threadIdx.x; idx < TR * 16 * RB; idx += 256) {
     const int tt = idx / (16 * RB), jj = idx % (16 * RB);
     if (tt >= rows || jj >= Rg) continue;
-    const float v = red[tt * RP + jj] + red[(32 + tt) * RP + jj] + red[(64 + tt) * RP + jj] +
-                    red[(96 + tt) * RP + jj];
+    const float v = red[tt * RP + jj] + red[(TR + tt) * RP + jj] + red[(2 * TR + tt) * RP + jj] +
+                    red[(3 * TR + tt) * RP + jj];
     a.Z[(long)(t0 + tt) * a.ldz + j0 + jj] = (bf16)v;
   }
 }
 
-hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s) {
-  if (a.R <= 0 || a.n <= 0) return hipSuccess;
-  const dim3 grid((a.n + 31) / 32, (a.R + 63) / 64);
+template <int TT>
+static hipError_t launch_skinny(const SkinnyArgs& a, hipStream_t s) {
+  const dim3 grid((a.n + 16 * TT - 1) / (16 * TT), (a.R + 63) / 64);
   switch ((std::min(a.R, 64) + 15) / 16) {
-    case 1: hipLaunchKernelGGL(lora_skinny_kernel<1>, grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(lora_skinny_kernel<2>, grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(lora_skinny_kernel<3>, grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(lora_skinny_kernel<4>, grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((lora_skinny_kernel<TT, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((lora_skinny_kernel<TT, 2>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((lora_skinny_kernel<TT, 3>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((lora_skinny_kernel<TT, 4>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s) {
+  if (a.R <= 0 || a.n <= 0) return hipSuccess;
+  // short rows at one rank group of 16: 16-token blocks (twice the blocks, two
+  // per CU); wider rank groups keep 32 tokens so the B chunk is shared by two
+  // token tiles
+  return a.K <= 8192 && a.R <= 16 ? launch_skinny<1>(a, s) : launch_skinny<2>(a, s);
 }
 
 // ------------------------------------------------------------------ TN
