@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   const int tile = blockIdx.x;
   if (tile >= *a.ntiles_dev) return;
   const int kvh = blockIdx.y, G = a.Hq / a.Hkv;
-  const int4 tl = a.tiles[tile];
+  const int4 tl = a.tiles_k[tile];
   const int st = tl.x, L = tl.y, k0 = tl.z;
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
   __shared__ float sLD[2][2][TR];  // [stage][lse | dsum][row]

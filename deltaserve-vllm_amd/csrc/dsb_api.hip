@@ -17,6 +17,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <array>
 #include <mutex>
 #include <string>
@@ -120,6 +121,19 @@ static int pack_cycle(const int32_t* seq_lens, int nseq, int n, int32_t* pos, in
 }
 
 static int max_tiles_for(int s_max, int max_seqs) { return (s_max + 127) / 128 + max_seqs; }
+
+// Tile dispatch orders, heaviest first so the last blocks of a launch are
+// short (blocks start roughly in index order): a query tile t0 of the causal
+// pass attends to t0 + 128 keys; a key tile is attended by the L - t0 queries
+// at or after it. Any order gives the same results (tiles write disjoint rows).
+static void order_tiles(const std::vector<int4>& tiles, std::vector<int4>& by_q,
+                        std::vector<int4>& by_k) {
+  by_q = tiles;
+  by_k = tiles;
+  std::stable_sort(by_q.begin(), by_q.end(), [](const int4& a, const int4& b) { return a.z > b.z; });
+  std::stable_sort(by_k.begin(), by_k.end(),
+                   [](const int4& a, const int4& b) { return a.y - a.z > b.y - b.z; });
+}
 
 static void rope_inv_freq_host(int hd, float theta, int type, float factor, float low,
                                float high, float orig, float* out) {
@@ -239,6 +253,7 @@ struct dsb_handle {
   int* d_pos = nullptr;
   int* d_pred = nullptr;
   int4* d_tiles = nullptr;
+  int4* d_tiles_k = nullptr;
   // optimizer
   CastJob* d_jobs = nullptr;
   int2* d_cast_chunks = nullptr;
@@ -401,7 +416,7 @@ int finalize(dsb_handle* h) {
   // step staging: header | positions | pred | tiles
   const size_t off_pos = 64, off_pred = off_pos + ((size_t)N * 4 + 63) / 64 * 64;
   const size_t off_tiles = off_pred + ((size_t)N * 4 + 63) / 64 * 64;
-  h->stage_bytes = off_tiles + (size_t)h->max_tiles * sizeof(int4);
+  h->stage_bytes = off_tiles + 2 * (size_t)h->max_tiles * sizeof(int4);  // query, key orders
   CK(hipHostMalloc(&h->h_stage, h->stage_bytes, hipHostMallocDefault));
   memset(h->h_stage, 0, h->stage_bytes);
   char* ds = nullptr;
@@ -411,6 +426,7 @@ int finalize(dsb_handle* h) {
   h->d_pos = reinterpret_cast<int*>(ds + off_pos);
   h->d_pred = reinterpret_cast<int*>(ds + off_pred);
   h->d_tiles = reinterpret_cast<int4*>(ds + off_tiles);
+  h->d_tiles_k = h->d_tiles + h->max_tiles;
 
   // LoRA bf16 operand copies + cast jobs + optimizer tensor table.
   std::vector<CastJob> jobs;
@@ -713,7 +729,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     at.dq = h->gqkv; at.lddq = W3;
     at.dk = h->gqkv + q; at.lddk = W3;
     at.dv = h->gqkv + q + kv; at.lddv = W3;
-    at.tiles = h->d_tiles; at.ntiles_dev = &h->d_hdr->ntiles; at.max_tiles = h->max_tiles;
+    at.tiles = h->d_tiles; at.tiles_k = h->d_tiles_k; at.ntiles_dev = &h->d_hdr->ntiles;
+    at.max_tiles = h->max_tiles;
     at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
     // one causal attention matmul = Hq·Hd·S flops (S = sum L(L+1), unmasked pairs ×2)
     const double au = Hq * 128.0;
@@ -976,7 +993,11 @@ int step_prepare(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float 
                             &tiles);
   if (nv < 0) return fail(h, "dsb_step: seq_lens must be non-negative and sum to n");
   if ((int)tiles.size() > h->max_tiles) return fail(h, "dsb_step: too many attention tiles");
-  memcpy(hs + off_tiles, tiles.data(), tiles.size() * sizeof(int4));
+  std::vector<int4> by_q, by_k;
+  order_tiles(tiles, by_q, by_k);
+  memcpy(hs + off_tiles, by_q.data(), by_q.size() * sizeof(int4));
+  memcpy(hs + off_tiles + (size_t)h->max_tiles * sizeof(int4), by_k.data(),
+         by_k.size() * sizeof(int4));
   StepHdr hdr{};
   hdr.n = n;
   hdr.ntiles = (int)tiles.size();
@@ -1563,16 +1584,21 @@ int attn_setup(const int32_t* seq_lens, int nseq, TmpDev& tmp, AttnArgs& a, int*
   for (int i = 0; i < nseq; ++i) n += seq_lens[i];
   if (pack_cycle(seq_lens, nseq, (int)n, nullptr, nullptr, &tiles) < 0)
     return fail(nullptr, "attention: bad seq_lens");
-  int4* dt = tmp.alloc<int4>(tiles.size() + 1);
+  std::vector<int4> by_q, by_k;
+  order_tiles(tiles, by_q, by_k);
+  int4* dt = tmp.alloc<int4>(2 * tiles.size() + 2);
   int* dn = tmp.alloc<int>(2);
   if (!dt || !dn) return fail(nullptr, "attention: hipMalloc failed");
   int hv[2] = {(int)tiles.size(), (int)n};
   if (!tiles.empty() &&
-      hipMemcpy(dt, tiles.data(), tiles.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess)
+      (hipMemcpy(dt, by_q.data(), by_q.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess ||
+       hipMemcpy(dt + tiles.size(), by_k.data(), by_k.size() * sizeof(int4),
+                 hipMemcpyHostToDevice) != hipSuccess))
     return fail(nullptr, "attention: copy failed");
   if (hipMemcpy(dn, hv, sizeof(hv), hipMemcpyHostToDevice) != hipSuccess)
     return fail(nullptr, "attention: copy failed");
   a.tiles = dt;
+  a.tiles_k = dt + tiles.size();
   a.ntiles_dev = dn;
   a.max_tiles = (int)tiles.size();
   a.n_dev = dn + 1;

@@ -43,7 +43,8 @@ struct AttnArgs {
   bf16* dq; long lddq;       // bwd out
   bf16* dk; long lddk;
   bf16* dv; long lddv;
-  const int4* tiles;
+  const int4* tiles;          // {start, L, t0, 0} per 128-row tile, heaviest query tile first
+  const int4* tiles_k;        // the same tiles, heaviest key tile first (dK/dV pass)
   const int* ntiles_dev;
   int max_tiles;
   int Hq, Hkv;
