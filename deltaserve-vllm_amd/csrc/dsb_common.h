@@ -95,6 +95,9 @@ DSB_DEV void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Wait for every outstanding LDS access (and scalar memory load) of the wave.
+DSB_DEV void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // Workgroup barrier without a memory fence (a fence would wait for every
 // outstanding load, including the prefetched stages); the empty asm statements
 // keep the compiler from moving memory accesses across it.

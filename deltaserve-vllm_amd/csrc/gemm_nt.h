@@ -11,15 +11,20 @@
 // fetched by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds; 8 lanes
 // cover one row, so every request is a whole 128-byte line) into one of two
 // LDS stages. Each wave owns a (BM/WM)×(BN/WN) sub-tile of
-// v_mfma_f32_32x32x16_bf16 accumulators. Per K step (four 16-deep slices):
-//   read slices 0-1 → MFMAs of slice 0 (+ half of the next stage's loads) →
-//   read slice 2 → MFMAs of slice 1 (+ the other half) → read slice 3 →
-//   MFMAs of slices 2, 3 → wait for the own loads → barrier.
+// v_mfma_f32_32x32x16_bf16 accumulators. Per K step (four 16-deep slices,
+// slice 0 already in registers): MFMAs of slice s, with the fragment reads
+// of slice s+1 issued one after each of the first MFMAs and the stage loads
+// one after each of the later ones; before the last slice: wait for the own
+// loads and reads → barrier → MFMAs of slice 3 with the reads of slice 0 of
+// stage kt+1 and the first half of stage kt+2's loads (the second half goes
+// with slice 0 of the next step). A wave issues at most one instruction every
+// few cycles, so anything issued in bursts between MFMAs idles the matrix
+// pipe; one or two instructions between MFMAs issue in the shadow of the
+// previous MFMA.
 // The one barrier per step publishes stage kt+1 (every wave's loads landed)
-// and retires stage kt (every wave's reads of it were consumed by its
-// MFMAs), so the next step can fill that slot. Loads issue one at a time
-// between MFMAs; past the end of K they zero-fill the slot without touching
-// memory, so the waits are constants.
+// and retires stage kt (every wave's reads of it returned), so the loads
+// after it can fill that slot. Past the end of K the loads zero-fill the slot
+// without touching memory, so the waits are constants.
 //
 // LDS layout per stage and operand: rows of 128 B (64 bf16) as eight 16-byte
 // chunks; chunk c of row r sits in slot c ^ f(r), f(r) = ((r>>1)&7) ^ ((r&1)<<2),
@@ -297,31 +302,73 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     for (int fn = 0; fn < FN; ++fn)
       bfr[buf][fn] = *reinterpret_cast<const bf16x8*>(b + brow + ch + fn * 32 * BK);
   };
-  // MFMAs of one slice, with loads j0 .. j0+nj-1 of `f` spread among them:
-  // their scalar set-up and issue run in the MFMA shadow.
-  auto mma = [&](int buf, const Fill& f, int j0, int nj) {
-    constexpr int NM = FM * FN;
-    const int every = nj > 0 ? (NM / nj > 0 ? NM / nj : 1) : NM + 1;
-    int j = j0;
+  // Fragment i of slice s into buffer `buf`: A fragment i (i < FM), else B
+  // fragment i - FM.
+  auto read_one = [&](const bf16* b, int s, int buf, int i) {
+    const int ch = ((2 * s + lh) ^ g) << 3;
+    if (i < FM)
+      af[buf][i] = *reinterpret_cast<const bf16x8*>(b + arow + ch + i * 32 * BK);
+    else
+      bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(b + brow + ch + (i - FM) * 32 * BK);
+  };
+  // MFMAs of the slice held in `buf`. The FM+FN fragment reads of the next
+  // slice (slice ns of the stage at nb, into buffer nbuf) go one after each
+  // of the first MFMAs, then loads j0 .. j0+nj-1 of `f` one after each of
+  // the following ones. A wave issues at most one instruction every few
+  // cycles, so bursts of reads or loads between MFMAs would leave the matrix
+  // pipe idle; one or two instructions between MFMAs issue while the
+  // previous MFMA runs.
+  auto mma = [&](int buf, const bf16* nb, int ns, int nbuf, const Fill& f, int j0, int nj) {
+    constexpr int NM = FM * FN, NR = FM + FN;
+    int r = 0, j = j0;
 #pragma unroll
     for (int t = 0; t < NM; ++t) {
       const int fm = t / FN, fn = t % FN;
       acc[fm][fn] = mfma32(bfr[buf][fn], af[buf][fm], acc[fm][fn]);
-      if (t % every == every - 1 && j < j0 + nj) {
+      if (r < NR) {
+        __builtin_amdgcn_sched_barrier(0);
+        read_one(nb, ns, nbuf, r++);
+        __builtin_amdgcn_sched_barrier(0);
+      } else if (j < j0 + nj) {
         __builtin_amdgcn_sched_barrier(0);
         issue_one(f, j++);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
+    for (int rr = 0; rr < NR; ++rr)
+      if (rr >= r) read_one(nb, ns, nbuf, rr);
+#pragma unroll
     for (int jj = 0; jj < IAB; ++jj)
       if (jj >= j && jj < j0 + nj) issue_one(f, jj);
   };
+  // Loads of K tile kt (< nk1, first segment) into slot `slot`: the
+  // descriptors and row offsets are the loop-invariant ones of segment 1.
+  auto make_fill1 = [&](int kt, int slot) {
+    Fill f;
+    const int k0 = kt * BK;
+    const int kb = (k0 * 2) | ((k0 + lch * 8 < p.K1) ? 0 : OOB);
+    f.dA = dA1;
+    f.dB = dB1;
+    f.voA = voA1 + kb;
+    f.voB = voB1 + kb;
+    f.stA = stA1;
+    f.s1 = true;
+    f.dst = lds0 + (unsigned)(slot * SE * 2) + (unsigned)(8 * wave * BK * 2);
+    return f;
+  };
 
   // Two stages of BK = 64. Step kt computes on slot kt&1 while the loads of
-  // stage kt+1 fill the other slot; the step ends with the wave's own loads
-  // landed and one barrier, which both publishes stage kt+1 and retires
-  // stage kt (every wave's fragment reads of it were consumed by its MFMAs).
+  // stage kt+1 fill the other slot. The step's barrier sits before its last
+  // slice: by then every wave has its own loads of stage kt+1 landed
+  // (vmcnt 0) and its fragment reads of stage kt returned (lgkmcnt 0), so the
+  // barrier both publishes stage kt+1 and frees slot kt&1. After it, the
+  // first slice of stage kt+1 is read and the loads of stage kt+2 start
+  // while the MFMAs of the last slice of stage kt run, so neither the LDS
+  // read latency nor the loads' set-up leaves the matrix pipe idle at the
+  // step boundary. The loads of a stage are split between the last slice of
+  // one step and the first slice of the next.
+  constexpr int H1 = IAB / 2;
   {
     const Fill f = make_fill(0, 0);
 #pragma unroll
@@ -329,29 +376,40 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   }
   wait_vm<0>();
   lds_barrier();
+  read(smem, 0, 0);
+  Fill fn = make_fill(1, 1);
+#pragma unroll
+  for (int j = 0; j < H1; ++j) issue_one(fn, j);
 
-  for (int kt = 0; kt < nk; ++kt) {
+  auto step = [&](int kt, auto&& mk) {
     const int cur = kt & 1;
     const bf16* b = smem + cur * SE;
-    const Fill f = make_fill(kt + 1, cur ^ 1);
-    read(b, 0, 0);
-    read(b, 1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mma(0, f, 0, IAB / 2);
+    mma(0, b, 1, 1, fn, H1, IAB - H1);
     __builtin_amdgcn_sched_barrier(0);
-    read(b, 2, 0);
+    const Fill fnn = mk(kt + 2, cur);
+    mma(1, b, 2, 0, fn, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mma(1, f, IAB / 2, IAB - IAB / 2);
+    mma(0, b, 3, 1, fn, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    read(b, 3, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(0, f, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(1, f, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkm0();
     wait_vm<0>();
     lds_barrier();
-  }
+    fn = fnn;
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, smem + (cur ^ 1) * SE, 0, 0, fn, 0, H1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Steps whose prefetch (tile kt+2) stays in segment 1 use the invariant
+  // segment-1 fill; the last few steps select the segment per tile.
+  const int nfast = max(0, min(nk, nk1 - 2));
+  int kt = 0;
+  for (; kt < nfast; ++kt) step(kt, make_fill1);
+  for (; kt < nk; ++kt) step(kt, make_fill);
+  // the last step's loads (zero fills past K) land before the epilogue
+  // reuses the LDS
+  wait_vm<0>();
+  lds_barrier();
 
   epi.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
                                    (void*)smem);
