@@ -140,12 +140,15 @@ DSB_DEV void for_each_row8(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, i
 }
 
 // 8 values to bf16 at p[0 .. min(8, lim)); 16-byte store when whole and aligned.
+// The 16-byte store is non-temporal: the outputs of a whole wave of tiles land
+// at once, and streaming them keeps them from evicting the A/B panels the
+// next tiles read from L2.
 DSB_DEV void store8_bf16(bf16* p, const float* v, int lim) {
   if (lim >= 8 && ((unsigned long)p & 15) == 0) {
     bf16x8 o;
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = (bf16)v[i];
-    *reinterpret_cast<bf16x8*>(p) = o;
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(p));
   } else {
     for (int i = 0; i < 8 && i < lim; ++i) p[i] = (bf16)v[i];
   }
