@@ -646,6 +646,28 @@ int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, i
   return 0;
 }
 
+// grad_Z = bf16(G·(s·B)) into gZ and grad_B = s·Gᵀ·Z into gB [C, r] from one
+// pass over the adapter's output gradient G [n, C] (lora_dual). Returns 1
+// when the shape is outside what the fused kernel handles (the caller then
+// runs lora_skinny and lora_tn).
+int dual(dsb_handle* h, const bf16* G, long ldg, int C, const bf16* Z, long ldz, const bf16* BT,
+         int r, bf16* gZ, long ldgz, float* gB, hipStream_t s) {
+  if (!lora_dual_supported(r, r, C)) return 1;
+  const int ncb = (C + 511) / 512;
+  const long ywork = (long)ncb * h->N * r;
+  int ns = std::max(1, std::min(256 / ncb, h->N / 64));
+  while (ns > 1 && ywork + (long)ns * C * r > h->tn_work_elems) --ns;
+  if (ywork + (long)ns * C * r > h->tn_work_elems) return 1;
+  DualArgs a{};
+  a.X = G; a.ldx = ldg; a.P = Z; a.ldp = ldz; a.W = BT; a.ldw = C;
+  a.R1 = r; a.R2 = r; a.C = C;
+  a.n = h->N; a.n_dev = &h->d_hdr->n; a.n_alloc = h->N; a.nsplit = ns;
+  a.work = h->tn_work; a.Y = gZ; a.ldy = ldgz; a.out = gB; a.scale = h->s;
+  KScope ks(h, s, "lora_dual", 4.0 * r * C, 0, 0, 2.0 * C + 4.0 * r, 0, 6.0 * r * C);
+  LK(lora_dual(a, s));
+  return 0;
+}
+
 // One segment of the cycle on stream st. Segments: 0 = RoPE table, LoRA
 // operand casts and the LM head (head.py:42-100); 1 .. L = decoder layer
 // L - seg, forward recompute + backward; L + 1 = per-layer clip, AdamW and the
@@ -801,7 +823,15 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     if (hd) CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
 
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
-    if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
+    // grad_Z and grad_B of down from one pass over g (lora_dual), else the
+    // skinny product here and the TN reduction after the dX product
+    int dual_d = 1;
+    if (hd) {
+      dual_d = dual(h, g, D, D, h->Zd_b, r, ls.BTd, r, h->gZd_b, r,
+                    ls.lora[DSB_PROJ_DOWN].gB, st);
+      if (dual_d < 0) return -1;
+      if (dual_d) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
+    }
     {
       // gh = g·W_down (+ gZ_d·A_d): grad wrt h = silu(gate)·up
       GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
@@ -816,11 +846,17 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
       CKR(tn(h, h->gZd_b, r, h->hb, I, r, I, t.gA, nullptr, nullptr, r, 0, 1.f, st));
-      CKR(tn(h, h->Zd_b, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
+      if (dual_d) CKR(tn(h, h->Zd_b, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
+    int dual_g = 1, dual_u = 1;
     if (hg) {
-      CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
-      CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
+      dual_g = dual(h, h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, r, h->gZgu_b, 2L * r,
+                    ls.lora[DSB_PROJ_GATE].gB, st);
+      dual_u = dual(h, h->Ggu + I, 2L * I, I, h->Zgu_b + r, 2L * r, ls.BTu, r, h->gZgu_b + r,
+                    2L * r, ls.lora[DSB_PROJ_UP].gB, st);
+      if (dual_g < 0 || dual_u < 0) return -1;
+      if (dual_g) CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
+      if (dual_u) CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
     }
     {
       GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
@@ -832,15 +868,24 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
       const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
       CKR(tn(h, h->gZgu_b, 2 * r, h->xn2, D, 2 * r, D, tg.gA, tu.gA, nullptr, r, 0, 1.f, st));
-      CKR(tn(h, h->Zgu_b, 2 * r, h->Ggu, 2L * I, r, I, tg.gB, nullptr, nullptr, r, 1, h->s, st));
-      CKR(tn(h, h->Zgu_b + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1, h->s, st));
+      if (dual_g)
+        CKR(tn(h, h->Zgu_b, 2 * r, h->Ggu, 2L * I, r, I, tg.gB, nullptr, nullptr, r, 1, h->s, st));
+      if (dual_u)
+        CKR(tn(h, h->Zgu_b + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1,
+               h->s, st));
     }
     {
       KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
       LK(rmsnorm_bwd(h->resid, D, h->gxn2, false, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
                      nd, D, eps, st));
     }
-    if (ho) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_b, r, st));
+    int dual_o = 1;
+    if (ho) {
+      dual_o = dual(h, h->grm, D, D, h->Zo_b, r, ls.BTo, r, h->gZo_b, r, ls.lora[DSB_PROJ_O].gB,
+                    st);
+      if (dual_o < 0) return -1;
+      if (dual_o) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_b, r, st));
+    }
     {
       GemmProblem p{h->grm, (long)D, ls.oT, (long)D, ho ? h->gZo_b : nullptr, (long)r,
                     ho ? ls.AoT : nullptr, (long)r, N, q, D, ho ? r : 0, nd};
@@ -850,7 +895,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     if (ho) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
       CKR(tn(h, h->gZo_b, r, h->ctx, q, r, q, t.gA, nullptr, nullptr, r, 0, 1.f, st));
-      CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
+      if (dual_o) CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
       KScope ks(h, st, "attn_dsum", 0, 0, 0, 6.0 * q + 4.0 * Hq, 0, 0);
@@ -869,10 +914,18 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
                   h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
+    int dual_q = 1, dual_k = 1, dual_v = 1;
     if (hq) {
-      CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
-      CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_b + r, 3 * r, st));
-      CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_b + 2 * r, 3 * r, st));
+      dual_q = dual(h, h->gqkv, W3, q, h->Zqkv_b, 3L * r, ls.BTq, r, h->gZqkv_b, 3L * r,
+                    ls.lora[DSB_PROJ_Q].gB, st);
+      dual_k = dual(h, h->gqkv + q, W3, kv, h->Zqkv_b + r, 3L * r, ls.BTk, r, h->gZqkv_b + r,
+                    3L * r, ls.lora[DSB_PROJ_K].gB, st);
+      dual_v = dual(h, h->gqkv + q + kv, W3, kv, h->Zqkv_b + 2 * r, 3L * r, ls.BTv, r,
+                    h->gZqkv_b + 2 * r, 3L * r, ls.lora[DSB_PROJ_V].gB, st);
+      if (dual_q < 0 || dual_k < 0 || dual_v < 0) return -1;
+      if (dual_q) CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
+      if (dual_k) CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_b + r, 3 * r, st));
+      if (dual_v) CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_b + 2 * r, 3 * r, st));
     }
     {
       GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
@@ -885,10 +938,14 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       const dsb_lora_tensors& tk = ls.lora[DSB_PROJ_K];
       const dsb_lora_tensors& tv = ls.lora[DSB_PROJ_V];
       CKR(tn(h, h->gZqkv_b, 3 * r, h->xn1, D, 3 * r, D, tq.gA, tk.gA, tv.gA, r, 0, 1.f, st));
-      CKR(tn(h, h->Zqkv_b, 3 * r, h->gqkv, W3, r, q, tq.gB, nullptr, nullptr, r, 1, h->s, st));
-      CKR(tn(h, h->Zqkv_b + r, 3 * r, h->gqkv + q, W3, r, kv, tk.gB, nullptr, nullptr, r, 1, h->s, st));
-      CKR(tn(h, h->Zqkv_b + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, tv.gB, nullptr, nullptr, r, 1,
-             h->s, st));
+      if (dual_q)
+        CKR(tn(h, h->Zqkv_b, 3 * r, h->gqkv, W3, r, q, tq.gB, nullptr, nullptr, r, 1, h->s, st));
+      if (dual_k)
+        CKR(tn(h, h->Zqkv_b + r, 3 * r, h->gqkv + q, W3, r, kv, tk.gB, nullptr, nullptr, r, 1,
+               h->s, st));
+      if (dual_v)
+        CKR(tn(h, h->Zqkv_b + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, tv.gB, nullptr, nullptr,
+               r, 1, h->s, st));
     }
     {
       KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
@@ -1723,6 +1780,28 @@ int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, i
   hipStream_t s = (hipStream_t)stream;
   SkinnyArgs a{(const bf16*)X, ldx, (const bf16*)B, ldb, R, K, (bf16*)Z, ldz, n, nullptr};
   OPCK(lora_skinny(a, s));
+  OPCK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dsb_op_lora_dual(const void* G, int64_t ldg, const void* Z, int64_t ldz, const void* BT,
+                     int64_t ldbt, int n, int r, int C, float scale, void* gZ, int64_t ldgz,
+                     float* gB, void* stream) {
+  if (!lora_dual_supported(r, r, C) || ldg % 8 || ldbt % 8 || n < 0)
+    return fail(nullptr, "dsb_op_lora_dual: r must be 16 or 32; C, ldg, ldbt multiples of 8");
+  if (n == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int ncb = (C + 511) / 512;
+  const int ns = std::max(1, std::min(256 / ncb, n / 64));
+  TmpDev tmp;
+  float* work = tmp.alloc<float>((size_t)ncb * n * r + (size_t)ns * C * r);
+  if (!work) return fail(nullptr, "dsb_op_lora_dual: hipMalloc failed");
+  DualArgs a{};
+  a.X = (const bf16*)G; a.ldx = ldg; a.P = (const bf16*)Z; a.ldp = ldz;
+  a.W = (const bf16*)BT; a.ldw = ldbt; a.R1 = r; a.R2 = r; a.C = C;
+  a.n = n; a.n_dev = nullptr; a.n_alloc = n; a.nsplit = ns; a.work = work;
+  a.Y = (bf16*)gZ; a.ldy = ldgz; a.out = gB; a.scale = scale;
+  OPCK(lora_dual(a, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
 }

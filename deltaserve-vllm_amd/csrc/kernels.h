@@ -93,6 +93,26 @@ struct TnArgs {
   float scale;
 };
 hipError_t lora_tn(const TnArgs& a, hipStream_t s);
+// One pass over G [n, C] for the two rank-r products that read it
+// (ops.py:142 grad_Z = gy @ (s·B) and ops.py:144 grad_B = s · gy.t() @ Z):
+//   Y[t, j] = bf16(sum_c G[t, c]·W[j, c])          (W = (s·B)ᵀ [R2, C])
+//   out[c, j] = scale · sum_t P[t, j]·G[t, c]      (P = Z [n, R1], out = grad_B)
+// R1 = 16·RB1 and R2 = 16·RB2 with RB1, RB2 in {1, 2}; C a multiple of 8.
+// work holds ceil(C/512)·n_alloc·R2 + nsplit·C·R1 floats.
+struct DualArgs {
+  const bf16* X; long ldx;  // G
+  const bf16* P; long ldp;  // Z
+  const bf16* W; long ldw;  // (s·B)ᵀ
+  int R1, R2, C;
+  int n; const int* n_dev;
+  int n_alloc;              // row stride of the Y partials (n <= n_alloc)
+  int nsplit;
+  float* work;
+  bf16* Y; long ldy;
+  float* out; float scale;  // out[c, j], row pitch R1
+};
+hipError_t lora_dual(const DualArgs& a, hipStream_t s);
+bool lora_dual_supported(int R1, int R2, int C);
 
 // ---- head.hip
 struct HeadArgs {

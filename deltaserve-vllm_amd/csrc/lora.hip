@@ -284,4 +284,202 @@ hipError_t lora_tn(const TnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ dual
+// One pass over X = G [n, C] for both rank-r products that read it.
+// Block: 512 columns (four 128-column tiles, tile q at the wave-q slot of the
+// chunk) × one token split; 32-token chunks of X and P stream through a
+// 4-stage direct-to-LDS ring (one barrier per chunk).
+//  * TN (grad_B): wave w owns tile w (8 column tiles of 16) and accumulates
+//    Pᵀ·X over the split's tokens with transposed LDS reads, as lora_tn does;
+//    the fp32 partials go to workT[split][c][j].
+//  * skinny (grad_Z): the chunk's two 16-token tiles go to two waves in turn
+//    (token tile tt of chunk k to wave (2k + tt) % 4), each multiplying its
+//    16 rows × 512 columns with the W fragments it holds in registers; the
+//    fp32 partial over the block's columns goes to workY[cb][t][j].
+// Two small kernels reduce the partials in a fixed order (deterministic).
+template <int RB1, int RB2>
+__global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualArgs a) {
+  constexpr int R1 = 16 * RB1, R2 = 16 * RB2;
+  constexpr int XT = 32 * 512, PT = 32 * R1, SE = XT + PT, NS = 4;
+  constexpr int LPS = 8;  // X loads per lane per chunk (+1 P load on waves < RB1)
+  __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
+  int N = a.n;
+  if (a.n_dev) N = min(N, *a.n_dev);
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cb = blockIdx.x, c0 = cb * 512, sp = blockIdx.y;
+  int per = (N + a.nsplit - 1) / a.nsplit;
+  per = (per + 31) & ~31;
+  const int ta = min(N, sp * per), tb = min(N, ta + per);
+  const int nk = (tb - ta + 31) / 32;
+
+  // W fragments for the block's 512 columns: k-step ks covers columns
+  // c0 + 32ks .. +31; lane l holds W row 16j + l%16, columns + 8(l/16) .. +7
+  bf16x8 wf[16][RB2];
+  {
+    const __amdgpu_buffer_rsrc_t wr =
+        make_brsrc(a.W, (int)(((long)(R2 - 1) * a.ldw + a.C) * 2));
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks)
+#pragma unroll
+      for (int j = 0; j < RB2; ++j) {
+        const int row = 16 * j + (lane & 15), col = c0 + 32 * ks + 8 * (lane >> 4);
+        const int off = col < a.C ? (int)(((long)row * a.ldw + col) * 2) : 0x7ff00000;
+        wf[ks][j] = __builtin_bit_cast(bf16x8, buf_load16(wr, off));
+      }
+  }
+  const bool pw = w < RB1;
+  auto issue = [&](int k, int slot) {
+    const int t = ta + k * 32, rv = max(min(tb - t, 32), 0);
+    bf16* d = smem + slot * SE;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int cc = c0 + 128 * q, cv = max(min(a.C - cc, 128), 0);
+      tile256_dma<32>(rv > 0 && cv > 0 ? a.X + (long)t * a.ldx + cc : a.X, a.ldx,
+                      cv > 0 ? rv : 0, cv, d + q * 32 * 128, w, lane);
+    }
+    if (pw) {
+      // P rows of R1 ranks: lane q of load w covers row q / (R1/8), ranks 8·(q % (R1/8))
+      const int qq = w * 64 + lane, per_row = R1 / 8;
+      const int row = qq / per_row, ch = qq % per_row;
+      const int bytes = rv > 0 ? (int)((((long)(rv - 1) * a.ldp) + R1) * 2) : 0;
+      const u32x4 rs = make_rsrc(rv > 0 ? a.P + (long)t * a.ldp : a.P, bytes);
+      const int voff = row < 32 ? (int)(((long)row * a.ldp + ch * 8) * 2) : 0x7ff00000;
+      lds_dma16(rs, voff, lds_addr(d + XT + w * 512));
+    }
+  };
+  f32x4 accT[8][RB1];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < RB1; ++j) accT[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // transposed-read byte offsets (TN): X tile w, row 8g + j/4 (+4), column
+  // 16i + 4(j%4); P row 8g + j/4 (+4), rank 4(j%4) at a row pitch of 2·R1 bytes
+  const int g = lane >> 4, jl = lane & 15;
+  const int xr = 8 * g + (jl >> 2);
+  int xo[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xo[i][h] = (w * 32 * 128 + toff(xr + 4 * h, 16 * i + 4 * (jl & 3))) * 2;
+  const int po = (xr * R1 + 4 * (jl & 3)) * 2;
+  // row-fragment byte offsets (skinny): row l%16 of a 16-row tile, columns 32kk + 8(l/16)
+  int xs[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) xs[kk] = toff(lane & 15, 32 * kk + 8 * (lane >> 4)) * 2;
+  const int ncb = (a.C + 511) / 512;
+  float* workY = a.work;
+  float* workT = a.work + (long)ncb * a.n_alloc * R2;
+
+#pragma unroll
+  for (int k = 0; k < NS - 1; ++k) issue(k, k);
+  for (int k = 0; k < nk; ++k) {
+    if (pw) wait_vm<(NS - 2) * (LPS + 1)>(); else wait_vm<(NS - 2) * LPS>();
+    lds_barrier();  // chunk k visible; the slot of chunk k-1 is free
+    issue(k + NS - 1, (k + NS - 1) % NS);
+    const char* st = reinterpret_cast<const char*>(smem + (k % NS) * SE);
+    bf16x8 pf[RB1];
+#pragma unroll
+    for (int j = 0; j < RB1; ++j) {
+      const char* pp = st + XT * 2 + po + j * 32;
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pp);
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(pp + 4 * R1 * 2));
+      pf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + xo[i][0]));
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + xo[i][1]));
+      const bf16x8 xf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+      for (int j = 0; j < RB1; ++j) accT[i][j] = mfma16(pf[j], xf, accT[i][j]);
+    }
+    const int tt = (w - 2 * k) & 3;  // uniform
+    if (tt < 2) {
+      f32x4 ay[RB2];
+#pragma unroll
+      for (int j = 0; j < RB2; ++j) ay[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const bf16x8 xf =
+              *reinterpret_cast<const bf16x8*>(st + q * 32 * 128 * 2 + tt * 16 * 256 + xs[kk]);
+#pragma unroll
+          for (int j = 0; j < RB2; ++j) ay[j] = mfma16(wf[4 * q + kk][j], xf, ay[j]);
+        }
+      // ay[j]: token 16tt + l%16 of the chunk, ranks 16j + 4(l/16) .. +3
+      const int t = ta + 32 * k + 16 * tt + (lane & 15);
+      if (t < tb) {
+#pragma unroll
+        for (int j = 0; j < RB2; ++j)
+          *reinterpret_cast<f32x4*>(workY + ((long)cb * a.n_alloc + t) * R2 + 16 * j +
+                                    4 * (lane >> 4)) = ay[j];
+      }
+    }
+  }
+  wait_vm<0>();
+  // accT[i][j]: column c0 + 128w + 16i + l%16, ranks 16j + 4(l/16) .. +3
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int col = c0 + 128 * w + 16 * i + (lane & 15);
+    if (col >= a.C) continue;
+#pragma unroll
+    for (int j = 0; j < RB1; ++j)
+      *reinterpret_cast<f32x4*>(workT + ((long)sp * a.C + col) * R1 + 16 * j + 4 * (lane >> 4)) =
+          accT[i][j];
+  }
+}
+
+// Both reductions of lora_dual in one launch, each in a fixed order
+// (deterministic): indices below n_alloc·R2 give Y[t, j] = bf16(sum over the
+// column blocks of the skinny partials) for live tokens t; the next C·R1 give
+// out[c, j] = scale · (sum over the token splits of the TN partials).
+__global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualArgs a) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const long ny = (long)a.n_alloc * a.R2;
+  const int ncb = (a.C + 511) / 512;
+  if (idx < ny) {
+    int N = a.n;
+    if (a.n_dev) N = min(N, *a.n_dev);
+    const int t = (int)(idx / a.R2), j = (int)(idx % a.R2);
+    if (t >= N) return;
+    float s = 0.f;
+    for (int c = 0; c < ncb; ++c) s += a.work[((long)c * a.n_alloc + t) * a.R2 + j];
+    a.Y[(long)t * a.ldy + j] = (bf16)s;
+    return;
+  }
+  const long k = idx - ny;
+  if (k >= (long)a.R1 * a.C) return;
+  const float* wt = a.work + ny * ncb;
+  const int c = (int)(k / a.R1), j = (int)(k % a.R1);
+  float s = 0.f;
+#pragma unroll 8
+  for (int sp = 0; sp < a.nsplit; ++sp) s += wt[((long)sp * a.C + c) * a.R1 + j];
+  a.out[(long)c * a.R1 + j] = s * a.scale;
+}
+
+bool lora_dual_supported(int R1, int R2, int C) {
+  return (R1 == 16 || R1 == 32) && (R2 == 16 || R2 == 32) && C % 8 == 0 && C > 0;
+}
+
+hipError_t lora_dual(const DualArgs& a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  if (!lora_dual_supported(a.R1, a.R2, a.C) || a.n > a.n_alloc || a.nsplit < 1)
+    return hipErrorInvalidValue;
+  const dim3 grid((a.C + 511) / 512, a.nsplit);
+  const int k = (a.R1 / 16 - 1) * 2 + (a.R2 / 16 - 1);
+  switch (k) {
+    case 0: hipLaunchKernelGGL((lora_dual_kernel<1, 1>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((lora_dual_kernel<1, 2>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((lora_dual_kernel<2, 1>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((lora_dual_kernel<2, 2>), grid, dim3(256), 0, s, a); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const long tot = (long)a.n_alloc * a.R2 + (long)a.R1 * a.C;
+  hipLaunchKernelGGL(lora_dual_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
+                     s, a);
+  return hipGetLastError();
+}
+
 }  // namespace dsb

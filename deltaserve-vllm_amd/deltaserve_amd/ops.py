@@ -230,6 +230,20 @@ def lora_skinny(X, B):
     return Z
 
 
+def lora_dual(G, Z, BT, scale=1.0):
+    """ops.py:142 and :144 from one pass over G [n, C]: returns
+    (bf16(G·BTᵀ) [n, r], scale·Gᵀ·Z fp32 [C, r]) for BT = (s·B)ᵀ [r, C]."""
+    _dev(G, Z, BT)
+    n, C = G.shape
+    r = BT.shape[0]
+    gZ = torch.empty(n, r, dtype=BF16, device=G.device)
+    gB = torch.empty(C, r, dtype=torch.float32, device=G.device)
+    L.check(L.load().dsb_op_lora_dual(_p(G), _ld(G), _p(Z), _ld(Z), _p(BT), _ld(BT), n, r, C,
+                                      float(scale), _p(gZ), _ld(gZ), _p(gB), _stream()),
+            what="dsb_op_lora_dual")
+    return gZ, gB
+
+
 def clip_adamw_(ws, gs, ms, vs, groups, lr, step, beta1=0.9, beta2=0.999, eps=1e-8, wd=0.0,
                 max_norm=1.0, clip=True):
     """trainer.py:624-636 + :668 over fp32 CUDA tensors (in place)."""

@@ -238,6 +238,26 @@ def test_lora_skinny(n, R, K):
     assert max_rel(Z, ref) < 8e-3
 
 
+@pytest.mark.parametrize("n,r,C", [(700, 16, 1536), (8192, 16, 14336), (333, 32, 520), (33, 16, 1024),
+                                   (4100, 32, 4096)])
+def test_lora_dual(n, r, C):
+    """One pass over G for grad_Z and grad_B: against fp32 products on the
+    CPU and against the separate skinny / TN kernels."""
+    from deltaserve_amd import ops
+    G = _bf(_rnd(n, C, seed=55)).to(DEV)
+    Z = _bf(_rnd(n, r, seed=56)).to(DEV)
+    BT = _bf(_rnd(r, C, seed=57) * 0.1).to(DEV)
+    gZ, gB = ops.lora_dual(G, Z, BT, scale=2.0)
+    Gc, Zc, Bc = G.float().cpu(), Z.float().cpu(), BT.float().cpu()
+    assert max_rel(gZ, Gc @ Bc.t()) < 8e-3
+    assert max_rel(gB, 2.0 * (Gc.t() @ Zc)) < 1e-5
+    gZ2 = ops.lora_skinny(G, BT)
+    gB2 = torch.empty(C, r, device=DEV)
+    ops.lora_tn(Z, G, r, True, [gB2], scale=2.0)
+    assert max_rel(gZ, gZ2) < 8e-3
+    assert max_rel(gB, gB2) < 1e-5
+
+
 def test_clip_adamw():
     from deltaserve_amd import ops
     shapes = [(8, 64), (96, 8), (8, 4100), (33,)]
