@@ -646,23 +646,32 @@ int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, i
   return 0;
 }
 
-// grad_Z = bf16(G·(s·B)) into gZ and grad_B = s·Gᵀ·Z into gB [C, r] from one
-// pass over the adapter's output gradient G [n, C] (lora_dual). Returns 1
-// when the shape is outside what the fused kernel handles (the caller then
-// runs lora_skinny and lora_tn).
-int dual(dsb_handle* h, const bf16* G, long ldg, int C, const bf16* Z, long ldz, const bf16* BT,
-         int r, bf16* gZ, long ldgz, float* gB, hipStream_t s) {
-  if (!lora_dual_supported(r, r, C)) return 1;
+// Token splits of a lora_dual pass over C columns at rank r, or 0 when the
+// shape is outside what the fused kernel handles (the caller then runs
+// lora_skinny and lora_tn).
+int dual_splits(const dsb_handle* h, int C, int r) {
+  if (!lora_dual_supported(r, r, C)) return 0;
   const int ncb = (C + 511) / 512;
   const long ywork = (long)ncb * h->N * r;
   int ns = std::max(1, std::min(256 / ncb, h->N / 64));
   while (ns > 1 && ywork + (long)ns * C * r > h->tn_work_elems) --ns;
-  if (ywork + (long)ns * C * r > h->tn_work_elems) return 1;
+  return ywork + (long)ns * C * r > h->tn_work_elems ? 0 : ns;
+}
+
+// One lora_dual pass over X [n, C]: Y = bf16(X·Wᵀ) [n, r] and
+// out = scale·Pᵀ·X, as [C, r] (transpose) or [r, C]. For an adapter's output
+// gradient G: W = (s·B)ᵀ, P = Z gives grad_Z and grad_B (scale s, [C, r]).
+// Returns 1 when the shape needs the separate kernels.
+int dual(dsb_handle* h, const bf16* X, long ldx, int C, const bf16* P, long ldp, const bf16* W,
+         int r, bf16* Y, long ldy, float* out, hipStream_t s, float scale, int transpose) {
+  const int ns = dual_splits(h, C, r);
+  if (ns == 0) return 1;
   DualArgs a{};
-  a.X = G; a.ldx = ldg; a.P = Z; a.ldp = ldz; a.W = BT; a.ldw = C;
+  a.X = X; a.ldx = ldx; a.P = P; a.ldp = ldp; a.W = W; a.ldw = C;
   a.R1 = r; a.R2 = r; a.C = C;
   a.n = h->N; a.n_dev = &h->d_hdr->n; a.n_alloc = h->N; a.nsplit = ns;
-  a.work = h->tn_work; a.Y = gZ; a.ldy = ldgz; a.out = gB; a.scale = h->s;
+  a.work = h->tn_work; a.Y = Y; a.ldy = ldy; a.out = out; a.scale = scale;
+  a.transpose_out = transpose;
   KScope ks(h, s, "lora_dual", 4.0 * r * C, 0, 0, 2.0 * C + 4.0 * r, 0, 6.0 * r * C);
   LK(lora_dual(a, s));
   return 0;
@@ -820,18 +829,14 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
         }
       }
     }
-    if (hd) CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
+    // Z_d = h·A_dᵀ feeds only grad_B of down (the down product itself is not
+    // recomputed): when the fused kernel fits, it is computed in the backward
+    // together with grad_A_d from one pass over h
+    const bool hdual = hd && dual_splits(h, I, r) > 0;
+    if (hd && !hdual) CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
 
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
-    // grad_Z and grad_B of down from one pass over g (lora_dual), else the
-    // skinny product here and the TN reduction after the dX product
-    int dual_d = 1;
-    if (hd) {
-      dual_d = dual(h, g, D, D, h->Zd_b, r, ls.BTd, r, h->gZd_b, r,
-                    ls.lora[DSB_PROJ_DOWN].gB, st);
-      if (dual_d < 0) return -1;
-      if (dual_d) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
-    }
+    if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
     {
       // gh = g·W_down (+ gZ_d·A_d): grad wrt h = silu(gate)·up
       GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
@@ -845,15 +850,21 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
-      CKR(tn(h, h->gZd_b, r, h->hb, I, r, I, t.gA, nullptr, nullptr, r, 0, 1.f, st));
-      if (dual_d) CKR(tn(h, h->Zd_b, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
+      if (hdual) {
+        // Z_d = bf16(h·A_dᵀ) and grad_A_d = grad_Z_dᵀ·h [r, I] in one pass over h
+        const int rc = dual(h, h->hb, I, I, h->gZd_b, r, ls.Ad, r, h->Zd_b, r, t.gA, st, 1.f, 0);
+        if (rc != 0) return -1;
+      } else {
+        CKR(tn(h, h->gZd_b, r, h->hb, I, r, I, t.gA, nullptr, nullptr, r, 0, 1.f, st));
+      }
+      CKR(tn(h, h->Zd_b, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     int dual_g = 1, dual_u = 1;
     if (hg) {
       dual_g = dual(h, h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, r, h->gZgu_b, 2L * r,
-                    ls.lora[DSB_PROJ_GATE].gB, st);
+                    ls.lora[DSB_PROJ_GATE].gB, st, h->s, 1);
       dual_u = dual(h, h->Ggu + I, 2L * I, I, h->Zgu_b + r, 2L * r, ls.BTu, r, h->gZgu_b + r,
-                    2L * r, ls.lora[DSB_PROJ_UP].gB, st);
+                    2L * r, ls.lora[DSB_PROJ_UP].gB, st, h->s, 1);
       if (dual_g < 0 || dual_u < 0) return -1;
       if (dual_g) CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
       if (dual_u) CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
@@ -882,7 +893,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     int dual_o = 1;
     if (ho) {
       dual_o = dual(h, h->grm, D, D, h->Zo_b, r, ls.BTo, r, h->gZo_b, r, ls.lora[DSB_PROJ_O].gB,
-                    st);
+                    st, h->s, 1);
       if (dual_o < 0) return -1;
       if (dual_o) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_b, r, st));
     }
@@ -917,11 +928,11 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     int dual_q = 1, dual_k = 1, dual_v = 1;
     if (hq) {
       dual_q = dual(h, h->gqkv, W3, q, h->Zqkv_b, 3L * r, ls.BTq, r, h->gZqkv_b, 3L * r,
-                    ls.lora[DSB_PROJ_Q].gB, st);
+                    ls.lora[DSB_PROJ_Q].gB, st, h->s, 1);
       dual_k = dual(h, h->gqkv + q, W3, kv, h->Zqkv_b + r, 3L * r, ls.BTk, r, h->gZqkv_b + r,
-                    3L * r, ls.lora[DSB_PROJ_K].gB, st);
+                    3L * r, ls.lora[DSB_PROJ_K].gB, st, h->s, 1);
       dual_v = dual(h, h->gqkv + q + kv, W3, kv, h->Zqkv_b + 2 * r, 3L * r, ls.BTv, r,
-                    h->gZqkv_b + 2 * r, 3L * r, ls.lora[DSB_PROJ_V].gB, st);
+                    h->gZqkv_b + 2 * r, 3L * r, ls.lora[DSB_PROJ_V].gB, st, h->s, 1);
       if (dual_q < 0 || dual_k < 0 || dual_v < 0) return -1;
       if (dual_q) CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
       if (dual_k) CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_b + r, 3 * r, st));
@@ -1786,7 +1797,7 @@ int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, i
 
 int dsb_op_lora_dual(const void* G, int64_t ldg, const void* Z, int64_t ldz, const void* BT,
                      int64_t ldbt, int n, int r, int C, float scale, void* gZ, int64_t ldgz,
-                     float* gB, void* stream) {
+                     float* gB, int transpose_out, void* stream) {
   if (!lora_dual_supported(r, r, C) || ldg % 8 || ldbt % 8 || n < 0)
     return fail(nullptr, "dsb_op_lora_dual: r must be 16 or 32; C, ldg, ldbt multiples of 8");
   if (n == 0) return 0;
@@ -1800,7 +1811,7 @@ int dsb_op_lora_dual(const void* G, int64_t ldg, const void* Z, int64_t ldz, con
   a.X = (const bf16*)G; a.ldx = ldg; a.P = (const bf16*)Z; a.ldp = ldz;
   a.W = (const bf16*)BT; a.ldw = ldbt; a.R1 = r; a.R2 = r; a.C = C;
   a.n = n; a.n_dev = nullptr; a.n_alloc = n; a.nsplit = ns; a.work = work;
-  a.Y = (bf16*)gZ; a.ldy = ldgz; a.out = gB; a.scale = scale;
+  a.Y = (bf16*)gZ; a.ldy = ldgz; a.out = gB; a.scale = scale; a.transpose_out = transpose_out;
   OPCK(lora_dual(a, s));
   OPCK(hipStreamSynchronize(s));
   return 0;

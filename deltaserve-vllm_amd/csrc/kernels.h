@@ -97,6 +97,8 @@ hipError_t lora_tn(const TnArgs& a, hipStream_t s);
 // (ops.py:142 grad_Z = gy @ (s·B) and ops.py:144 grad_B = s · gy.t() @ Z):
 //   Y[t, j] = bf16(sum_c G[t, c]·W[j, c])          (W = (s·B)ᵀ [R2, C])
 //   out[c, j] = scale · sum_t P[t, j]·G[t, c]      (P = Z [n, R1], out = grad_B)
+// The same pass serves grad_A = grad_Zᵀ·h with Z = h·Aᵀ (W = A, P = grad_Z,
+// out[j, c] when transpose_out = 0).
 // R1 = 16·RB1 and R2 = 16·RB2 with RB1, RB2 in {1, 2}; C a multiple of 8.
 // work holds ceil(C/512)·n_alloc·R2 + nsplit·C·R1 floats.
 struct DualArgs {
@@ -109,7 +111,8 @@ struct DualArgs {
   int nsplit;
   float* work;
   bf16* Y; long ldy;
-  float* out; float scale;  // out[c, j], row pitch R1
+  float* out; float scale;  // out[c, j] (row pitch R1), or out[j, c] when !transpose_out
+  int transpose_out;
 };
 hipError_t lora_dual(const DualArgs& a, hipStream_t s);
 bool lora_dual_supported(int R1, int R2, int C);

@@ -455,7 +455,10 @@ __global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualArgs a) {
   float s = 0.f;
 #pragma unroll 8
   for (int sp = 0; sp < a.nsplit; ++sp) s += wt[((long)sp * a.C + c) * a.R1 + j];
-  a.out[(long)c * a.R1 + j] = s * a.scale;
+  if (a.transpose_out)
+    a.out[(long)c * a.R1 + j] = s * a.scale;
+  else
+    a.out[(long)j * a.C + c] = s * a.scale;
 }
 
 bool lora_dual_supported(int R1, int R2, int C) {

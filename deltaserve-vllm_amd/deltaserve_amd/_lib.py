@@ -130,7 +130,7 @@ _SIGS = {
                                    c_void_p, c_int64, c_void_p]),
     "dsb_op_lora_dual": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                  c_int, c_int, c_int, c_float, c_void_p, c_int64, c_void_p,
-                                 c_void_p]),
+                                 c_int, c_void_p]),
     "dsb_op_clip_adamw": (c_int, [POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
                                   POINTER(c_void_p), POINTER(c_int32), POINTER(c_int32),
                                   c_int, c_int, c_float, c_float, c_float, c_float, c_float,

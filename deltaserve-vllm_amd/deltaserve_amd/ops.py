@@ -230,17 +230,19 @@ def lora_skinny(X, B):
     return Z
 
 
-def lora_dual(G, Z, BT, scale=1.0):
+def lora_dual(G, Z, BT, scale=1.0, transpose_out=True):
     """ops.py:142 and :144 from one pass over G [n, C]: returns
-    (bf16(G·BTᵀ) [n, r], scale·Gᵀ·Z fp32 [C, r]) for BT = (s·B)ᵀ [r, C]."""
+    (bf16(G·BTᵀ) [n, r], scale·Gᵀ·Z fp32 [C, r] (or [r, C])) for BT = (s·B)ᵀ
+    [r, C]; with G = xin, BT = A, Z = grad_Z it gives Z and grad_A."""
     _dev(G, Z, BT)
     n, C = G.shape
     r = BT.shape[0]
     gZ = torch.empty(n, r, dtype=BF16, device=G.device)
-    gB = torch.empty(C, r, dtype=torch.float32, device=G.device)
+    shape = (C, r) if transpose_out else (r, C)
+    gB = torch.empty(*shape, dtype=torch.float32, device=G.device)
     L.check(L.load().dsb_op_lora_dual(_p(G), _ld(G), _p(Z), _ld(Z), _p(BT), _ld(BT), n, r, C,
-                                      float(scale), _p(gZ), _ld(gZ), _p(gB), _stream()),
-            what="dsb_op_lora_dual")
+                                      float(scale), _p(gZ), _ld(gZ), _p(gB), int(transpose_out),
+                                      _stream()), what="dsb_op_lora_dual")
     return gZ, gB
 
 

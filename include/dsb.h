@@ -267,11 +267,12 @@ int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, i
                        void* Z, int64_t ldz, void* stream);
 /* grad_Z and grad_B of ops.py:142 and :144 from one pass over gy = G [n, C]:
  * gZ = bf16(G·BTᵀ) with BT = (s·B)ᵀ [r, C] (ld ldbt), and gB[c, j] = scale ·
- * sum_t G[t, c]·Z[t, j] (fp32 [C, r]). r in {16, 32}; C, ldg, ldbt multiples
- * of 8. */
+ * sum_t G[t, c]·Z[t, j] (fp32 [C, r], or [r, C] when transpose_out = 0; the
+ * same pass over xin with BT = A and Z = grad_Z gives ops.py:141 Z and :143
+ * grad_A). r in {16, 32}; C, ldg, ldbt multiples of 8. */
 int dsb_op_lora_dual(const void* G, int64_t ldg, const void* Z, int64_t ldz, const void* BT,
                      int64_t ldbt, int n, int r, int C, float scale, void* gZ, int64_t ldgz,
-                     float* gB, void* stream);
+                     float* gB, int transpose_out, void* stream);
 /* trainer.py:624-636 + :668 on a flat tensor list: per-group clip then AdamW. */
 int dsb_op_clip_adamw(float* const* w, float* const* g, float* const* m, float* const* v,
                       const int32_t* numel, const int32_t* group, int ntensors, int ngroups,

@@ -256,6 +256,9 @@ def test_lora_dual(n, r, C):
     ops.lora_tn(Z, G, r, True, [gB2], scale=2.0)
     assert max_rel(gZ, gZ2) < 8e-3
     assert max_rel(gB, gB2) < 1e-5
+    # the same pass over xin for Z and grad_A ([r, C])
+    _, gA = ops.lora_dual(G, Z, BT, scale=1.0, transpose_out=False)
+    assert max_rel(gA, Zc.t() @ Gc) < 1e-5
 
 
 def test_clip_adamw():
