@@ -646,34 +646,58 @@ int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, i
   return 0;
 }
 
-// Token splits of a lora_dual pass over C columns at rank r, or 0 when the
-// shape is outside what the fused kernel handles (the caller then runs
-// lora_skinny and lora_tn).
-int dual_splits(const dsb_handle* h, int C, int r) {
-  if (!lora_dual_supported(r, r, C)) return 0;
-  const int ncb = (C + 511) / 512;
-  const long ywork = (long)ncb * h->N * r;
-  int ns = std::max(1, std::min(256 / ncb, h->N / 64));
-  while (ns > 1 && ywork + (long)ns * C * r > h->tn_work_elems) --ns;
-  return ywork + (long)ns * C * r > h->tn_work_elems ? 0 : ns;
-}
-
 // One lora_dual pass over X [n, C]: Y = bf16(X·Wᵀ) [n, r] and
 // out = scale·Pᵀ·X, as [C, r] (transpose) or [r, C]. For an adapter's output
 // gradient G: W = (s·B)ᵀ, P = Z gives grad_Z and grad_B (scale s, [C, r]).
-// Returns 1 when the shape needs the separate kernels.
-int dual(dsb_handle* h, const bf16* X, long ldx, int C, const bf16* P, long ldp, const bf16* W,
-         int r, bf16* Y, long ldy, float* out, hipStream_t s, float scale, int transpose) {
-  const int ns = dual_splits(h, C, r);
+struct DualSpec {
+  const bf16* X; long ldx; int C;
+  const bf16* P; long ldp;
+  const bf16* W;
+  bf16* Y; long ldy;
+  float* out; float scale; int transpose;
+};
+
+// Token splits for passes over the given column counts at rank r in one
+// launch, or 0 when the shape is outside what the fused kernel handles (the
+// caller then runs lora_skinny and lora_tn).
+int dual_splits(const dsb_handle* h, const int* C, int count, int r) {
+  int ncb = 0;
+  long ywork = 0, cols = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!lora_dual_supported(r, r, C[i])) return 0;
+    ncb += (C[i] + 511) / 512;
+    ywork += (long)((C[i] + 511) / 512) * h->N * r;
+    cols += C[i];
+  }
+  int ns = std::max(1, std::min(256 / ncb, h->N / 64));
+  while (ns > 1 && ywork + (long)ns * cols * r > h->tn_work_elems) --ns;
+  return ywork + (long)ns * cols * r > h->tn_work_elems ? 0 : ns;
+}
+
+// The passes of `sp` (count <= 3, rank r each) in one launch. Returns 1 when
+// the shapes need the separate kernels.
+int dual(dsb_handle* h, const DualSpec* sp, int count, int r, hipStream_t s) {
+  int C[3];
+  for (int i = 0; i < count; ++i) C[i] = sp[i].C;
+  const int ns = dual_splits(h, C, count, r);
   if (ns == 0) return 1;
-  DualArgs a{};
-  a.X = X; a.ldx = ldx; a.P = P; a.ldp = ldp; a.W = W; a.ldw = C;
-  a.R1 = r; a.R2 = r; a.C = C;
-  a.n = h->N; a.n_dev = &h->d_hdr->n; a.n_alloc = h->N; a.nsplit = ns;
-  a.work = h->tn_work; a.Y = Y; a.ldy = ldy; a.out = out; a.scale = scale;
-  a.transpose_out = transpose;
-  KScope ks(h, s, "lora_dual", 4.0 * r * C, 0, 0, 2.0 * C + 4.0 * r, 0, 6.0 * r * C);
-  LK(lora_dual(a, s));
+  DualArgs a[3] = {};
+  float* work = h->tn_work;
+  double flops_n = 0, bytes_n = 0, bytes_c = 0;
+  for (int i = 0; i < count; ++i) {
+    DualArgs& x = a[i];
+    x.X = sp[i].X; x.ldx = sp[i].ldx; x.P = sp[i].P; x.ldp = sp[i].ldp; x.W = sp[i].W;
+    x.ldw = sp[i].C; x.R1 = r; x.R2 = r; x.C = sp[i].C;
+    x.n = h->N; x.n_dev = &h->d_hdr->n; x.n_alloc = h->N; x.nsplit = ns;
+    x.work = work; x.Y = sp[i].Y; x.ldy = sp[i].ldy; x.out = sp[i].out; x.scale = sp[i].scale;
+    x.transpose_out = sp[i].transpose;
+    work += (long)((x.C + 511) / 512) * h->N * r + (long)ns * x.C * r;
+    flops_n += 4.0 * r * x.C;
+    bytes_n += 2.0 * x.C + 4.0 * r;
+    bytes_c += 6.0 * r * x.C;
+  }
+  KScope ks(h, s, "lora_dual", flops_n, 0, 0, bytes_n, 0, bytes_c);
+  LK(lora_dual(a, count, s));
   return 0;
 }
 
@@ -832,7 +856,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     // Z_d = h·A_dᵀ feeds only grad_B of down (the down product itself is not
     // recomputed): when the fused kernel fits, it is computed in the backward
     // together with grad_A_d from one pass over h
-    const bool hdual = hd && dual_splits(h, I, r) > 0;
+    const bool hdual = hd && dual_splits(h, &I, 1, r) > 0;
     if (hd && !hdual) CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
 
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
@@ -852,7 +876,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
       if (hdual) {
         // Z_d = bf16(h·A_dᵀ) and grad_A_d = grad_Z_dᵀ·h [r, I] in one pass over h
-        const int rc = dual(h, h->hb, I, I, h->gZd_b, r, ls.Ad, r, h->Zd_b, r, t.gA, st, 1.f, 0);
+        const DualSpec d{h->hb, I, I, h->gZd_b, r, ls.Ad, h->Zd_b, r, t.gA, 1.f, 0};
+        const int rc = dual(h, &d, 1, r, st);
         if (rc != 0) return -1;
       } else {
         CKR(tn(h, h->gZd_b, r, h->hb, I, r, I, t.gA, nullptr, nullptr, r, 0, 1.f, st));
@@ -861,10 +886,15 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     int dual_g = 1, dual_u = 1;
     if (hg) {
-      dual_g = dual(h, h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, r, h->gZgu_b, 2L * r,
-                    ls.lora[DSB_PROJ_GATE].gB, st, h->s, 1);
-      dual_u = dual(h, h->Ggu + I, 2L * I, I, h->Zgu_b + r, 2L * r, ls.BTu, r, h->gZgu_b + r,
-                    2L * r, ls.lora[DSB_PROJ_UP].gB, st, h->s, 1);
+      const DualSpec d[2] = {
+          {h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, h->gZgu_b, 2L * r,
+           ls.lora[DSB_PROJ_GATE].gB, h->s, 1},
+          {h->Ggu + I, 2L * I, I, h->Zgu_b + r, 2L * r, ls.BTu, h->gZgu_b + r, 2L * r,
+           ls.lora[DSB_PROJ_UP].gB, h->s, 1}};
+      // two launches: 2 × 28 column blocks at C3 would leave a 256-CU grid
+      // with 224 blocks (one split fewer per pass), one pass keeps 28 × 9
+      dual_g = dual(h, &d[0], 1, r, st);
+      dual_u = dual(h, &d[1], 1, r, st);
       if (dual_g < 0 || dual_u < 0) return -1;
       if (dual_g) CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
       if (dual_u) CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
@@ -892,8 +922,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     int dual_o = 1;
     if (ho) {
-      dual_o = dual(h, h->grm, D, D, h->Zo_b, r, ls.BTo, r, h->gZo_b, r, ls.lora[DSB_PROJ_O].gB,
-                    st, h->s, 1);
+      const DualSpec d{h->grm, D, D, h->Zo_b, r, ls.BTo, h->gZo_b, r, ls.lora[DSB_PROJ_O].gB,
+                       h->s, 1};
+      dual_o = dual(h, &d, 1, r, st);
       if (dual_o < 0) return -1;
       if (dual_o) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_b, r, st));
     }
@@ -927,13 +958,15 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     int dual_q = 1, dual_k = 1, dual_v = 1;
     if (hq) {
-      dual_q = dual(h, h->gqkv, W3, q, h->Zqkv_b, 3L * r, ls.BTq, r, h->gZqkv_b, 3L * r,
-                    ls.lora[DSB_PROJ_Q].gB, st, h->s, 1);
-      dual_k = dual(h, h->gqkv + q, W3, kv, h->Zqkv_b + r, 3L * r, ls.BTk, r, h->gZqkv_b + r,
-                    3L * r, ls.lora[DSB_PROJ_K].gB, st, h->s, 1);
-      dual_v = dual(h, h->gqkv + q + kv, W3, kv, h->Zqkv_b + 2 * r, 3L * r, ls.BTv, r,
-                    h->gZqkv_b + 2 * r, 3L * r, ls.lora[DSB_PROJ_V].gB, st, h->s, 1);
-      if (dual_q < 0 || dual_k < 0 || dual_v < 0) return -1;
+      const DualSpec d[3] = {
+          {h->gqkv, W3, q, h->Zqkv_b, 3L * r, ls.BTq, h->gZqkv_b, 3L * r, ls.lora[DSB_PROJ_Q].gB,
+           h->s, 1},
+          {h->gqkv + q, W3, kv, h->Zqkv_b + r, 3L * r, ls.BTk, h->gZqkv_b + r, 3L * r,
+           ls.lora[DSB_PROJ_K].gB, h->s, 1},
+          {h->gqkv + q + kv, W3, kv, h->Zqkv_b + 2 * r, 3L * r, ls.BTv, h->gZqkv_b + 2 * r, 3L * r,
+           ls.lora[DSB_PROJ_V].gB, h->s, 1}};
+      dual_q = dual_k = dual_v = dual(h, d, 3, r, st);
+      if (dual_q < 0) return -1;
       if (dual_q) CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
       if (dual_k) CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_b + r, 3 * r, st));
       if (dual_v) CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_b + 2 * r, 3 * r, st));
@@ -1812,7 +1845,7 @@ int dsb_op_lora_dual(const void* G, int64_t ldg, const void* Z, int64_t ldz, con
   a.W = (const bf16*)BT; a.ldw = ldbt; a.R1 = r; a.R2 = r; a.C = C;
   a.n = n; a.n_dev = nullptr; a.n_alloc = n; a.nsplit = ns; a.work = work;
   a.Y = (bf16*)gZ; a.ldy = ldgz; a.out = gB; a.scale = scale; a.transpose_out = transpose_out;
-  OPCK(lora_dual(a, s));
+  OPCK(lora_dual(&a, 1, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
 }

@@ -114,7 +114,9 @@ struct DualArgs {
   float* out; float scale;  // out[c, j] (row pitch R1), or out[j, c] when !transpose_out
   int transpose_out;
 };
-hipError_t lora_dual(const DualArgs& a, hipStream_t s);
+// Up to 3 passes with the same R1, R2, n and nsplit in one launch (plus one
+// launch for all their reductions); each a[i].work is its own region.
+hipError_t lora_dual(const DualArgs* a, int count, hipStream_t s);
 bool lora_dual_supported(int R1, int R2, int C);
 
 // ---- head.hip

@@ -297,16 +297,29 @@ hipError_t lora_tn(const TnArgs& a, hipStream_t s) {
 //    16 rows × 512 columns with the W fragments it holds in registers; the
 //    fp32 partial over the block's columns goes to workY[cb][t][j].
 // Two small kernels reduce the partials in a fixed order (deterministic).
+// A launch covers up to 3 passes (adapters sharing ranks and token splits):
+// grid.x runs over the column blocks of all of them, cb0[i] .. cb0[i+1]-1
+// being those of pass i; the reductions likewise cover the passes' index
+// ranges r0[i] .. r0[i+1]-1 in order.
+struct DualBatch {
+  DualArgs a[3];
+  int count;
+  int cb0[4];
+  long r0[4];
+};
+
 template <int RB1, int RB2>
-__global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualArgs a) {
+__global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
   constexpr int R1 = 16 * RB1, R2 = 16 * RB2;
+  const int pi = blockIdx.x >= b.cb0[2] ? 2 : (blockIdx.x >= b.cb0[1] ? 1 : 0);  // uniform
+  const DualArgs& a = b.a[pi];
   constexpr int XT = 32 * 512, PT = 32 * R1, SE = XT + PT, NS = 4;
   constexpr int LPS = 8;  // X loads per lane per chunk (+1 P load on waves < RB1)
   __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int cb = blockIdx.x, c0 = cb * 512, sp = blockIdx.y;
+  const int cb = blockIdx.x - b.cb0[pi], c0 = cb * 512, sp = blockIdx.y;
   int per = (N + a.nsplit - 1) / a.nsplit;
   per = (per + 31) & ~31;
   const int ta = min(N, sp * per), tb = min(N, ta + per);
@@ -434,8 +447,12 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualArgs a) {
 // (deterministic): indices below n_alloc·R2 give Y[t, j] = bf16(sum over the
 // column blocks of the skinny partials) for live tokens t; the next C·R1 give
 // out[c, j] = scale · (sum over the token splits of the TN partials).
-__global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualArgs a) {
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+__global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualBatch b) {
+  long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= b.r0[b.count]) return;
+  const int pi = idx >= b.r0[2] ? 2 : (idx >= b.r0[1] ? 1 : 0);
+  const DualArgs& a = b.a[pi];
+  idx -= b.r0[pi];
   const long ny = (long)a.n_alloc * a.R2;
   const int ncb = (a.C + 511) / 512;
   if (idx < ny) {
@@ -465,23 +482,39 @@ bool lora_dual_supported(int R1, int R2, int C) {
   return (R1 == 16 || R1 == 32) && (R2 == 16 || R2 == 32) && C % 8 == 0 && C > 0;
 }
 
-hipError_t lora_dual(const DualArgs& a, hipStream_t s) {
-  if (a.n <= 0) return hipSuccess;
-  if (!lora_dual_supported(a.R1, a.R2, a.C) || a.n > a.n_alloc || a.nsplit < 1)
-    return hipErrorInvalidValue;
-  const dim3 grid((a.C + 511) / 512, a.nsplit);
-  const int k = (a.R1 / 16 - 1) * 2 + (a.R2 / 16 - 1);
+hipError_t lora_dual(const DualArgs* a, int count, hipStream_t s) {
+  if (count < 1 || count > 3) return hipErrorInvalidValue;
+  if (a[0].n <= 0) return hipSuccess;
+  DualBatch b{};
+  b.count = count;
+  b.cb0[0] = 0;
+  b.r0[0] = 0;
+  for (int i = 0; i < count; ++i) {
+    const DualArgs& x = a[i];
+    if (!lora_dual_supported(x.R1, x.R2, x.C) || x.n > x.n_alloc || x.nsplit < 1 ||
+        x.R1 != a[0].R1 || x.R2 != a[0].R2 || x.nsplit != a[0].nsplit || x.n != a[0].n)
+      return hipErrorInvalidValue;
+    b.a[i] = x;
+    b.cb0[i + 1] = b.cb0[i] + (x.C + 511) / 512;
+    b.r0[i + 1] = b.r0[i] + (long)x.n_alloc * x.R2 + (long)x.R1 * x.C;
+  }
+  for (int i = count; i < 3; ++i) {
+    b.cb0[i + 1] = b.cb0[count];
+    b.r0[i + 1] = b.r0[count];
+  }
+  const dim3 grid(b.cb0[count], a[0].nsplit);
+  const int k = (a[0].R1 / 16 - 1) * 2 + (a[0].R2 / 16 - 1);
   switch (k) {
-    case 0: hipLaunchKernelGGL((lora_dual_kernel<1, 1>), grid, dim3(256), 0, s, a); break;
-    case 1: hipLaunchKernelGGL((lora_dual_kernel<1, 2>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((lora_dual_kernel<2, 1>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((lora_dual_kernel<2, 2>), grid, dim3(256), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((lora_dual_kernel<1, 1>), grid, dim3(256), 0, s, b); break;
+    case 1: hipLaunchKernelGGL((lora_dual_kernel<1, 2>), grid, dim3(256), 0, s, b); break;
+    case 2: hipLaunchKernelGGL((lora_dual_kernel<2, 1>), grid, dim3(256), 0, s, b); break;
+    default: hipLaunchKernelGGL((lora_dual_kernel<2, 2>), grid, dim3(256), 0, s, b); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const long tot = (long)a.n_alloc * a.R2 + (long)a.R1 * a.C;
+  const long tot = b.r0[count];
   hipLaunchKernelGGL(lora_dual_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
-                     s, a);
+                     s, b);
   return hipGetLastError();
 }
 
