@@ -203,19 +203,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
-// dsum[h, t] = sum_d dO[t, h*128 + d] * O[t, h*128 + d]
+// dsum[h, t] = sum_d dO[t, h*128 + d] * O[t, h*128 + d]. 16 lanes per
+// (token, head) row, each reading 8 dims with 16- and 32-byte loads; 4 rows
+// per wave, 16 per block.
 __global__ __launch_bounds__(256) void attn_dsum_kernel(AttnArgs a) {
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
-  const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long item = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
   if (item >= (long)N * a.Hq) return;
-  const int t = (int)(item / a.Hq), h = (int)(item % a.Hq), l = threadIdx.x & 63;
-  const bf16* d = a.dout + (long)t * a.lddo + h * HD;
-  const float* o = a.o32 + (long)t * a.ldo32 + h * HD;
-  const bf16x2 dv = *reinterpret_cast<const bf16x2*>(d + 2 * l);
-  const f32x2 ov = *reinterpret_cast<const f32x2*>(o + 2 * l);
-  float v = (float)dv[0] * ov[0] + (float)dv[1] * ov[1];
-  v = wave_sum(v);
+  const int t = (int)(item / a.Hq), h = (int)(item % a.Hq), l = threadIdx.x & 15;
+  const bf16* d = a.dout + (long)t * a.lddo + h * HD + 8 * l;
+  const float* o = a.o32 + (long)t * a.ldo32 + h * HD + 8 * l;
+  float dv[8];
+  unpack8(ldg128(d), dv);
+  const f32x4 o0 = *reinterpret_cast<const f32x4*>(o);
+  const f32x4 o1 = *reinterpret_cast<const f32x4*>(o + 4);
+  float v = dv[0] * o0[0] + dv[1] * o0[1] + dv[2] * o0[2] + dv[3] * o0[3] + dv[4] * o1[0] +
+            dv[5] * o1[1] + dv[6] * o1[2] + dv[7] * o1[3];
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
   if (l == 0) a.dsum[(long)h * a.ld_stat + t] = v;
 }
 
@@ -495,7 +501,7 @@ hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
 hipError_t attn_bwd_prep(const AttnArgs& a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const long items = (long)a.n * a.Hq;
-  hipLaunchKernelGGL(attn_dsum_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_dsum_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

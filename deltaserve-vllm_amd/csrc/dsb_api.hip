@@ -1734,6 +1734,9 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
                     int64_t lddv, const int32_t* seq_lens, int nseq, int Hq, int Hkv,
                     void* stream) {
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(nullptr, "attn: bad head counts");
+  if (ldq % 8 || ldk % 8 || ldv % 8 || lddo % 8 ||
+      (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)o32) & 15))
+    return fail(nullptr, "attn: rows must be 16-byte aligned (ld multiple of 8)");
   hipStream_t s = (hipStream_t)stream;
   TmpDev tmp;
   AttnArgs a{};
