@@ -62,6 +62,11 @@ DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool 
   }
 }
 
+// An empty volatile asm in a wave-uniform branch: the compiler may not
+// execute it speculatively, so the branch stays a branch instead of being
+// flattened into selects that every tile would pay for (the masks below).
+DSB_DEV void keep_branch() { asm volatile(""); }
+
 DSB_DEV bf16x8 pack_chunk(const f32x16& s, int c) {
   bf16x8 b;
 #pragma unroll
@@ -102,18 +107,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const FragOffs fo(lane);
   tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
   tile_dma(a.v, a.ldv, st, 0, L, kvh * HD, smem + TILE, w, lane);
-  for (int t = 0; t < nt; ++t) {
-    const int k0 = t * TR;
-    const char* sK = reinterpret_cast<const char*>(smem + (t & 1) * 2 * TILE);
-    const char* sV = sK + TILE * 2;
+  // The wave computes the tiles with a key at or before its last query
+  // (t < nt_w); after those it only takes part in the block's loads and
+  // barriers. Two loops, so the compute loop has no skip path (a skip path
+  // makes the compiler copy the accumulators on every iteration).
+  const int nt_w = min(nt, wq_last / TR + 1);
+  auto advance = [&](int t) {
     wait_vm<0>();
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
     if (t + 1 < nt) {
       bf16* nxt = smem + ((t + 1) & 1) * 2 * TILE;
-      tile_dma(a.k, a.ldk, st, k0 + TR, L, kvh * HD, nxt, w, lane);
-      tile_dma(a.v, a.ldv, st, k0 + TR, L, kvh * HD, nxt + TILE, w, lane);
+      tile_dma(a.k, a.ldk, st, (t + 1) * TR, L, kvh * HD, nxt, w, lane);
+      tile_dma(a.v, a.ldv, st, (t + 1) * TR, L, kvh * HD, nxt + TILE, w, lane);
     }
-    if (k0 > wq_last) continue;  // every key of the tile is after this wave's queries
+  };
+  for (int t = 0; t < nt_w; ++t) {
+    const int k0 = t * TR;
+    const char* sK = reinterpret_cast<const char*>(smem + (t & 1) * 2 * TILE);
+    const char* sV = sK + TILE * 2;
+    advance(t);
 
     f32x16 s[2];
 #pragma unroll
@@ -125,13 +137,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int kk = 1; kk < 8; ++kk) s[kf] = mfma32(kfr[kk], qf[kk], s[kf]);
     }
-#pragma unroll
-    for (int kf = 0; kf < 2; ++kf)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kf][r] *= sl2;
+    // scores stay unscaled until the exponent: max(s)·c = max(s·c) for c > 0,
+    // and exp2(s·c − m) is one fma + exp
     // causal / length mask, only on tiles that reach past this wave's first
     // query or past the sequence end (wave-uniform)
     if (k0 + TR - 1 > q0 + w * 32 || k0 + TR > L) {
+      keep_branch();
       const int lim = min(qpos, L - 1) - k0 - 4 * lh;  // key offset limit of this lane's rows
 #pragma unroll
       for (int kf = 0; kf < 2; ++kf)
@@ -144,7 +155,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     for (int kf = 0; kf < 2; ++kf)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kf][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
     // Lazy rescale: the running max m_i only moves when some row's tile max
     // exceeds it by more than 8 (log2 units); otherwise p = exp2(s − m_i) <= 256,
     // exact after the final 1/l normalisation.
@@ -159,15 +170,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
       m_i = m_new;
     }
     const float m_use = m_i == -INFINITY ? 0.f : m_i;
-    float rs = 0.f;
+    float rs4[4] = {0.f, 0.f, 0.f, 0.f};  // four partial sums: no serial add chain
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(s[kf][r] - m_use);
+        const float p = fast_exp2(__builtin_fmaf(s[kf][r], sl2, -m_use));
         s[kf][r] = p;
-        rs += p;
+        rs4[r & 3] += p;
       }
+    float rs = (rs4[0] + rs4[1]) + (rs4[2] + rs4[3]);
     rs += __shfl_xor(rs, 32, 64);
     l_i += rs;
 #pragma unroll
@@ -180,6 +192,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
       for (int df = 0; df < 4; ++df) o[df] = mfma32(vfr[df], pb, o[df]);
     }
   }
+  for (int t = nt_w; t < nt; ++t) advance(t);
 
   if (qok) {
     const float inv_l = 1.f / l_i;
@@ -203,9 +216,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
-// dsum[h, t] = sum_d dO[t, h*128 + d] * O[t, h*128 + d]. 16 lanes per
-// (token, head) row, each reading 8 dims with 16- and 32-byte loads; 4 rows
-// per wave, 16 per block.
+// dsum[h, t] = sum_d dO[t, h*128 + d] * O[t, h*128 + d], O from the fp32
+// copy when the forward wrote one (FP32 = true), else from the bf16 ctx (the
+// backward cycle: O rounded to bf16, as flash-attention backwards take it;
+// it saves the 4-byte copy's write and re-read). 16 lanes per (token, head)
+// row, each reading 8 dims; 4 rows per wave, 16 per block.
+template <bool FP32>
 __global__ __launch_bounds__(256) void attn_dsum_kernel(AttnArgs a) {
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
@@ -213,13 +229,22 @@ __global__ __launch_bounds__(256) void attn_dsum_kernel(AttnArgs a) {
   if (item >= (long)N * a.Hq) return;
   const int t = (int)(item / a.Hq), h = (int)(item % a.Hq), l = threadIdx.x & 15;
   const bf16* d = a.dout + (long)t * a.lddo + h * HD + 8 * l;
-  const float* o = a.o32 + (long)t * a.ldo32 + h * HD + 8 * l;
-  float dv[8];
+  float dv[8], ov[8];
   unpack8(ldg128(d), dv);
-  const f32x4 o0 = *reinterpret_cast<const f32x4*>(o);
-  const f32x4 o1 = *reinterpret_cast<const f32x4*>(o + 4);
-  float v = dv[0] * o0[0] + dv[1] * o0[1] + dv[2] * o0[2] + dv[3] * o0[3] + dv[4] * o1[0] +
-            dv[5] * o1[1] + dv[6] * o1[2] + dv[7] * o1[3];
+  if (FP32) {
+    const float* o = a.o32 + (long)t * a.ldo32 + h * HD + 8 * l;
+    const f32x4 o0 = *reinterpret_cast<const f32x4*>(o);
+    const f32x4 o1 = *reinterpret_cast<const f32x4*>(o + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ov[i] = o0[i];
+      ov[4 + i] = o1[i];
+    }
+  } else {
+    unpack8(ldg128(a.ctx + (long)t * a.ldc + h * HD + 8 * l), ov);
+  }
+  float v = dv[0] * ov[0] + dv[1] * ov[1] + dv[2] * ov[2] + dv[3] * ov[3] + dv[4] * ov[4] +
+            dv[5] * ov[5] + dv[6] * ov[6] + dv[7] * ov[7];
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
   if (l == 0) a.dsum[(long)h * a.ld_stat + t] = v;
@@ -258,18 +283,25 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   const FragOffs fo(lane);
   tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
   tile_dma(a.v, a.ldv, st, 0, L, kvh * HD, smem + TILE, w, lane);
-  for (int t = 0; t < nt; ++t) {
+  // The wave computes the tiles with a key at or before its last query
+  // (t < nt_w); after those it only takes part in the block's loads and
+  // barriers. Two loops, so the compute loop has no skip path (a skip path
+  // makes the compiler copy the accumulators on every iteration).
+  const int nt_w = min(nt, wq_last / TR + 1);
+  auto advance = [&](int t) {
+    wait_vm<0>();
+    lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
+    if (t + 1 < nt) {
+      bf16* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+      tile_dma(a.k, a.ldk, st, (t + 1) * TR, L, kvh * HD, nxt, w, lane);
+      tile_dma(a.v, a.ldv, st, (t + 1) * TR, L, kvh * HD, nxt + TILE, w, lane);
+    }
+  };
+  for (int t = 0; t < nt_w; ++t) {
     const int k0 = t * TR;
     const char* sK = reinterpret_cast<const char*>(smem + (t & 1) * 2 * TILE);
     const char* sV = sK + TILE * 2;
-    wait_vm<0>();
-    lds_barrier();
-    if (t + 1 < nt) {
-      bf16* nxt = smem + ((t + 1) & 1) * 2 * TILE;
-      tile_dma(a.k, a.ldk, st, k0 + TR, L, kvh * HD, nxt, w, lane);
-      tile_dma(a.v, a.ldv, st, k0 + TR, L, kvh * HD, nxt + TILE, w, lane);
-    }
-    if (k0 > wq_last) continue;
+    advance(t);
 
     f32x16 s[2], dp[2];
 #pragma unroll
@@ -294,6 +326,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kf][r] = fast_exp2(s[kf][r] * sl2 - lse2);
     if (k0 + TR - 1 > q0 + w * 32 || k0 + TR > L) {
+      keep_branch();
       const int lim = min(qpos, L - 1) - k0 - 4 * lh;
 #pragma unroll
       for (int kf = 0; kf < 2; ++kf)
@@ -315,6 +348,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
       for (int d4 = 0; d4 < 4; ++d4) dq[d4] = mfma32(kt[d4], sb, dq[d4]);
     }
   }
+  for (int t = nt_w; t < nt; ++t) advance(t);
 
   if (qok) {
     const long row = st + qpos;
@@ -402,29 +436,51 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
       load_ld(it + 1);
       stage(it + 1, sidx ^ 1);
     }
-    if (q0 + TR - 1 >= wk_first) {  // else every query of the tile is before this wave's keys
+    // Every wave computes every pair: a wave whose keys all come after the
+    // tile's queries gets an all-masked tile (zero contributions). Skipping it
+    // would not shorten the block, whose waves meet at the next barrier, and
+    // a skip path makes the compiler copy the accumulators each iteration.
+    // The two 32-query halves run one after the other through S, dP, the
+    // softmax terms and the dV/dK products, so only one half's scores are live.
+    {
       const char* cQ = reinterpret_cast<const char*>(sQ);
       const char* cO = reinterpret_cast<const char*>(sO);
-      f32x16 s[2], dp[2];
+      // Mask (tiles at the diagonal or the sequence end, wave-uniform test):
+      // query q pairs with the lane's key iff key <= q < L and key < L. With
+      // q = q0 + 4·lh + off, off the compile-time qf·32 + 8(r/4) + r%4, that is
+      // lo <= off < hi. Masked scores become −inf, so P and dS = P∘(dP − D)
+      // come out 0.
+      const bool masked = q0 < wk_first + 31 || q0 + TR > L || wk_first + 31 >= L;
+      const int base = q0 + 4 * lh;
+      const int lo = key - base;
+      const int hi = kok ? L - base : lo;
 #pragma unroll
       for (int qf = 0; qf < 2; ++qf) {
-        bf16x8 qfr[8], ofr[8];
+        // lane: key row; r: queries qf·32 + 8(r/4) + 4·lh + r%4
+        f32x16 s, dp;
+        {
+          bf16x8 qfr[8], ofr[8];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          qfr[kk] = row_frag(cQ, fo, qf * 32, kk);
-          ofr[kk] = row_frag(cO, fo, qf * 32, kk);
+          for (int kk = 0; kk < 8; ++kk) {
+            qfr[kk] = row_frag(cQ, fo, qf * 32, kk);
+            ofr[kk] = row_frag(cO, fo, qf * 32, kk);
+          }
+          s = mfma32(qfr[0], kf_[0], f32x16{});
+          dp = mfma32(ofr[0], vf_[0], f32x16{});
+#pragma unroll
+          for (int kk = 1; kk < 8; ++kk) {
+            s = mfma32(qfr[kk], kf_[kk], s);
+            dp = mfma32(ofr[kk], vf_[kk], dp);
+          }
         }
-        s[qf] = mfma32(qfr[0], kf_[0], f32x16{});
-        dp[qf] = mfma32(ofr[0], vf_[0], f32x16{});
+        if (masked) {
+          keep_branch();
 #pragma unroll
-        for (int kk = 1; kk < 8; ++kk) {
-          s[qf] = mfma32(qfr[kk], kf_[kk], s[qf]);
-          dp[qf] = mfma32(ofr[kk], vf_[kk], dp[qf]);
+          for (int r = 0; r < 16; ++r) {
+            const int off = qf * 32 + 8 * (r >> 2) + (r & 3);
+            if (off < lo || off >= hi) s[r] = -INFINITY;
+          }
         }
-      }
-      // lane: key row; r: queries qf·32 + 8(r/4) + 4·lh + r%4 (4 consecutive per r/4)
-#pragma unroll
-      for (int qf = 0; qf < 2; ++qf)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int qi = qf * 32 + 8 * r4 + 4 * lh;
@@ -432,38 +488,27 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sLD[sidx][1][qi]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float p = fast_exp2(s[qf][4 * r4 + e] * sl2 - l4[e]);
-            s[qf][4 * r4 + e] = p;
-            dp[qf][4 * r4 + e] = p * (dp[qf][4 * r4 + e] - d4[e]);
+            const float p = fast_exp2(s[4 * r4 + e] * sl2 - l4[e]);
+            s[4 * r4 + e] = p;
+            dp[4 * r4 + e] = p * (dp[4 * r4 + e] - d4[e]);
           }
         }
-      // mask: query < key or query >= L or key >= L (tiles at the diagonal or the end)
-      if (q0 < wk_first + 31 || q0 + TR > L || wk_first + 31 >= L) {
 #pragma unroll
-        for (int qf = 0; qf < 2; ++qf)
+        for (int c = 0; c < 2; ++c) {
+          const int qc = 2 * qf + c;
+          bf16x8 ot[4], qt[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int query = q0 + qf * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            if (!(kok && query < L && query >= key)) {
-              s[qf][r] = 0.f;
-              dp[qf][r] = 0.f;
-            }
+          for (int d4 = 0; d4 < 4; ++d4) {
+            ot[d4] = tr_frag(cO, fo, qc * 16, d4);
+            qt[d4] = tr_frag(cQ, fo, qc * 16, d4);
           }
-      }
+          const bf16x8 pb = pack_chunk(s, c);
+          const bf16x8 sb = pack_chunk(dp, c);
 #pragma unroll
-      for (int qc = 0; qc < 4; ++qc) {
-        bf16x8 ot[4], qt[4];
-#pragma unroll
-        for (int d4 = 0; d4 < 4; ++d4) {
-          ot[d4] = tr_frag(cO, fo, qc * 16, d4);
-          qt[d4] = tr_frag(cQ, fo, qc * 16, d4);
-        }
-        const bf16x8 pb = pack_chunk(s[qc >> 1], qc & 1);
-        const bf16x8 sb = pack_chunk(dp[qc >> 1], qc & 1);
-#pragma unroll
-        for (int d4 = 0; d4 < 4; ++d4) {
-          dv[d4] = mfma32(ot[d4], pb, dv[d4]);
-          dk[d4] = mfma32(qt[d4], sb, dk[d4]);
+          for (int d4 = 0; d4 < 4; ++d4) {
+            dv[d4] = mfma32(ot[d4], pb, dv[d4]);
+            dk[d4] = mfma32(qt[d4], sb, dk[d4]);
+          }
         }
       }
     }
@@ -501,7 +546,11 @@ hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
 hipError_t attn_bwd_prep(const AttnArgs& a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const long items = (long)a.n * a.Hq;
-  hipLaunchKernelGGL(attn_dsum_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0, s, a);
+  const dim3 grid((unsigned)((items + 15) / 16));
+  if (a.o32)
+    hipLaunchKernelGGL(attn_dsum_kernel<true>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(attn_dsum_kernel<false>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -232,7 +232,7 @@ struct dsb_handle {
   std::vector<void*> allocs;
   // workspace
   bf16 *xn1, *qkv_pre, *qk, *ctx, *resid, *xn2, *gu, *hb, *gh;
-  float *o32, *lse, *dsum;
+  float *lse, *dsum;
   bf16 *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
   bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
   bf16 *g0, *g1, *Ggu, *grm, *gctx, *gqkv;
@@ -368,7 +368,6 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->qkv_pre, NN * W3));
   CKR(dalloc(h, &h->qk, NN * (q + kv)));
   CKR(dalloc(h, &h->ctx, NN * q));
-  CKR(dalloc(h, &h->o32, NN * q));
   CKR(dalloc(h, &h->lse, (long)h->Hq * NN));
   CKR(dalloc(h, &h->dsum, (long)h->Hq * NN));
   CKR(dalloc(h, &h->resid, NN * D));
@@ -778,7 +777,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     at.q = h->qk; at.ldq = q + kv;
     at.k = h->qk + q; at.ldk = q + kv;
     at.v = h->qkv_pre + q + kv; at.ldv = W3;
-    at.ctx = h->ctx; at.ldc = q; at.o32 = h->o32; at.ldo32 = q;
+    at.ctx = h->ctx; at.ldc = q; at.o32 = nullptr; at.ldo32 = 0;  // dsum reads the bf16 ctx
     at.lse = h->lse; at.dsum = h->dsum; at.ld_stat = N + 1;
     at.dout = h->gctx; at.lddo = q;
     at.dq = h->gqkv; at.lddq = W3;
@@ -1734,6 +1733,7 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
                     int64_t lddv, const int32_t* seq_lens, int nseq, int Hq, int Hkv,
                     void* stream) {
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(nullptr, "attn: bad head counts");
+  if (!o32 || !lse) return fail(nullptr, "attn: o32 and lse from the forward are required");
   if (ldq % 8 || ldk % 8 || ldv % 8 || lddo % 8 ||
       (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)o32) & 15))
     return fail(nullptr, "attn: rows must be 16-byte aligned (ld multiple of 8)");

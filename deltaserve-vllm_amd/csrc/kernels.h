@@ -34,7 +34,8 @@ struct AttnArgs {
   const bf16* k; long ldk;   // [n, Hkv*128] (post-RoPE)
   const bf16* v; long ldv;   // [n, Hkv*128]
   bf16* ctx; long ldc;       // fwd out [n, Hq*128]
-  float* o32;                // fwd out fp32 copy of ctx, ld = ldo32
+  float* o32;                // fwd out fp32 copy of ctx, ld = ldo32; null: none,
+                             // and dsum takes O from the bf16 ctx
   long ldo32;
   float* lse;                // [Hq, ld_stat] log2-domain row log-sum-exp
   float* dsum;               // [Hq, ld_stat] rowsum(dO ∘ O)
