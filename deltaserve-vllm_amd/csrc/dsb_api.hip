@@ -818,7 +818,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
                   h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     {
-      KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 6.0 * q + 4.0 * Hq, 0, 0);
+      KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 2.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_fwd(at, st));
     }
     if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Zo_b, r, st));
@@ -939,7 +939,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       if (dual_o) CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      KScope ks(h, st, "attn_dsum", 0, 0, 0, 6.0 * q + 4.0 * Hq, 0, 0);
+      // per token: dO and O (bf16 ctx) rows read, Hq fp32 sums written
+      KScope ks(h, st, "attn_dsum", 0, 0, 0, 4.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_bwd_prep(at, st));
     }
     {
