@@ -444,9 +444,11 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
 }
 
 // Both reductions of lora_dual in one launch, each in a fixed order
-// (deterministic): indices below n_alloc·R2 give Y[t, j] = bf16(sum over the
-// column blocks of the skinny partials) for live tokens t; the next C·R1 give
-// out[c, j] = scale · (sum over the token splits of the TN partials).
+// (deterministic). A thread handles 4 consecutive j with 16-byte partial loads;
+// the first n_alloc·R2/4 threads of an entry give Y[t, j..j+3] = bf16(sum over
+// the column blocks of the skinny partials) for live tokens t, the next
+// C·R1/4 give out[c, j..j+3] = scale · (sum over the token splits of the TN
+// partials).
 __global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualBatch b) {
   long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= b.r0[b.count]) return;
@@ -455,27 +457,33 @@ __global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualBatch b) {
   idx -= b.r0[pi];
   const long ny = (long)a.n_alloc * a.R2;
   const int ncb = (a.C + 511) / 512;
-  if (idx < ny) {
+  if (idx < ny / 4) {
     int N = a.n;
     if (a.n_dev) N = min(N, *a.n_dev);
-    const int t = (int)(idx / a.R2), j = (int)(idx % a.R2);
+    const int t = (int)(idx / (a.R2 / 4)), j = 4 * (int)(idx % (a.R2 / 4));
     if (t >= N) return;
-    float s = 0.f;
-    for (int c = 0; c < ncb; ++c) s += a.work[((long)c * a.n_alloc + t) * a.R2 + j];
-    a.Y[(long)t * a.ldy + j] = (bf16)s;
+    const float* w = a.work + (long)t * a.R2 + j;
+    f32x4 s = *reinterpret_cast<const f32x4*>(w);
+    for (int c = 1; c < ncb; ++c) s += *reinterpret_cast<const f32x4*>(w + (long)c * ny);
+    bf16* y = a.Y + (long)t * a.ldy + j;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = (bf16)s[e];
     return;
   }
-  const long k = idx - ny;
-  if (k >= (long)a.R1 * a.C) return;
-  const float* wt = a.work + ny * ncb;
-  const int c = (int)(k / a.R1), j = (int)(k % a.R1);
-  float s = 0.f;
-#pragma unroll 8
-  for (int sp = 0; sp < a.nsplit; ++sp) s += wt[((long)sp * a.C + c) * a.R1 + j];
-  if (a.transpose_out)
-    a.out[(long)c * a.R1 + j] = s * a.scale;
-  else
-    a.out[(long)j * a.C + c] = s * a.scale;
+  const long k = idx - ny / 4;
+  if (k >= (long)a.R1 * a.C / 4) return;
+  const int c = (int)(k / (a.R1 / 4)), j = 4 * (int)(k % (a.R1 / 4));
+  const float* wt = a.work + ny * ncb + (long)c * a.R1 + j;
+  const long sstride = (long)a.C * a.R1;
+  f32x4 s = *reinterpret_cast<const f32x4*>(wt);
+  for (int sp = 1; sp < a.nsplit; ++sp) s += *reinterpret_cast<const f32x4*>(wt + sp * sstride);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (a.transpose_out)
+      a.out[(long)c * a.R1 + j + e] = s[e] * a.scale;
+    else
+      a.out[(long)(j + e) * a.C + c] = s[e] * a.scale;
+  }
 }
 
 bool lora_dual_supported(int R1, int R2, int C) {
@@ -496,7 +504,7 @@ hipError_t lora_dual(const DualArgs* a, int count, hipStream_t s) {
       return hipErrorInvalidValue;
     b.a[i] = x;
     b.cb0[i + 1] = b.cb0[i] + (x.C + 511) / 512;
-    b.r0[i + 1] = b.r0[i] + (long)x.n_alloc * x.R2 + (long)x.R1 * x.C;
+    b.r0[i + 1] = b.r0[i] + ((long)x.n_alloc * x.R2 + (long)x.R1 * x.C) / 4;
   }
   for (int i = count; i < 3; ++i) {
     b.cb0[i + 1] = b.cb0[count];
