@@ -127,15 +127,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     const char* sV = sK + TILE * 2;
     advance(t);
 
-    f32x16 s[2];
+    // S = Q·Kᵀ for the two 32-key halves, their MFMA chains alternating
+    // (step i: half i%2, dim chunk i/2); each K fragment read runs four steps
+    // ahead of its MFMA (sched_barrier pins the order) so LDS latency hides
+    // under the MFMAs.
+    f32x16 s[2] = {};
+    {
+      bf16x8 kfr[16];
 #pragma unroll
-    for (int kf = 0; kf < 2; ++kf) {
-      bf16x8 kfr[8];
+      for (int i = 0; i < 4; ++i) kfr[i] = row_frag(sK, fo, (i & 1) * 32, i >> 1);
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) kfr[kk] = row_frag(sK, fo, kf * 32, kk);
-      s[kf] = mfma32(kfr[0], qf[0], f32x16{});
-#pragma unroll
-      for (int kk = 1; kk < 8; ++kk) s[kf] = mfma32(kfr[kk], qf[kk], s[kf]);
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 4 < 16) kfr[i + 4] = row_frag(sK, fo, ((i + 4) & 1) * 32, (i + 4) >> 1);
+        __builtin_amdgcn_sched_barrier(0);
+        s[i & 1] = mfma32(kfr[i], qf[i >> 1], s[i & 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     // scores stay unscaled until the exponent: max(s)·c = max(s·c) for c > 0,
     // and exp2(s·c − m) is one fma + exp
@@ -303,22 +311,29 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
     const char* sV = sK + TILE * 2;
     advance(t);
 
-    f32x16 s[2], dp[2];
+    // S = Q·Kᵀ and dP = dO·Vᵀ per 32-key half; the K and V fragment reads
+    // run two dim chunks ahead of their MFMAs (sched_barrier pins the order).
+    f32x16 s[2] = {}, dp[2] = {};
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf) {
       bf16x8 kfr[8], vfr[8];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
+      for (int kk = 0; kk < 2; ++kk) {
         kfr[kk] = row_frag(sK, fo, kf * 32, kk);
         vfr[kk] = row_frag(sV, fo, kf * 32, kk);
       }
-      s[kf] = mfma32(kfr[0], qf[0], f32x16{});
-      dp[kf] = mfma32(vfr[0], df_[0], f32x16{});
 #pragma unroll
-      for (int kk = 1; kk < 8; ++kk) {
+      for (int kk = 0; kk < 8; ++kk) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (kk + 2 < 8) {
+          kfr[kk + 2] = row_frag(sK, fo, kf * 32, kk + 2);
+          vfr[kk + 2] = row_frag(sV, fo, kf * 32, kk + 2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         s[kf] = mfma32(kfr[kk], qf[kk], s[kf]);
         dp[kf] = mfma32(vfr[kk], df_[kk], dp[kf]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     // P = exp2(S·scale·log2e − lse); dS = P∘(dP − dsum); masked pairs give 0
 #pragma unroll
@@ -457,21 +472,29 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
 #pragma unroll
       for (int qf = 0; qf < 2; ++qf) {
         // lane: key row; r: queries qf·32 + 8(r/4) + 4·lh + r%4
-        f32x16 s, dp;
+        // S = Q·Kᵀ and dP = dO·Vᵀ over the 8 dim chunks. The fragment reads
+        // run two chunks ahead of the MFMAs (sched_barrier pins the order), so
+        // the LDS latency hides under the MFMAs instead of stalling each pair.
+        f32x16 s = {}, dp = {};
         {
           bf16x8 qfr[8], ofr[8];
 #pragma unroll
-          for (int kk = 0; kk < 8; ++kk) {
+          for (int kk = 0; kk < 2; ++kk) {
             qfr[kk] = row_frag(cQ, fo, qf * 32, kk);
             ofr[kk] = row_frag(cO, fo, qf * 32, kk);
           }
-          s = mfma32(qfr[0], kf_[0], f32x16{});
-          dp = mfma32(ofr[0], vf_[0], f32x16{});
 #pragma unroll
-          for (int kk = 1; kk < 8; ++kk) {
+          for (int kk = 0; kk < 8; ++kk) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk + 2 < 8) {
+              qfr[kk + 2] = row_frag(cQ, fo, qf * 32, kk + 2);
+              ofr[kk + 2] = row_frag(cO, fo, qf * 32, kk + 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
             s = mfma32(qfr[kk], kf_[kk], s);
             dp = mfma32(ofr[kk], vf_[kk], dp);
           }
+          __builtin_amdgcn_sched_barrier(0);
         }
         if (masked) {
           keep_branch();
@@ -493,22 +516,28 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
             dp[4 * r4 + e] = p * (dp[4 * r4 + e] - d4[e]);
           }
         }
+        // dV += Pᵀ·dO and dK += dSᵀ·Q over the two 16-query chunks of the
+        // half; the transposed reads of a dim block go one block ahead.
+        {
+          const bf16x8 pb[2] = {pack_chunk(s, 0), pack_chunk(s, 1)};
+          const bf16x8 sb[2] = {pack_chunk(dp, 0), pack_chunk(dp, 1)};
+          bf16x8 ot[8], qt[8];  // [chunk·4 + d4]
+          ot[0] = tr_frag(cO, fo, (2 * qf) * 16, 0);
+          qt[0] = tr_frag(cQ, fo, (2 * qf) * 16, 0);
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int qc = 2 * qf + c;
-          bf16x8 ot[4], qt[4];
-#pragma unroll
-          for (int d4 = 0; d4 < 4; ++d4) {
-            ot[d4] = tr_frag(cO, fo, qc * 16, d4);
-            qt[d4] = tr_frag(cQ, fo, qc * 16, d4);
+          for (int i = 0; i < 8; ++i) {
+            const int c = i >> 2, d4 = i & 3;
+            __builtin_amdgcn_sched_barrier(0);
+            if (i + 1 < 8) {
+              const int c1 = (i + 1) >> 2, e1 = (i + 1) & 3;
+              ot[i + 1] = tr_frag(cO, fo, (2 * qf + c1) * 16, e1);
+              qt[i + 1] = tr_frag(cQ, fo, (2 * qf + c1) * 16, e1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            dv[d4] = mfma32(ot[i], pb[c], dv[d4]);
+            dk[d4] = mfma32(qt[i], sb[c], dk[d4]);
           }
-          const bf16x8 pb = pack_chunk(s, c);
-          const bf16x8 sb = pack_chunk(dp, c);
-#pragma unroll
-          for (int d4 = 0; d4 < 4; ++d4) {
-            dv[d4] = mfma32(ot[d4], pb, dv[d4]);
-            dk[d4] = mfma32(qt[d4], sb, dk[d4]);
-          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
