@@ -385,8 +385,25 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
 
 #pragma unroll
   for (int k = 0; k < NS - 1; ++k) issue(k, k);
+  // Skinny partials of chunk j are stored by the waves with (w - 2j) % 4 < 2,
+  // RB2 buffer stores each, always issued (rows past tb fall outside the
+  // descriptor and are dropped), so the vector-memory count is exact: after
+  // the loads of chunk k come the stores of chunks k-3 .. k-1 and the loads of
+  // chunks k+1 and k+2; the wait leaves exactly those outstanding.
+  auto stores_at = [&](int j) { return j >= 0 && ((w - 2 * j) & 3) < 2 ? 1 : 0; };
+  const __amdgpu_buffer_rsrc_t yr =
+      make_brsrc(workY + (long)cb * a.n_alloc * R2, tb * R2 * 4);
   for (int k = 0; k < nk; ++k) {
-    if (pw) wait_vm<(NS - 2) * (LPS + 1)>(); else wait_vm<(NS - 2) * LPS>();
+    const int sa = stores_at(k - 3) + stores_at(k - 2) + stores_at(k - 1);  // uniform, 0..2
+    if (pw) {
+      if (sa == 0) wait_vm<(NS - 2) * (LPS + 1)>();
+      else if (sa == 1) wait_vm<(NS - 2) * (LPS + 1) + RB2>();
+      else wait_vm<(NS - 2) * (LPS + 1) + 2 * RB2>();
+    } else {
+      if (sa == 0) wait_vm<(NS - 2) * LPS>();
+      else if (sa == 1) wait_vm<(NS - 2) * LPS + RB2>();
+      else wait_vm<(NS - 2) * LPS + 2 * RB2>();
+    }
     lds_barrier();  // chunk k visible; the slot of chunk k-1 is free
     issue(k + NS - 1, (k + NS - 1) % NS);
     const char* st = reinterpret_cast<const char*>(smem + (k % NS) * SE);
@@ -422,12 +439,10 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
         }
       // ay[j]: token 16tt + l%16 of the chunk, ranks 16j + 4(l/16) .. +3
       const int t = ta + 32 * k + 16 * tt + (lane & 15);
-      if (t < tb) {
 #pragma unroll
-        for (int j = 0; j < RB2; ++j)
-          *reinterpret_cast<f32x4*>(workY + ((long)cb * a.n_alloc + t) * R2 + 16 * j +
-                                    4 * (lane >> 4)) = ay[j];
-      }
+      for (int j = 0; j < RB2; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ay[j]), yr,
+                                               (t * R2 + 16 * j + 4 * (lane >> 4)) * 4, 0, 0);
     }
   }
   wait_vm<0>();
@@ -463,8 +478,17 @@ __global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualBatch b) {
     const int t = (int)(idx / (a.R2 / 4)), j = 4 * (int)(idx % (a.R2 / 4));
     if (t >= N) return;
     const float* w = a.work + (long)t * a.R2 + j;
-    f32x4 s = *reinterpret_cast<const f32x4*>(w);
-    for (int c = 1; c < ncb; ++c) s += *reinterpret_cast<const f32x4*>(w + (long)c * ny);
+    // partials loaded 8 at a time (loads in flight together), summed in order
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < ncb; c0 += 8) {
+      f32x4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i < ncb) v[i] = *reinterpret_cast<const f32x4*>(w + (long)(c0 + i) * ny);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i < ncb) s += v[i];
+    }
     bf16* y = a.Y + (long)t * a.ldy + j;
 #pragma unroll
     for (int e = 0; e < 4; ++e) y[e] = (bf16)s[e];
@@ -475,8 +499,16 @@ __global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualBatch b) {
   const int c = (int)(k / (a.R1 / 4)), j = 4 * (int)(k % (a.R1 / 4));
   const float* wt = a.work + ny * ncb + (long)c * a.R1 + j;
   const long sstride = (long)a.C * a.R1;
-  f32x4 s = *reinterpret_cast<const f32x4*>(wt);
-  for (int sp = 1; sp < a.nsplit; ++sp) s += *reinterpret_cast<const f32x4*>(wt + sp * sstride);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int sp0 = 0; sp0 < a.nsplit; sp0 += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (sp0 + i < a.nsplit) v[i] = *reinterpret_cast<const f32x4*>(wt + (sp0 + i) * sstride);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (sp0 + i < a.nsplit) s += v[i];
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     if (a.transpose_out)
