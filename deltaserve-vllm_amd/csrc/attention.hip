@@ -67,6 +67,40 @@ DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool 
 // flattened into selects that every tile would pay for (the masks below).
 DSB_DEV void keep_branch() { asm volatile(""); }
 
+// Query-side block layout (forward and dQ passes). A 128-row tile of the
+// table holds 4 subtiles of 32 queries; with G = Hq / Hkv q-heads per kv
+// head its 4·G (subtile, head) pairs are taken subtile-major, heaviest
+// subtile first, one per wave and four per block: G blocks per tile and kv
+// head (grid x = tiles·G, y = kv heads). The waves of a block share the kv
+// head's K/V stream; for G = 4 they also share the subtile, so all four
+// attend the same keys and none idles at the block's barriers while another
+// finishes its diagonal tiles.
+struct QBlock {
+  int st, L;   // sequence start row and length
+  int q0, h;   // the wave's first query row (in the sequence) and q-head
+  int nt;      // key tiles the block streams
+  int nt_w;    // key tiles the wave attends (0 if it has no query)
+  bool empty;  // no wave of the block has a query (block-uniform)
+};
+DSB_DEV QBlock q_block(const AttnArgs& a, int w) {
+  const int G = a.Hq / a.Hkv;
+  const int tile = blockIdx.x / G, b = blockIdx.x - tile * G;
+  QBlock r{};
+  r.empty = tile >= *a.ntiles_dev;
+  if (r.empty) return r;
+  const int4 tl = a.tiles[tile];
+  r.st = tl.x;
+  r.L = tl.y;
+  const int p = 4 * b + w;
+  r.q0 = tl.z + 32 * (3 - p / G);
+  r.h = blockIdx.y * G + p % G;
+  r.empty = tl.z + 32 * (3 - (4 * b + 3) / G) >= r.L;  // the block's lightest subtile
+  const int q_end = min(r.L, tl.z + 32 * (4 - (4 * b) / G));
+  r.nt = (q_end + TR - 1) / TR;
+  r.nt_w = r.q0 < r.L ? min(r.nt, (r.q0 + 31) / TR + 1) : 0;
+  return r;
+}
+
 DSB_DEV bf16x8 pack_chunk(const f32x16& s, int c) {
   bf16x8 b;
 #pragma unroll
@@ -76,20 +110,18 @@ DSB_DEV bf16x8 pack_chunk(const f32x16& s, int c) {
 }  // namespace
 
 // ---------------------------------------------------------------- forward
-// Block: 128 queries (4 waves × 32) of q-head h; streams K/V tiles of its
-// kv head. LDS: 2 stages × (K tile + V tile) = 64 KB → 2 blocks per CU.
+// Block: 4 waves × 32 queries (q_block layout) of one kv head's q-heads;
+// streams the kv head's K/V tiles. LDS: 2 stages × (K tile + V tile) = 64 KB
+// → 2 blocks per CU.
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
-  const int tile = blockIdx.x;
-  if (tile >= *a.ntiles_dev) return;
-  const int h = blockIdx.y, kvh = h / (a.Hq / a.Hkv);
-  const int4 tl = a.tiles[tile];
-  const int st = tl.x, L = tl.y, q0 = tl.z;
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, lh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qpos = q0 + w * 32 + lr;
+  const QBlock qb = q_block(a, w);
+  if (qb.empty) return;
+  const int kvh = blockIdx.y, h = qb.h, st = qb.st, L = qb.L;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
+  const int qpos = qb.q0 + lr;
   const bool qok = qpos < L;
-  const int wq_last = q0 + w * 32 + 31;  // wave-uniform: last query row of this wave
 
   bf16x8 qf[8];
   load_row_frags(a.q, a.ldq, st + qpos, h * HD, qok, lh, qf);
@@ -101,8 +133,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
   float m_i = -INFINITY, l_i = 0.f;
   const float sl2 = kScale * kLog2e;
-  const int kv_end = min(L, q0 + 128);
-  const int nt = (kv_end + TR - 1) / TR;
+  const int nt = qb.nt;
 
   const FragOffs fo(lane);
   tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
@@ -111,7 +142,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
   // makes the compiler copy the accumulators on every iteration).
-  const int nt_w = min(nt, wq_last / TR + 1);
+  const int nt_w = qb.nt_w;
   auto advance = [&](int t) {
     wait_vm<0>();
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
@@ -149,7 +180,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     // and exp2(s·c − m) is one fma + exp
     // causal / length mask, only on tiles that reach past this wave's first
     // query or past the sequence end (wave-uniform)
-    if (k0 + TR - 1 > q0 + w * 32 || k0 + TR > L) {
+    if (k0 + TR - 1 > qb.q0 || k0 + TR > L) {
       keep_branch();
       const int lim = min(qpos, L - 1) - k0 - 4 * lh;  // key offset limit of this lane's rows
 #pragma unroll
@@ -259,19 +290,17 @@ __global__ __launch_bounds__(256) void attn_dsum_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------- dQ
-// Block: 128 queries of q-head h; streams K/V tiles. dQ = scale · dS·K.
+// Block: 4 waves × 32 queries (q_block layout) of one kv head's q-heads;
+// streams the kv head's K/V tiles. dQ = scale · dS·K.
 __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
-  const int tile = blockIdx.x;
-  if (tile >= *a.ntiles_dev) return;
-  const int h = blockIdx.y, kvh = h / (a.Hq / a.Hkv);
-  const int4 tl = a.tiles[tile];
-  const int st = tl.x, L = tl.y, q0 = tl.z;
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, lh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qpos = q0 + w * 32 + lr;
+  const QBlock qb = q_block(a, w);
+  if (qb.empty) return;
+  const int kvh = blockIdx.y, h = qb.h, st = qb.st, L = qb.L;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
+  const int qpos = qb.q0 + lr;
   const bool qok = qpos < L;
-  const int wq_last = q0 + w * 32 + 31;
 
   bf16x8 qf[8], df_[8];
   load_row_frags(a.q, a.ldq, st + qpos, h * HD, qok, lh, qf);
@@ -285,8 +314,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
   const float sl2 = kScale * kLog2e;
-  const int kv_end = min(L, q0 + 128);
-  const int nt = (kv_end + TR - 1) / TR;
+  const int nt = qb.nt;
 
   const FragOffs fo(lane);
   tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
@@ -295,7 +323,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
   // makes the compiler copy the accumulators on every iteration).
-  const int nt_w = min(nt, wq_last / TR + 1);
+  const int nt_w = qb.nt_w;
   auto advance = [&](int t) {
     wait_vm<0>();
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
@@ -340,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
     for (int kf = 0; kf < 2; ++kf)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kf][r] = fast_exp2(s[kf][r] * sl2 - lse2);
-    if (k0 + TR - 1 > q0 + w * 32 || k0 + TR > L) {
+    if (k0 + TR - 1 > qb.q0 || k0 + TR > L) {
       keep_branch();
       const int lim = min(qpos, L - 1) - k0 - 4 * lh;
 #pragma unroll
@@ -568,7 +596,8 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
 
 hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
   if (a.max_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(a.max_tiles, a.Hq), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(a.max_tiles * (a.Hq / a.Hkv), a.Hkv), dim3(256), 0, s,
+                     a);
   return hipGetLastError();
 }
 
@@ -591,7 +620,8 @@ hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
 
 hipError_t attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
   if (a.max_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_dq_kernel, dim3(a.max_tiles, a.Hq), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_dq_kernel, dim3(a.max_tiles * (a.Hq / a.Hkv), a.Hkv), dim3(256), 0, s,
+                     a);
   return hipGetLastError();
 }
 
