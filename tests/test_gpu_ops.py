@@ -161,8 +161,12 @@ def test_rope_fwd_bwd(qk_norm):
     assert torch.equal(gd[:, q + kv:].cpu(), g[:, q + kv:])  # v columns untouched
 
 
+# group sizes Hq/Hkv 1..8: forward and dQ blocks take four (32-query subtile,
+# q-head) pairs of one kv head, so G = 3 and 5 mix subtiles within a block
 @pytest.mark.parametrize("seq_lens,Hq,Hkv", [([37, 128, 1, 200, 64], 4, 2), ([300], 8, 2),
-                                             ([5, 129, 256], 2, 1), ([1, 1, 2], 4, 4)])
+                                             ([5, 129, 256], 2, 1), ([1, 1, 2], 4, 4),
+                                             ([33, 95, 160, 1, 250], 10, 2), ([70, 31, 129], 6, 2),
+                                             ([200, 64], 8, 1)])
 def test_attention(seq_lens, Hq, Hkv):
     from deltaserve_amd import ops
     n = sum(seq_lens)
