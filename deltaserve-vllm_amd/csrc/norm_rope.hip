@@ -28,13 +28,16 @@ __global__ __launch_bounds__(NORM_NT) void rmsnorm_fwd_kernel(
   __shared__ float red[NORM_NT / 64];
   const bf16* xr = x + (long)row * ldx;
   const int nch = D >> 3;
-  float v[NORM_RPT][8];
+  // the weight chunks are loaded with the row, so their latency overlaps the
+  // row's and the block reduction's
+  float v[NORM_RPT][8], wv[NORM_RPT][8];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NORM_RPT; ++i) {
     const int c = threadIdx.x + i * NORM_NT;
     if (c < nch) {
       unpack8(ldg128(xr + c * 8), v[i]);
+      unpack8(ldg128(w + c * 8), wv[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
     }
@@ -46,10 +49,9 @@ __global__ __launch_bounds__(NORM_NT) void rmsnorm_fwd_kernel(
   for (int i = 0; i < NORM_RPT; ++i) {
     const int c = threadIdx.x + i * NORM_NT;
     if (c < nch) {
-      float wf[8], o[8];
-      unpack8(ldg128(w + c * 8), wf);
+      float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (v[i][e] * inv) * wf[e];
+      for (int e = 0; e < 8; ++e) o[e] = (v[i][e] * inv) * wv[i][e];
       stg128(yr + c * 8, pack8(o));
     }
   }
