@@ -1,14 +1,16 @@
 // Packed varlen causal GQA attention (head_dim 128) on gfx950 MFMA:
-// forward recompute (ctx, fp32 ctx copy, row log-sum-exp) and the FA2-style
-// backward split into a dK/dV pass (one block per 128 keys of one kv head,
-// summing its q-head group in registers, no atomics) and a dQ pass (one block
-// per 128 queries of one q head). Softmax statistics, P and dS stay fp32 in
-// registers; P and dS are rounded to bf16 only as MFMA operands.
+// forward recompute (ctx, optional fp32 ctx copy, row log-sum-exp) and the
+// FA2-style backward split into a dK/dV pass (one block per 128 keys of one kv
+// head, summing its q-head group in registers, no atomics) and a dQ pass
+// (forward and dQ blocks: 4 waves of 32 queries sharing one kv head, see
+// q_block). Softmax statistics, P and dS stay fp32 in registers; P and dS are
+// rounded to bf16 only as MFMA operands.
 //
 // Semantics: deltaserve-plugin/deltaserve/bwd_services/common/attention.py
 //   attn_forward_core   :20-45   (scale 1/sqrt(Hd), causal mask, fp32 softmax)
 //   attn_backward_core  :48-112  (dS = P∘(dP − rowsum(dP∘P)), GQA group sums)
-// rowsum(dP∘P) is computed as rowsum(dO∘O) with the fp32 O of the forward.
+// rowsum(dP∘P) is computed as rowsum(dO∘O), with the fp32 O of the forward
+// when it wrote one, else with the bf16 ctx (the backward cycle).
 // The reference fills masked scores with −1e9 before the softmax; exp of that
 // underflows to exactly 0, so skipping masked pairs is the same arithmetic.
 //
