@@ -120,7 +120,21 @@ static int pack_cycle(const int32_t* seq_lens, int nseq, int n, int32_t* pos, in
   return n_valid;
 }
 
+// Attention tiles of a cycle: one per 128 tokens of each sequence, so at
+// most ceil(n/128) + (sequences - 1) <= ceil(s_max/128) + max_seqs.
 static int max_tiles_for(int s_max, int max_seqs) { return (s_max + 127) / 128 + max_seqs; }
+
+// Grid capacity (tiles) of the attention launches of a captured graph: the
+// smallest of ceil(s_max/128) + 32·2^b (b = 0, 1, ...) that holds the cycle's
+// tiles, capped at the handle's bound. A graph is captured per capacity in
+// use, so a packing of many short sequences does not make every cycle launch
+// its worst-case grid.
+static int tile_capacity(int s_max, int bound, int ntiles) {
+  const int base = (s_max + 127) / 128;
+  long cap = base + 32;
+  while (cap < ntiles && cap < bound) cap = base + 2 * (cap - base);
+  return (int)std::min<long>(cap, bound);
+}
 
 // Tile dispatch orders, heaviest first so the last blocks of a launch are
 // short (blocks start roughly in index order): a query tile t0 of the causal
@@ -193,6 +207,8 @@ struct KClass {
 struct LayerState {
   dsb_layer_weights w{};
   bool bound = false;
+  // LoRA groups: q/k/v share one K-concatenated operand slab, gate/up another;
+  // a projection of a group that is not bound has zero slices (frozen).
   bf16 *qkvT = nullptr, *oT = nullptr, *guT = nullptr, *downT = nullptr;
   dsb_lora_tensors lora[DSB_NUM_PROJ]{};
   bool has[DSB_NUM_PROJ]{};
@@ -212,9 +228,18 @@ bool aligned16(const P*... ps) {
   return ok;
 }
 
+struct GraphSet {  // the cycle's graphs for one attention grid capacity
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<hipGraph_t> seg_graph;
+  std::vector<hipGraphExec_t> seg_exec;
+};
+
 struct dsb_handle {
   dsb_desc d{};
-  int D, Hq, Hkv, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk;
+  int D, Hq, Hkv, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk, nvc;
+  int gemm_cfg = -1;  // forced dense-product tile (GEMM_*), -1 by shape
+  int tile_cap = 0;   // attention grid capacity of the current cycle
   float s;
   bool qwen = false;
   hipStream_t hs = nullptr;
@@ -225,6 +250,8 @@ struct dsb_handle {
   bf16* lm_wT = nullptr;  // [D, ldwt], columns V..ldwt zero
   long ldwt = 0;
   std::vector<const bf16*> layer_in;
+  std::vector<const bf16*> gate_up_in;  // saved gate‖up per layer (empty: recompute)
+  long ld_gate_up = 0;
   const bf16* final_in = nullptr;
   const int64_t* ids = nullptr;
   long act_ld = 0;
@@ -237,10 +264,16 @@ struct dsb_handle {
   bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
   bf16 *g0, *g1, *Ggu, *grm, *gctx, *gqkv;
   bf16 *gxn2, *gxn1;  // the FFN / attention input gradients, bf16 as the reference's cdt
+  // the residual-stream gradient in fp32 (g32[2] alternate by layer like g0 /
+  // g1, which hold its bf16 copies for the MFMA and LoRA operands; grm32 the
+  // post-attention residual's): rounding it to bf16 at every layer would
+  // compound over the layers
+  float *g32[2], *grm32;
+  float* o32;  // fp32 attention output: rowsum(dO∘O) of the backward from unrounded O
   bf16 *normed, *dlog;
   float2* stats;
   float *tgt_logit, *lse_h, *loss_row, *dH;
-  float* logits = nullptr;  // [N + 1, ldwt] fp32 head logits (stats pass → grad pass)
+  float* sink = nullptr;  // gradient outputs of unbound projections of a LoRA group
   float* tn_work;
   long tn_work_elems;
   float *cosb, *sinb, *inv_freq;
@@ -283,15 +316,13 @@ struct dsb_handle {
   int2* d_pub_chunks = nullptr;
   int npub_chunks = 0;
   long pub_elems = 0;
-  // graph
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t gexec = nullptr;
+  // graphs, one set per attention grid capacity; the pause-point path
+  // captures one graph per segment
+  std::vector<std::pair<int, GraphSet>> graphs;
   bool graph_failed = false;
-  // pause-point path: one graph per segment, run-ahead event ring
-  std::vector<hipGraphExec_t> seg_exec;
-  std::vector<hipGraph_t> seg_graph;
-  std::vector<hipEvent_t> ring;
+  std::vector<hipEvent_t> ring;  // run-ahead event ring of the pause-point path
   bool in_step = false;
+  bool seg_graphed = false;  // the last segment launched replayed its graph
   int seg_next = 0;
   int step_nseq = 0;
   std::vector<int32_t> step_lens;
@@ -337,6 +368,27 @@ int dalloc(dsb_handle* h, T** p, size_t count) {
     if ((expr) != 0) return -1; \
   } while (0)
 
+template <class T>
+int dalloc_zero(dsb_handle* h, T** p, size_t count) {
+  if (dalloc(h, p, count)) return -1;
+  CK(hipMemset(*p, 0, count * sizeof(T)));
+  return 0;
+}
+
+bool has_qkv(const LayerState& ls) {
+  return ls.has[DSB_PROJ_Q] || ls.has[DSB_PROJ_K] || ls.has[DSB_PROJ_V];
+}
+bool has_gu(const LayerState& ls) { return ls.has[DSB_PROJ_GATE] || ls.has[DSB_PROJ_UP]; }
+
+// Gradient outputs of projection p of layer i: its torch-owned buffers, or
+// the shared sink when p is an unbound member of a bound group.
+float* grad_a(dsb_handle* h, const LayerState& ls, int p) {
+  return ls.has[p] ? ls.lora[p].gA : h->sink;
+}
+float* grad_b(dsb_handle* h, const LayerState& ls, int p) {
+  return ls.has[p] ? ls.lora[p].gB : h->sink;
+}
+
 int finalize(dsb_handle* h) {
   if (h->finalized) return 0;
   for (int i = 0; i < h->L; ++i)
@@ -348,20 +400,6 @@ int finalize(dsb_handle* h) {
   if (!h->lm_w || !h->norm_w) return fail(h, "LM head / final norm not bound");
   if (!h->final_in || !h->ids || (int)h->layer_in.size() != h->L)
     return fail(h, "activations not bound");
-  for (int i = 0; i < h->L; ++i) {
-    LayerState& ls = h->layers[i];
-    const bool q = ls.has[DSB_PROJ_Q], k = ls.has[DSB_PROJ_K], v = ls.has[DSB_PROJ_V];
-    if (q != k || q != v) {
-      set_error("layer %d: q/k/v LoRA must be bound together", i);
-      h->err = get_error();
-      return -1;
-    }
-    if (ls.has[DSB_PROJ_GATE] != ls.has[DSB_PROJ_UP]) {
-      set_error("layer %d: gate/up LoRA must be bound together", i);
-      h->err = get_error();
-      return -1;
-    }
-  }
   const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
   const long NN = N + 1;
   CKR(dalloc(h, &h->xn1, NN * D));
@@ -391,14 +429,18 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->gqkv, NN * W3));
   CKR(dalloc(h, &h->gxn2, NN * D));
   CKR(dalloc(h, &h->gxn1, NN * D));
+  CKR(dalloc(h, &h->g32[0], NN * D));
+  CKR(dalloc(h, &h->g32[1], NN * D));
+  CKR(dalloc(h, &h->grm32, NN * D));
+  CKR(dalloc(h, &h->o32, NN * q));
   CKR(dalloc(h, &h->normed, NN * D));
   CKR(dalloc(h, &h->stats, NN * h->ntn));
   CKR(dalloc(h, &h->tgt_logit, NN));
   CKR(dalloc(h, &h->lse_h, NN));
   CKR(dalloc(h, &h->loss_row, NN));
   CKR(dalloc(h, &h->dlog, NN * h->vchunk));
-  CKR(dalloc(h, &h->logits, NN * h->ldwt));
   CKR(dalloc(h, &h->dH, NN * D));
+  CKR(dalloc(h, &h->sink, (size_t)r * std::max(std::max(D, q), I)));
   h->tn_work_elems = 32L << 20;
   CKR(dalloc(h, &h->tn_work, h->tn_work_elems));
   CKR(dalloc(h, &h->cosb, NN * 64));
@@ -427,7 +469,9 @@ int finalize(dsb_handle* h) {
   h->d_tiles = reinterpret_cast<int4*>(ds + off_tiles);
   h->d_tiles_k = h->d_tiles + h->max_tiles;
 
-  // LoRA bf16 operand copies + cast jobs + optimizer tensor table.
+  // LoRA bf16 operand copies + cast jobs + optimizer tensor table. Operand
+  // slabs start zeroed; only bound projections get cast jobs, so an unbound
+  // member of a group keeps zero slices and contributes nothing.
   std::vector<CastJob> jobs;
   std::vector<OptTensor> opt;
   std::vector<int2> layer_chunks;
@@ -437,17 +481,17 @@ int finalize(dsb_handle* h) {
                  float sc) { jobs.push_back(CastJob{src, dst, rows, cols, lds, ldd, tr, sc, 0.f}); };
   for (int i = 0; i < h->L; ++i) {
     LayerState& ls = h->layers[i];
-    if (ls.has[DSB_PROJ_Q]) {
-      CKR(dalloc(h, &ls.Aqkv, 3L * r * D));
-      CKR(dalloc(h, &ls.AqkvT, (long)D * 3 * r));
-      CKR(dalloc(h, &ls.B2qkv, (long)W3 * 3 * r));
-      CK(hipMemset(ls.B2qkv, 0, (size_t)W3 * 3 * r * 2));
-      CKR(dalloc(h, &ls.BTq, (long)r * q));
-      CKR(dalloc(h, &ls.BTk, (long)r * kv));
-      CKR(dalloc(h, &ls.BTv, (long)r * kv));
+    if (has_qkv(ls)) {
+      CKR(dalloc_zero(h, &ls.Aqkv, 3L * r * D));
+      CKR(dalloc_zero(h, &ls.AqkvT, (long)D * 3 * r));
+      CKR(dalloc_zero(h, &ls.B2qkv, (long)W3 * 3 * r));
+      CKR(dalloc_zero(h, &ls.BTq, (long)r * q));
+      CKR(dalloc_zero(h, &ls.BTk, (long)r * kv));
+      CKR(dalloc_zero(h, &ls.BTv, (long)r * kv));
       const int outs[3] = {q, kv, kv}, rowoff[3] = {0, q, q + kv};
       bf16* bts[3] = {ls.BTq, ls.BTk, ls.BTv};
       for (int p = 0; p < 3; ++p) {
+        if (!ls.has[p]) continue;
         const dsb_lora_tensors& t = ls.lora[p];
         job(t.A, r, D, D, ls.Aqkv + (long)p * r * D, D, 0, 1.f);
         job(t.A, r, D, D, ls.AqkvT + p * r, 3 * r, 1, 1.f);
@@ -466,23 +510,26 @@ int finalize(dsb_handle* h) {
       job(t.B, D, r, r, ls.Bo, r, 0, s);
       job(t.B, D, r, r, ls.BTo, D, 1, s);
     }
-    if (ls.has[DSB_PROJ_GATE]) {
-      CKR(dalloc(h, &ls.Agu, 2L * r * D));
-      CKR(dalloc(h, &ls.AguT, (long)D * 2 * r));
-      CKR(dalloc(h, &ls.B2gu, 2L * I * 2 * r));
-      CK(hipMemset(ls.B2gu, 0, (size_t)2 * I * 2 * r * 2));
-      CKR(dalloc(h, &ls.BTg, (long)r * I));
-      CKR(dalloc(h, &ls.BTu, (long)r * I));
-      const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
-      const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
-      job(tg.A, r, D, D, ls.Agu, D, 0, 1.f);
-      job(tg.A, r, D, D, ls.AguT, 2 * r, 1, 1.f);
-      job(tu.A, r, D, D, ls.Agu + (long)r * D, D, 0, 1.f);
-      job(tu.A, r, D, D, ls.AguT + r, 2 * r, 1, 1.f);
-      job(tg.B, I, r, r, ls.B2gu, 2 * r, 0, s);
-      job(tg.B, I, r, r, ls.BTg, I, 1, s);
-      job(tu.B, I, r, r, ls.B2gu + (long)I * 2 * r + r, 2 * r, 0, s);
-      job(tu.B, I, r, r, ls.BTu, I, 1, s);
+    if (has_gu(ls)) {
+      CKR(dalloc_zero(h, &ls.Agu, 2L * r * D));
+      CKR(dalloc_zero(h, &ls.AguT, (long)D * 2 * r));
+      CKR(dalloc_zero(h, &ls.B2gu, 2L * I * 2 * r));
+      CKR(dalloc_zero(h, &ls.BTg, (long)r * I));
+      CKR(dalloc_zero(h, &ls.BTu, (long)r * I));
+      if (ls.has[DSB_PROJ_GATE]) {
+        const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
+        job(tg.A, r, D, D, ls.Agu, D, 0, 1.f);
+        job(tg.A, r, D, D, ls.AguT, 2 * r, 1, 1.f);
+        job(tg.B, I, r, r, ls.B2gu, 2 * r, 0, s);
+        job(tg.B, I, r, r, ls.BTg, I, 1, s);
+      }
+      if (ls.has[DSB_PROJ_UP]) {
+        const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
+        job(tu.A, r, D, D, ls.Agu + (long)r * D, D, 0, 1.f);
+        job(tu.A, r, D, D, ls.AguT + r, 2 * r, 1, 1.f);
+        job(tu.B, I, r, r, ls.B2gu + (long)I * 2 * r + r, 2 * r, 0, s);
+        job(tu.B, I, r, r, ls.BTu, I, 1, s);
+      }
     }
     if (ls.has[DSB_PROJ_DOWN]) {
       CKR(dalloc(h, &ls.Ad, (long)r * I));
@@ -495,7 +542,7 @@ int finalize(dsb_handle* h) {
       job(t.B, D, r, r, ls.Bd, r, 0, s);
       job(t.B, D, r, r, ls.BTd, D, 1, s);
     }
-    // optimizer tensors of this layer (A then B per projection, q..down)
+    // optimizer tensors of this layer (A then B per bound projection, q..down)
     const int first_chunk = (int)opt_chunks.size();
     const int ins[7] = {D, D, D, q, D, D, I}, outsz[7] = {q, kv, kv, D, I, I, D};
     for (int p = 0; p < DSB_NUM_PROJ; ++p) {
@@ -503,14 +550,10 @@ int finalize(dsb_handle* h) {
       const dsb_lora_tensors& t = ls.lora[p];
       const int na = r * ins[p], nb = outsz[p] * r;
       float *mA, *vA, *mB, *vB;
-      CKR(dalloc(h, &mA, na));
-      CKR(dalloc(h, &vA, na));
-      CKR(dalloc(h, &mB, nb));
-      CKR(dalloc(h, &vB, nb));
-      CK(hipMemset(mA, 0, (size_t)na * 4));
-      CK(hipMemset(vA, 0, (size_t)na * 4));
-      CK(hipMemset(mB, 0, (size_t)nb * 4));
-      CK(hipMemset(vB, 0, (size_t)nb * 4));
+      CKR(dalloc_zero(h, &mA, na));
+      CKR(dalloc_zero(h, &vA, na));
+      CKR(dalloc_zero(h, &mB, nb));
+      CKR(dalloc_zero(h, &vB, nb));
       const int ia = (int)opt.size();
       opt.push_back(OptTensor{t.A, t.gA, mA, vA, na, i});
       opt.push_back(OptTensor{t.B, t.gB, mB, vB, nb, i});
@@ -607,8 +650,8 @@ const char* cfg_name(int cfg) {
 // C once at `ob` bytes per element, plus `xrow` extra bytes per output row.
 template <class Epi>
 int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hipStream_t st,
-         double ob, double xrow, int cfg = -1) {
-  if (cfg < 0) cfg = pick_gemm_cfg(p.M, p.N);
+         double ob, double xrow) {
+  const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(p.M, p.N);
   const double K = (double)p.K1 + p.K2;
   KScope ks(h, st, std::string(cfg_name(cfg)) + "_" + epi, 2.0 * p.N * K, 0, 0,
             2.0 * K + ob * p.N + xrow, 0, 2.0 * p.N * K);
@@ -700,91 +743,112 @@ int dual(dsb_handle* h, const DualSpec* sp, int count, int r, hipStream_t s) {
   return 0;
 }
 
-// One segment of the cycle on stream st. Segments: 0 = RoPE table, LoRA
-// operand casts and the LM head (head.py:42-100); 1 .. L = decoder layer
-// L - seg, forward recompute + backward; L + 1 = per-layer clip, AdamW and the
-// publish into the served LoRA slots. The cycle is the segments in order
-// (captured as one graph); the pause-point path (reference base.py:148-208,
-// _maybe_pause per layer) launches them one graph per segment.
+HeadArgs head_args(dsb_handle* h) {
+  HeadArgs ha{};
+  ha.normed = h->normed; ha.ldh = h->D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.ldwt = h->ldwt;
+  ha.labels = h->labels;
+  ha.n = h->N; ha.n_dev = &h->d_hdr->n; ha.D = h->D; ha.V = h->V; ha.stats = h->stats;
+  ha.ntn = h->ntn;
+  ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
+  ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
+  ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH; ha.gemm_cfg = h->gemm_cfg;
+  return ha;
+}
+
+// One segment of the cycle on stream st. With C vocab chunks: segments
+// 0 .. C-1 run the LM head's LSE pass one chunk each (segment 0 first builds
+// the RoPE table, the LoRA operand casts, the final norm and the labels; the
+// last reduces the statistics to the LSE and the loss); C .. 2C-1 its
+// gradient pass (the last ends with the final-norm backward); then one
+// segment per decoder layer, last layer first (forward recompute +
+// backward); the last segment runs the per-layer clip, AdamW and the publish
+// into the served LoRA slots. The cycle is the segments in order (captured
+// as one graph); the pause-point path (reference base.py:148-208,
+// _maybe_pause per vocab chunk and per layer) launches them one graph per
+// segment.
 int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
   const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
   const int* nd = &h->d_hdr->n;
   const float eps = h->d.rms_eps;
   const double Hq = h->Hq;
-  if (seg == 0) {
-    h->kpos = 0;  // kernel-timing records restart with every cycle
-    {
-      KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
-      LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
-    }
-    {
-      KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
-      LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
-    }
-
+  const int C = h->nvc;
+  if (seg < 2 * C) {
     // ---- head: loss and grad wrt final_in (head.py:42-100)
-    {
-      KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
-    }
-    {
-      KScope ks(h, st, "labels", 0, 0, 0, 16, 0, 0);
-      LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
-    }
-    HeadArgs ha{};
-    ha.normed = h->normed; ha.ldh = D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.ldwt = h->ldwt;
-    ha.labels = h->labels;
-    ha.n = N; ha.n_dev = nd; ha.D = D; ha.V = h->V; ha.stats = h->stats; ha.ntn = h->ntn;
-    ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
-    ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
-    ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH;
-    ha.logits = h->logits; ha.ldl = h->ldwt;
-    {
-      // the logits product: 2·M·D·V of the head's 4·M·D·V (the dH product is the rest)
-      KScope ks(h, st, "gemm256_ce_stats", 2.0 * h->V * D, 0, 0,
-                2.0 * D + 8.0 * h->ntn + 4.0 * h->V, 0, 2.0 * h->V * D);
-      LK(head_stats(ha, st));
-    }
-    {
-      KScope ks(h, st, "ce_reduce", 0, 0, 0, 8.0 * h->ntn + 16, 0, 0);
-      LK(head_reduce(ha, st));
-    }
-    for (int c0 = 0; c0 < h->V; c0 += h->vchunk) {
-      const int Nc = std::min(h->vchunk, h->V - c0);
+    const HeadArgs ha = head_args(h);
+    if (seg == 0) {
+      h->kpos = 0;  // kernel-timing records restart with every cycle
       {
-        KScope ks(h, st, "ce_grad", 0, 0, 0, 4.0 * Nc + 2.0 * ((Nc + 7) / 8 * 8) + 8.0, 0, 0);
-        LK(head_chunk_grad(ha, c0, st));
+        KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
+        LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
       }
       {
-        KScope ks(h, st, std::string(cfg_name(pick_gemm_cfg(N, D))) + "_f32", 2.0 * Nc * D, 0, 0,
-                  2.0 * Nc + 8.0 * D, 0, 2.0 * Nc * D);
-        LK(head_chunk_dh(ha, c0, st));
+        KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
+        LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
+      }
+      {
+        KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
+        LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
+      }
+      {
+        KScope ks(h, st, "labels", 0, 0, 0, 16, 0, 0);
+        LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
       }
     }
+    const int c = seg < C ? seg : seg - C;
+    const int c0 = c * h->vchunk, Vc = std::min(h->vchunk, h->V - c0);
+    if (seg < C) {
+      {
+        // 2·n·Vc·D of the head's algorithmic 4·M·D·V (the logits product)
+        KScope ks(h, st, "gemm256_ce_stats", 2.0 * Vc * D, 0, 0, 2.0 * D + 8.0 * Vc / 256.0, 0,
+                  2.0 * Vc * D);
+        LK(head_stats(ha, c0, st));
+      }
+      if (seg == C - 1) {
+        KScope ks(h, st, "ce_reduce", 0, 0, 0, 8.0 * h->ntn + 16, 0, 0);
+        LK(head_reduce(ha, st));
+      }
+      return 0;
+    }
     {
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, h->g0, D, N, nd, D,
-                     eps, st));
+      // the logits of the chunk again (not algorithmic work: the price of
+      // not keeping them), with the dlogits in the epilogue
+      KScope ks(h, st, "gemm256_ce_grad", 2.0 * Vc * D, 0, 0, 2.0 * D + 2.0 * Vc, 0,
+                2.0 * Vc * D);
+      LK(head_chunk_grad(ha, c0, st));
+    }
+    {
+      const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(N, D);
+      KScope ks(h, st, std::string(cfg_name(cfg)) + "_f32", 2.0 * Vc * D, 0, 0,
+                2.0 * Vc + 8.0 * D, 0, 2.0 * Vc * D);
+      LK(head_chunk_dh(ha, c0, st));
+    }
+    if (c == C - 1) {
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 12.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, h->g0, D,
+                     N, nd, D, eps, st, nullptr, h->g32[0]));
     }
     return 0;
   }
-  if (seg <= h->L) {
-    const int li = h->L - seg;
+  if (seg < 2 * C + h->L) {
+    const int lo = seg - 2 * C;  // layers done before this one in the cycle
+    const int li = h->L - 1 - lo;
     // the incoming gradient alternates between the two g buffers layer by layer
-    bf16* g = ((seg - 1) & 1) ? h->g1 : h->g0;
-    bf16* gnext = ((seg - 1) & 1) ? h->g0 : h->g1;
+    bf16* g = (lo & 1) ? h->g1 : h->g0;
+    bf16* gnext = (lo & 1) ? h->g0 : h->g1;
+    const float* g32 = h->g32[lo & 1];
+    float* gnext32 = h->g32[(lo & 1) ^ 1];
     AttnArgs at{};
     at.q = h->qk; at.ldq = q + kv;
     at.k = h->qk + q; at.ldk = q + kv;
     at.v = h->qkv_pre + q + kv; at.ldv = W3;
-    at.ctx = h->ctx; at.ldc = q; at.o32 = nullptr; at.ldo32 = 0;  // dsum reads the bf16 ctx
+    at.ctx = h->ctx; at.ldc = q; at.o32 = h->o32; at.ldo32 = q;
     at.lse = h->lse; at.dsum = h->dsum; at.ld_stat = N + 1;
     at.dout = h->gctx; at.lddo = q;
     at.dq = h->gqkv; at.lddq = W3;
     at.dk = h->gqkv + q; at.lddk = W3;
     at.dv = h->gqkv + q + kv; at.lddv = W3;
     at.tiles = h->d_tiles; at.tiles_k = h->d_tiles_k; at.ntiles_dev = &h->d_hdr->ntiles;
-    at.max_tiles = h->max_tiles;
+    at.max_tiles = h->tile_cap;
     at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
     // one causal attention matmul = Hq·Hd·S flops (S = sum L(L+1), unmasked pairs ×2)
     const double au = Hq * 128.0;
@@ -792,8 +856,13 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     LayerState& ls = h->layers[li];
     const bf16* x = h->layer_in[li];
     const long ldx = h->act_ld;
-    const bool hq = ls.has[DSB_PROJ_Q], ho = ls.has[DSB_PROJ_O], hg = ls.has[DSB_PROJ_GATE],
+    const bool hq = has_qkv(ls), ho = ls.has[DSB_PROJ_O], hg = has_gu(ls),
                hd = ls.has[DSB_PROJ_DOWN];
+    // gate‖up: the saved forward activations when the store carries them
+    // (ffn.py:18-26, llama3.py:63-72), else recomputed into h->gu
+    const bool saved_gu = !h->gate_up_in.empty();
+    const bf16* gu = saved_gu ? h->gate_up_in[li] : h->gu;
+    const long ldgu = saved_gu ? h->ld_gate_up : 2L * I;
     const bf16* wqkv = (const bf16*)ls.w.qkv;
     const bf16* wo = (const bf16*)ls.w.o;
     const bf16* wgu = (const bf16*)ls.w.gate_up;
@@ -818,7 +887,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
                   h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     {
-      KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 2.0 * q + 4.0 * Hq, 0, 0);
+      KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 6.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_fwd(at, st));
     }
     if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Zo_b, r, st));
@@ -833,7 +902,12 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       LK(rmsnorm_fwd(h->resid, D, (const bf16*)ls.w.post_ln, h->xn2, D, N, nd, D, eps, st));
     }
     if (hg) CKR(skinny(h, h->xn2, D, ls.Agu, 2 * r, D, h->Zgu_b, 2 * r, st));
-    {
+    if (saved_gu) {
+      if (hd) {
+        KScope ks(h, st, "swiglu_h", 0, 0, 0, 6.0 * I, 0, 0);
+        LK(swiglu_h(gu, ldgu, h->hb, I, N, nd, I, st));
+      }
+    } else {
       // gate‖up (ffn.py:25-26) with h = silu(gate)·up in the epilogue; h is the
       // down projection's input and only feeds its LoRA terms. The fused form
       // needs I to be a multiple of 64 (whole 32-column fragments per half).
@@ -869,7 +943,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     {
       KScope ks(h, st, "swiglu_bwd", 0, 0, 0, 10.0 * I, 0, 0);
-      LK(swiglu_bwd(h->gh, I, h->gu, 2L * I, h->Ggu, 2L * I, N, nd, I, st));
+      LK(swiglu_bwd(h->gh, I, gu, ldgu, h->Ggu, 2L * I, N, nd, I, st));
     }
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
@@ -887,9 +961,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     if (hg) {
       const DualSpec d[2] = {
           {h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, h->gZgu_b, 2L * r,
-           ls.lora[DSB_PROJ_GATE].gB, h->s, 1},
+           grad_b(h, ls, DSB_PROJ_GATE), h->s, 1},
           {h->Ggu + I, 2L * I, I, h->Zgu_b + r, 2L * r, ls.BTu, h->gZgu_b + r, 2L * r,
-           ls.lora[DSB_PROJ_UP].gB, h->s, 1}};
+           grad_b(h, ls, DSB_PROJ_UP), h->s, 1}};
       // two launches: 2 × 28 column blocks at C3 would leave a 256-CU grid
       // with 224 blocks (one split fewer per pass), one pass keeps 28 × 9
       dual_g = dual(h, &d[0], 1, r, st);
@@ -905,19 +979,20 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
     if (hg) {
-      const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
-      const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
-      CKR(tn(h, h->gZgu_b, 2 * r, h->xn2, D, 2 * r, D, tg.gA, tu.gA, nullptr, r, 0, 1.f, st));
+      float* gAg = grad_a(h, ls, DSB_PROJ_GATE);
+      float* gAu = grad_a(h, ls, DSB_PROJ_UP);
+      CKR(tn(h, h->gZgu_b, 2 * r, h->xn2, D, 2 * r, D, gAg, gAu, nullptr, r, 0, 1.f, st));
       if (dual_g)
-        CKR(tn(h, h->Zgu_b, 2 * r, h->Ggu, 2L * I, r, I, tg.gB, nullptr, nullptr, r, 1, h->s, st));
+        CKR(tn(h, h->Zgu_b, 2 * r, h->Ggu, 2L * I, r, I, grad_b(h, ls, DSB_PROJ_GATE), nullptr,
+               nullptr, r, 1, h->s, st));
       if (dual_u)
-        CKR(tn(h, h->Zgu_b + r, 2 * r, h->Ggu + I, 2L * I, r, I, tu.gB, nullptr, nullptr, r, 1,
-               h->s, st));
+        CKR(tn(h, h->Zgu_b + r, 2 * r, h->Ggu + I, 2L * I, r, I, grad_b(h, ls, DSB_PROJ_UP),
+               nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(h->resid, D, h->gxn2, false, D, (const bf16*)ls.w.post_ln, g, D, h->grm, D, N,
-                     nd, D, eps, st));
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 16.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(h->resid, D, h->gxn2, false, D, (const bf16*)ls.w.post_ln, nullptr, D,
+                     h->grm, D, N, nd, D, eps, st, g32, h->grm32));
     }
     int dual_o = 1;
     if (ho) {
@@ -939,8 +1014,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       if (dual_o) CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      // per token: dO and O (bf16 ctx) rows read, Hq fp32 sums written
-      KScope ks(h, st, "attn_dsum", 0, 0, 0, 4.0 * q + 4.0 * Hq, 0, 0);
+      // per token: dO (bf16) and O (fp32) rows read, Hq fp32 sums written
+      KScope ks(h, st, "attn_dsum", 0, 0, 0, 6.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_bwd_prep(at, st));
     }
     {
@@ -959,12 +1034,12 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     int dual_q = 1, dual_k = 1, dual_v = 1;
     if (hq) {
       const DualSpec d[3] = {
-          {h->gqkv, W3, q, h->Zqkv_b, 3L * r, ls.BTq, h->gZqkv_b, 3L * r, ls.lora[DSB_PROJ_Q].gB,
-           h->s, 1},
+          {h->gqkv, W3, q, h->Zqkv_b, 3L * r, ls.BTq, h->gZqkv_b, 3L * r,
+           grad_b(h, ls, DSB_PROJ_Q), h->s, 1},
           {h->gqkv + q, W3, kv, h->Zqkv_b + r, 3L * r, ls.BTk, h->gZqkv_b + r, 3L * r,
-           ls.lora[DSB_PROJ_K].gB, h->s, 1},
+           grad_b(h, ls, DSB_PROJ_K), h->s, 1},
           {h->gqkv + q + kv, W3, kv, h->Zqkv_b + 2 * r, 3L * r, ls.BTv, h->gZqkv_b + 2 * r, 3L * r,
-           ls.lora[DSB_PROJ_V].gB, h->s, 1}};
+           grad_b(h, ls, DSB_PROJ_V), h->s, 1}};
       dual_q = dual_k = dual_v = dual(h, d, 3, r, st);
       if (dual_q < 0) return -1;
       if (dual_q) CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
@@ -978,23 +1053,22 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
     if (hq) {
-      const dsb_lora_tensors& tq = ls.lora[DSB_PROJ_Q];
-      const dsb_lora_tensors& tk = ls.lora[DSB_PROJ_K];
-      const dsb_lora_tensors& tv = ls.lora[DSB_PROJ_V];
-      CKR(tn(h, h->gZqkv_b, 3 * r, h->xn1, D, 3 * r, D, tq.gA, tk.gA, tv.gA, r, 0, 1.f, st));
+      CKR(tn(h, h->gZqkv_b, 3 * r, h->xn1, D, 3 * r, D, grad_a(h, ls, DSB_PROJ_Q),
+             grad_a(h, ls, DSB_PROJ_K), grad_a(h, ls, DSB_PROJ_V), r, 0, 1.f, st));
       if (dual_q)
-        CKR(tn(h, h->Zqkv_b, 3 * r, h->gqkv, W3, r, q, tq.gB, nullptr, nullptr, r, 1, h->s, st));
-      if (dual_k)
-        CKR(tn(h, h->Zqkv_b + r, 3 * r, h->gqkv + q, W3, r, kv, tk.gB, nullptr, nullptr, r, 1,
-               h->s, st));
-      if (dual_v)
-        CKR(tn(h, h->Zqkv_b + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, tv.gB, nullptr, nullptr,
+        CKR(tn(h, h->Zqkv_b, 3 * r, h->gqkv, W3, r, q, grad_b(h, ls, DSB_PROJ_Q), nullptr, nullptr,
                r, 1, h->s, st));
+      if (dual_k)
+        CKR(tn(h, h->Zqkv_b + r, 3 * r, h->gqkv + q, W3, r, kv, grad_b(h, ls, DSB_PROJ_K), nullptr,
+               nullptr, r, 1, h->s, st));
+      if (dual_v)
+        CKR(tn(h, h->Zqkv_b + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, grad_b(h, ls, DSB_PROJ_V),
+               nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 8.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(x, ldx, h->gxn1, false, D, (const bf16*)ls.w.in_ln, h->grm, D, gnext, D, N,
-                     nd, D, eps, st));
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 16.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(x, ldx, h->gxn1, false, D, (const bf16*)ls.w.in_ln, nullptr, D, gnext, D,
+                     N, nd, D, eps, st, h->grm32, gnext32));
     }
     return 0;
   }
@@ -1013,7 +1087,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
   return 0;
 }
 
-int num_segments(const dsb_handle* h) { return h->L + 2; }
+int num_segments(const dsb_handle* h) { return 2 * h->nvc + h->L + 1; }
 
 // The whole cycle on stream st.
 int enqueue(dsb_handle* h, hipStream_t st) {
@@ -1023,16 +1097,24 @@ int enqueue(dsb_handle* h, hipStream_t st) {
 
 // Drops every captured graph (pointers baked into them changed).
 void drop_graphs(dsb_handle* h) {
-  if (h->gexec) (void)hipGraphExecDestroy(h->gexec);
-  if (h->graph) (void)hipGraphDestroy(h->graph);
-  h->gexec = nullptr;
-  h->graph = nullptr;
-  for (auto& e : h->seg_exec)
-    if (e) (void)hipGraphExecDestroy(e);
-  for (auto& g : h->seg_graph)
-    if (g) (void)hipGraphDestroy(g);
-  h->seg_exec.assign(h->seg_exec.size(), nullptr);
-  h->seg_graph.assign(h->seg_graph.size(), nullptr);
+  for (auto& kv : h->graphs) {
+    GraphSet& g = kv.second;
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (g.graph) (void)hipGraphDestroy(g.graph);
+    for (auto& e : g.seg_exec)
+      if (e) (void)hipGraphExecDestroy(e);
+    for (auto& x : g.seg_graph)
+      if (x) (void)hipGraphDestroy(x);
+  }
+  h->graphs.clear();
+}
+
+// The graph set of the current cycle's attention grid capacity.
+GraphSet& graph_set(dsb_handle* h) {
+  for (auto& kv : h->graphs)
+    if (kv.first == h->tile_cap) return kv.second;
+  h->graphs.emplace_back(h->tile_cap, GraphSet{});
+  return h->graphs.back().second;
 }
 
 // Publish jobs (trainer.py:760-802): A -> a_slot[:r, :in] and s·B ->
@@ -1082,7 +1164,8 @@ int step_prepare(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float 
                  hipStream_t cs) {
   h->err.clear();
   if (n <= 0 || n > h->N) return fail(h, "dsb_step: n must be in [1, s_max]");
-  if (nseq <= 0 || nseq > h->d.max_seqs) return fail(h, "dsb_step: nseq out of range");
+  if (nseq <= 0 || nseq > h->d.max_seqs)
+    return fail(h, "dsb_step: nseq must be in [1, max_seqs]");
   if (step < 1) return fail(h, "dsb_step: step must be >= 1");
   if (!seq_lens) return fail(h, "dsb_step: null seq_lens");
   if (finalize(h)) return -1;
@@ -1094,6 +1177,7 @@ int step_prepare(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float 
                             &tiles);
   if (nv < 0) return fail(h, "dsb_step: seq_lens must be non-negative and sum to n");
   if ((int)tiles.size() > h->max_tiles) return fail(h, "dsb_step: too many attention tiles");
+  h->tile_cap = tile_capacity(h->N, h->max_tiles, (int)tiles.size());
   std::vector<int4> by_q, by_k;
   order_tiles(tiles, by_q, by_k);
   memcpy(hs + off_tiles, by_q.data(), by_q.size() * sizeof(int4));
@@ -1212,6 +1296,10 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
     return fail(nullptr, "dsb_create: hidden (<= 8192) and intermediate must be multiples of 8, vocab positive");
   if (d->s_max <= 0 || d->max_seqs <= 0 || d->n_layers <= 0)
     return fail(nullptr, "dsb_create: s_max, max_seqs, n_layers must be positive");
+  if (d->vocab_chunk < 0 || d->vocab_chunk % 256)
+    return fail(nullptr, "dsb_create: vocab_chunk must be 0 or a positive multiple of 256");
+  if (d->gemm_tile != 0 && d->gemm_tile != 256 && d->gemm_tile != 128 && d->gemm_tile != 64)
+    return fail(nullptr, "dsb_create: gemm_tile must be 0, 256, 128 or 64");
   if (d->family != DSB_FAMILY_LLAMA3 && d->family != DSB_FAMILY_QWEN3)
     return fail(nullptr, "dsb_create: unknown family");
   auto* h = new dsb_handle();
@@ -1220,13 +1308,16 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
   h->q = h->Hq * 128; h->kv = h->Hkv * 128; h->W3 = h->q + 2 * h->kv;
   h->I = d->intermediate; h->V = d->vocab; h->r = d->lora_rank; h->L = d->n_layers;
   h->N = d->s_max; h->s = d->lora_scaling; h->qwen = d->family == DSB_FAMILY_QWEN3;
-  h->max_tiles = max_tiles_for(d->s_max, d->max_seqs);
+  h->max_tiles = max_tiles_for(d->s_max, std::min(d->max_seqs, d->s_max));
   h->ntn = (h->V + 255) / 256;
-  {  // bf16 dlogits chunk: at most 2^28 elements (512 MiB), multiple of 256 columns
-    long vc = (1L << 28) / std::max(1, h->N);
-    vc = std::max<long>(256, vc / 256 * 256);
-    h->vchunk = (int)std::min<long>(vc, ((long)h->V + 255) / 256 * 256);
-  }
+  // LM-head vocab chunk: one pause point per chunk in each pass, and the
+  // width of the bf16 dlogits tile (16384 columns: 268 MB at 8192 rows)
+  h->vchunk = d->vocab_chunk > 0 ? d->vocab_chunk : 16384;
+  h->vchunk = (int)std::min<long>(h->vchunk, ((long)h->V + 255) / 256 * 256);
+  h->nvc = (h->V + h->vchunk - 1) / h->vchunk;
+  h->gemm_cfg = d->gemm_tile == 256 ? GEMM_BIG
+              : d->gemm_tile == 128 ? GEMM_MID
+              : d->gemm_tile == 64  ? GEMM_SKINNY : -1;
   h->layers.resize(h->L);
   h->ktiming = (d->flags & DSB_FLAG_KTIMING) != 0;
   hipError_t e = hipStreamCreateWithFlags(&h->hs, hipStreamNonBlocking);
@@ -1283,6 +1374,10 @@ int dsb_bind_weights(dsb_handle* h, int layer, const dsb_layer_weights* w) {
   LayerState& ls = h->layers[layer];
   ls.w = *w;
   const int D = h->D, W3 = h->W3, q = h->q, I = h->I;
+  // The borrowed weights may still be being written by work the caller
+  // issued on its own streams (a dtype conversion, an IPC copy): finish all
+  // of it before the library's stream reads them.
+  CK(hipDeviceSynchronize());
   if (!ls.qkvT) {
     CK(hipMalloc(&ls.qkvT, (size_t)D * W3 * 2));
     CK(hipMalloc(&ls.oT, (size_t)q * D * 2));
@@ -1305,6 +1400,7 @@ int dsb_bind_head(dsb_handle* h, const void* lm_head, const void* final_norm) {
   h->lm_w = (const bf16*)lm_head;
   h->norm_w = (const bf16*)final_norm;
   h->ldwt = ((long)h->V + 7) / 8 * 8;
+  CK(hipDeviceSynchronize());  // as in dsb_bind_weights: the head may still be in flight
   if (!h->lm_wT) {
     CK(hipMalloc(&h->lm_wT, (size_t)h->ldwt * h->D * 2));
     CK(hipMemsetAsync(h->lm_wT, 0, (size_t)h->ldwt * h->D * 2, h->hs));
@@ -1330,12 +1426,27 @@ int dsb_bind_activations(dsb_handle* h, const dsb_activations* a) {
   if (!h || !a || !a->layer_in || !a->final_in || !a->input_ids)
     return fail(h, "dsb_bind_activations: null argument");
   std::lock_guard<std::mutex> lk(h->mu);
+  if (h->in_step) return fail(h, "dsb_bind_activations: a segmented cycle is in progress");
   if (a->ld < h->D || a->ld % 8) return fail(h, "dsb_bind_activations: bad row stride");
+  if (a->mlp_gate_up && (a->ld_gate_up < 2L * h->I || a->ld_gate_up % 8))
+    return fail(h, "dsb_bind_activations: mlp_gate_up row stride must be a multiple of 8 and "
+                   ">= 2*intermediate");
+  std::vector<const bf16*> gu;
+  if (a->mlp_gate_up) {
+    for (int i = 0; i < h->L; ++i) {
+      if (!a->mlp_gate_up[i] || ((uintptr_t)a->mlp_gate_up[i] & 15))
+        return fail(h, "dsb_bind_activations: mlp_gate_up pointers must be non-null, 16-byte "
+                       "aligned");
+      gu.push_back((const bf16*)a->mlp_gate_up[i]);
+    }
+  }
   h->layer_in.assign(h->L, nullptr);
   for (int i = 0; i < h->L; ++i) {
     if (!a->layer_in[i]) return fail(h, "dsb_bind_activations: null layer_in");
     h->layer_in[i] = (const bf16*)a->layer_in[i];
   }
+  h->gate_up_in = gu;
+  h->ld_gate_up = a->mlp_gate_up ? (long)a->ld_gate_up : 0;
   h->final_in = (const bf16*)a->final_in;
   h->ids = a->input_ids;
   h->act_ld = a->ld;
@@ -1417,9 +1528,10 @@ int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, 
   // event pairs recorded inside a captured graph, so timed cycles replay the
   // same kernel sequence eagerly on the same stream.
   if ((h->d.flags & DSB_FLAG_GRAPH) && !h->graph_failed && !h->ktiming) {
-    if (!h->gexec) CKR(capture(h, [&] { return enqueue(h, h->hs); }, &h->graph, &h->gexec));
-    if (h->gexec) {
-      CK(hipGraphLaunch(h->gexec, h->hs));
+    GraphSet& gs = graph_set(h);
+    if (!gs.exec) CKR(capture(h, [&] { return enqueue(h, h->hs); }, &gs.graph, &gs.exec));
+    if (gs.exec) {
+      CK(hipGraphLaunch(gs.exec, h->hs));
       used_graph = true;
     }
   }
@@ -1450,20 +1562,22 @@ int dsb_step_segment(dsb_handle* h, int seg, int run_ahead) {
   if (seg != h->seg_next) return fail(h, "dsb_step_segment: segments must run in order");
   if (run_ahead < 0 || run_ahead > 64) return fail(h, "dsb_step_segment: run_ahead must be in [0, 64]");
   const int ns = num_segments(h);
-  if ((int)h->seg_exec.size() != ns) {
-    h->seg_exec.assign(ns, nullptr);
-    h->seg_graph.assign(ns, nullptr);
-  }
   bool launched = false;
   if ((h->d.flags & DSB_FLAG_GRAPH) && !h->graph_failed && !h->ktiming) {
-    if (!h->seg_exec[seg])
-      CKR(capture(h, [&] { return enqueue_segment(h, seg, h->hs); }, &h->seg_graph[seg],
-                  &h->seg_exec[seg]));
-    if (h->seg_exec[seg]) {
-      CK(hipGraphLaunch(h->seg_exec[seg], h->hs));
+    GraphSet& gs = graph_set(h);
+    if ((int)gs.seg_exec.size() != ns) {
+      gs.seg_exec.assign(ns, nullptr);
+      gs.seg_graph.assign(ns, nullptr);
+    }
+    if (!gs.seg_exec[seg])
+      CKR(capture(h, [&] { return enqueue_segment(h, seg, h->hs); }, &gs.seg_graph[seg],
+                  &gs.seg_exec[seg]));
+    if (gs.seg_exec[seg]) {
+      CK(hipGraphLaunch(gs.seg_exec[seg], h->hs));
       launched = true;
     }
   }
+  h->seg_graphed = launched;
   if (!launched && enqueue_segment(h, seg, h->hs)) return -1;
   h->seg_next = seg + 1;
   // Run-ahead bound (base.py:155-183): record this boundary and wait for the
@@ -1489,8 +1603,7 @@ int dsb_step_end(dsb_handle* h, void* stream, float* loss, int* n_valid, dsb_cyc
   h->in_step = false;
   if (h->seg_next != num_segments(h))
     return fail(h, "dsb_step_end: not every segment ran; the cycle's results are incomplete");
-  const bool graph = !h->seg_exec.empty() && h->seg_exec[0] != nullptr;
-  return step_finish(h, (hipStream_t)stream, graph, loss, n_valid, info);
+  return step_finish(h, (hipStream_t)stream, h->seg_graphed, loss, n_valid, info);
 }
 
 int dsb_bind_served(dsb_handle* h, int layer, int proj, void* a_slot, int64_t lda, void* b_slot,
@@ -1756,16 +1869,18 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
 }
 
 int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t* ids,
-                const int32_t* seq_lens, int nseq, int n, int D, int V, float* dH, float* loss,
-                int* n_valid, void* stream) {
-  if (D % 8 || V <= 0 || ldh % 8) return fail(nullptr, "dsb_op_head: D and ldh must be multiples of 8, V positive");
+                const int32_t* seq_lens, int nseq, int n, int D, int V, int vocab_chunk,
+                float* dH, float* loss, int* n_valid, void* stream) {
+  if (D % 8 || V <= 0 || ldh % 8 || n < 0 || vocab_chunk < 0 || vocab_chunk % 256)
+    return fail(nullptr, "dsb_op_head: D and ldh multiples of 8, V positive, vocab_chunk a "
+                         "multiple of 256");
   hipStream_t s = (hipStream_t)stream;
   std::vector<int32_t> pred(n > 0 ? n : 1);
   const int nv = pack_cycle(seq_lens, nseq, n, nullptr, pred.data(), nullptr);
   if (nv < 0) return fail(nullptr, "dsb_op_head: seq_lens must sum to n");
   TmpDev tmp;
   const int ntn = (V + 255) / 256;
-  const int vchunk = std::min(((V + 255) / 256) * 256, 4096);
+  const int vchunk = std::min(vocab_chunk > 0 ? vocab_chunk : 16384, ((V + 255) / 256) * 256);
   const long ldwt = ((long)V + 7) / 8 * 8;
   bf16* WT = tmp.alloc<bf16>((size_t)ldwt * D);
   int* dpred = tmp.alloc<int>(n + 1);
@@ -1777,12 +1892,11 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   float* scal = tmp.alloc<float>(4);
   int* err = tmp.alloc<int>(1);
   bf16* dlog = tmp.alloc<bf16>((size_t)(n + 1) * vchunk);
-  float* logits = tmp.alloc<float>((size_t)(n + 1) * ldwt);
-  if (!WT || !dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog || !logits)
+  if (!WT || !dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog)
     return fail(nullptr, "dsb_op_head: hipMalloc failed");
   float hsc[4] = {nv > 0 ? 1.f / nv : 0.f, 0.f, 0.f, 0.f};
   OPCK(hipMemcpy(scal, hsc, sizeof(hsc), hipMemcpyHostToDevice));
-  OPCK(hipMemcpy(dpred, pred.data(), n * sizeof(int32_t), hipMemcpyHostToDevice));
+  if (n > 0) OPCK(hipMemcpy(dpred, pred.data(), n * sizeof(int32_t), hipMemcpyHostToDevice));
   OPCK(hipMemset(err, 0, sizeof(int)));
   OPCK(hipMemsetAsync(WT, 0, (size_t)ldwt * D * 2, s));
   OPCK(transpose_bf16((const bf16*)lm_w, D, WT, ldwt, V, D, s));
@@ -1791,7 +1905,7 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w; a.WT = WT; a.ldwt = ldwt;
   a.labels = labels; a.n = n; a.n_dev = nullptr; a.D = D; a.V = V; a.stats = stats; a.ntn = ntn;
   a.tgt_logit = tl; a.lse = lse; a.loss_row = lr; a.loss_out = scal + 1; a.inv_nvalid = scal;
-  a.dlog = dlog; a.vchunk = vchunk; a.dH = dH; a.logits = logits; a.ldl = ldwt;
+  a.dlog = dlog; a.vchunk = vchunk; a.dH = dH; a.gemm_cfg = -1;
   OPCK(head_fwd_bwd(a, s));
   OPCK(hipStreamSynchronize(s));
   int herr = 0;
@@ -1832,24 +1946,68 @@ int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, i
   return 0;
 }
 
-int dsb_op_lora_dual(const void* G, int64_t ldg, const void* Z, int64_t ldz, const void* BT,
-                     int64_t ldbt, int n, int r, int C, float scale, void* gZ, int64_t ldgz,
-                     float* gB, int transpose_out, void* stream) {
-  if (!lora_dual_supported(r, r, C) || ldg % 8 || ldbt % 8 || n < 0)
-    return fail(nullptr, "dsb_op_lora_dual: r must be 16 or 32; C, ldg, ldbt multiples of 8");
+}  // extern "C"
+
+namespace {
+// Validates a dsb_op_lora_dual request and fills the kernel arguments; the
+// partial-sum workspace of pass i is laid out at work_off[i] floats.
+int dual_setup(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r,
+               const int* n_dev, DualArgs* a, long* work_elems, const char* who) {
+  if (!passes || count < 1 || count > 3 || n < 0 || n_alloc < n || n_alloc < 1) {
+    set_error("%s: 1 to 3 passes, 0 <= n <= n_alloc", who);
+    return -1;
+  }
+  const int C0 = passes[0].C;
+  int ncb = 0;
+  for (int i = 0; i < count; ++i) ncb += (passes[i].C + 511) / 512;
+  const int ns = std::max(1, std::min(256 / std::max(ncb, 1), n_alloc / 64));
+  long off = 0;
+  for (int i = 0; i < count; ++i) {
+    const dsb_dual_pass& p = passes[i];
+    if (!lora_dual_supported(r, r, p.C) || p.ldg % 8 || p.ldbt % 8 || p.ldg < p.C ||
+        p.ldbt < p.C || p.ldz < r || p.ldgz < r || !p.G || !p.Z || !p.BT || !p.gZ || !p.gB ||
+        !aligned16(p.G, p.Z, p.BT)) {
+      set_error("%s: r must be 16 or 32; C, ldg, ldbt multiples of 8 (>= C), ldz and ldgz >= r, "
+                "G/Z/BT 16-byte aligned", who);
+      return -1;
+    }
+    DualArgs& x = a[i];
+    x = DualArgs{};
+    x.X = (const bf16*)p.G; x.ldx = p.ldg; x.P = (const bf16*)p.Z; x.ldp = p.ldz;
+    x.W = (const bf16*)p.BT; x.ldw = p.ldbt; x.R1 = r; x.R2 = r; x.C = p.C;
+    x.n = n; x.n_dev = n_dev; x.n_alloc = n_alloc; x.nsplit = ns;
+    x.Y = (bf16*)p.gZ; x.ldy = p.ldgz; x.out = p.gB; x.scale = p.scale;
+    x.transpose_out = p.transpose_out;
+    x.work = reinterpret_cast<float*>(off);  // offset; rebased by the caller
+    off += (long)((p.C + 511) / 512) * n_alloc * r + (long)ns * p.C * r;
+  }
+  (void)C0;
+  *work_elems = off;
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int dsb_op_lora_dual(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r,
+                     void* stream) {
+  DualArgs a[3];
+  long elems = 0;
+  if (dual_setup(passes, count, n, n_alloc, r, nullptr, a, &elems, "dsb_op_lora_dual"))
+    return -1;
   if (n == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
-  const int ncb = (C + 511) / 512;
-  const int ns = std::max(1, std::min(256 / ncb, n / 64));
   TmpDev tmp;
-  float* work = tmp.alloc<float>((size_t)ncb * n * r + (size_t)ns * C * r);
-  if (!work) return fail(nullptr, "dsb_op_lora_dual: hipMalloc failed");
-  DualArgs a{};
-  a.X = (const bf16*)G; a.ldx = ldg; a.P = (const bf16*)Z; a.ldp = ldz;
-  a.W = (const bf16*)BT; a.ldw = ldbt; a.R1 = r; a.R2 = r; a.C = C;
-  a.n = n; a.n_dev = nullptr; a.n_alloc = n; a.nsplit = ns; a.work = work;
-  a.Y = (bf16*)gZ; a.ldy = ldgz; a.out = gB; a.scale = scale; a.transpose_out = transpose_out;
-  OPCK(lora_dual(&a, 1, s));
+  float* work = tmp.alloc<float>((size_t)elems);
+  int* nd = tmp.alloc<int>(1);
+  if (!work || !nd) return fail(nullptr, "dsb_op_lora_dual: hipMalloc failed");
+  OPCK(hipMemcpy(nd, &n, sizeof(int), hipMemcpyHostToDevice));
+  for (int i = 0; i < count; ++i) {
+    a[i].work = work + reinterpret_cast<long>(a[i].work);
+    a[i].n_dev = nd;
+    a[i].n = n_alloc;  // grid sized for the capacity, live rows from the device
+  }
+  OPCK(lora_dual(a, count, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
 }

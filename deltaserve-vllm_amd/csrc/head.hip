@@ -1,22 +1,28 @@
-// Final-norm output → LM head → shifted cross-entropy → dH, without the
-// [rows, vocab] fp32 logits or probabilities of the reference.
+// Final-norm output → LM head → shifted cross-entropy → dH, streaming the
+// vocabulary in chunks: no [rows, vocab] logits, probabilities or dlogits
+// ever exist in memory, only a bf16 [rows, chunk] dlogits tile per chunk.
 //
 // Semantics: deltaserve-plugin/deltaserve/bwd_services/common/head.py:42-100
 //   loss = sum_rows CE(logits, target) / n_valid, dlogits = (softmax - onehot)/n_valid,
 //   grad_rows = dlogits · W. Rows that predict nothing (the last token of each
 //   sequence) carry label -1 and contribute neither loss nor gradient.
 //
-// Pass 1 (LSE): one vocab-tiled MFMA GEMM whose epilogue stores the fp32
-//   logits (row-contiguous, [n, round_up(V, 8)]), reduces each 256-wide vocab
-//   tile to (max, sum exp) per row and picks out the target logit.
+// Pass 1 (LSE), one launch per vocab chunk: an MFMA GEMM logits tile whose
+//   epilogue reduces each 256-wide vocab tile to (max, sum exp) per row and
+//   picks out the target logit; nothing else is stored.
 // Reduce: combine the per-tile statistics into the row LSE and the row loss;
 //   a single-block deterministic sum gives the cycle loss.
-// Pass 2, per vocab chunk: an elementwise kernel turns the stored logits into
-//   bf16 dlogits for the chunk, then dH += dlogits_chunk · W_chunk with the
-//   transposed head copy (fp32 accumulate in the epilogue). The logits are
-//   the same fp32 values the reference computes once per chunk; keeping them
-//   (4.2 GB at 8192 rows × 128256 vocab) costs one write and one read instead
-//   of a second vocab-wide GEMM.
+// Pass 2, per vocab chunk: the same GEMM recomputes the chunk's logits (bit
+//   for bit those of pass 1: same kernel, same K order) and its epilogue
+//   writes bf16 (exp(logit - lse) - onehot)/n_valid into the chunk's dlogits
+//   tile; then dH += dlogits_chunk · W_chunk with the transposed head copy
+//   (fp32 accumulate in the epilogue).
+// The recompute costs one more 2·M·D·V product than keeping the logits
+// (4.2 GB of fp32 at 8192 rows × 128256 vocab), which is what the reference
+// does (head.py:84-96); the chunk is the reference's VOCAB_CHUNK unit, so
+// the caller can pause between chunks in both passes (head.py:78-80, :92-94).
+// dlogits pass through bf16 (the MFMA operand type) where the reference keeps
+// them in fp32; the dH product accumulates in fp32.
 #include "gemm_nt.h"
 #include "kernels.h"
 
@@ -25,43 +31,29 @@ namespace dsb {
 namespace {
 constexpr int CE_BN = 256;
 
+// Per 256-column vocab tile of chunk [c0, c0 + Vc): (max, sum exp) per row
+// into stats[m, c0/256 + tile] and the target logit where the tile holds it.
 struct EpiCEStats {
   const int* labels;
   float2* stats;
   int ntn;
   float* tgt_logit;
-  int V;
-  float* logits;
-  long ldl;
+  int c0, Vc;
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
     constexpr int TM = FM * 32, TN = FN * 32, BMl = WM * TM;
-    static_assert(WM * WN * 32 * (TN + 4) * 4 + WN * BMl * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2,
-                  "row staging + reduction scratch fit in the stage buffers");
-    // the logits, row-contiguous through the per-wave staging of the LDS
-    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
-      const int lim = V - n;
-      if (lim <= 0) return;
-      float* d = logits + (long)m * ldl + n;
-      if (lim >= 8) {
-        *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
-        *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
-      } else {
-        for (int i = 0; i < lim; ++i) d[i] = v[i];
-      }
-    });
+    static_assert(WN * BMl * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2, "reduction scratch fits");
     const int wn = wave % WN, wm = wave / WN;
     const int n0 = nw - wn * TN;
-    const int pn = n0 / (WN * TN);
+    const int pn = c0 / (WN * TN) + n0 / (WN * TN);
     const int lr = lane & 31, lh = lane >> 5;
-    // [WN][BMl], past the staging rows of all waves
-    float* red = reinterpret_cast<float*>(smem) + WM * WN * 32 * (TN + 4);
+    float* red = reinterpret_cast<float*>(smem);  // [WN][BMl]
     float mx[FM];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int m = mw + fm * 32 + lr;
-      const int t = (m < M) ? labels[m] : -1;
+      const int t = (m < M) ? labels[m] - c0 : -1;
       float v = -INFINITY;
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
@@ -69,7 +61,7 @@ struct EpiCEStats {
         for (int r = 0; r < 16; ++r) {
           const int n = nw + fn * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
           const float x = acc[fm][fn][r];
-          if (n < V) v = fmaxf(v, x);
+          if (n < Vc) v = fmaxf(v, x);
           if (n == t) tgt_logit[m] = x;
         }
       mx[fm] = fmaxf(v, __shfl_xor(v, 32, 64));
@@ -92,7 +84,7 @@ struct EpiCEStats {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int n = nw + fn * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          if (n < V) s += __expf(acc[fm][fn][r] - b);
+          if (n < Vc) s += __expf(acc[fm][fn][r] - b);
         }
       sm[fm] = s + __shfl_xor(s, 32, 64);
     }
@@ -116,43 +108,41 @@ struct EpiCEStats {
 };
 
 // dlog[m, j] = bf16((exp(logit[m, c0 + j] - lse[m]) - [c0 + j == t_m]) / n_valid)
-// for the chunk's columns j < Nc (0 for rows without a target); columns
-// [Nc, Nc8) (Nc8 = round_up(Nc, 8)) are written as zero so the dH product
-// runs its K loop over whole 16-byte chunks. Eight columns per thread.
-__global__ __launch_bounds__(256) void ce_grad_kernel(const float* __restrict__ logits, long ldl,
-                                                      const int* __restrict__ labels,
-                                                      const float* __restrict__ lse,
-                                                      const float* __restrict__ inv_nvalid,
-                                                      bf16* __restrict__ D, long ldd, int c0,
-                                                      int Nc, int Nc8, int n, const int* n_dev) {
-  int N = n;
-  if (n_dev) N = min(N, *n_dev);
-  const int G = Nc8 / 8;
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  const int m = (int)(idx / G), g = (int)(idx % G);
-  if (m >= N) return;
-  const int t = labels[m];
-  const float l = lse[m], sc = *inv_nvalid;
-  const int j0 = 8 * g;
-  const float* src = logits + (long)m * ldl + c0 + j0;
-  float x[8];
-  if (j0 + 8 <= Nc) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(src);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
-    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
-    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
-  } else {
+// for the chunk's columns j < Vc (0 for rows without a target); columns
+// [Vc, Nc8) (Nc8 = round_up(Vc, 8)) are written as zero so the dH product
+// runs its K loop over whole 16-byte chunks.
+struct EpiCEGrad {
+  const int* labels;
+  const float* lse;
+  const float* inv_nvalid;
+  bf16* D;
+  long ldd;
+  int c0, Vc, Nc8;
+  template <int FM, int FN, int WM, int WN>
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
+    const float sc = *inv_nvalid;
+    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+      const int lim = Nc8 - n;
+      if (lim <= 0) return;
+      const int t = labels[m];
+      const float l = lse[m];
+      float p[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = j0 + i < Nc ? src[i] : 0.f;
+      for (int i = 0; i < 8; ++i) {
+        const int j = n + i;
+        const float e = __expf(v[i] - l) - ((c0 + j) == t ? 1.f : 0.f);
+        p[i] = (t >= 0 && j < Vc) ? e * sc : 0.f;
+      }
+      bf16* d = D + (long)m * ldd + n;
+      if (lim >= 8) {
+        stg128(d, pack8(p));
+      } else {
+        for (int i = 0; i < lim; ++i) d[i] = (bf16)p[i];
+      }
+    });
   }
-  float p[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float e = __expf(x[i] - l) - ((c0 + j0 + i) == t ? 1.f : 0.f);
-    p[i] = (t >= 0 && j0 + i < Nc) ? e * sc : 0.f;
-  }
-  stg128(D + (long)m * ldd + j0, pack8(p));
-}
+};
 
 }  // namespace
 
@@ -195,12 +185,19 @@ __global__ __launch_bounds__(1024) void ce_loss_kernel(const float* __restrict__
   if (threadIdx.x == 0) out[0] = s * (*inv_nvalid);
 }
 
-hipError_t head_stats(const HeadArgs& a, hipStream_t s) {
+int head_num_chunks(const HeadArgs& a) { return (a.V + a.vchunk - 1) / a.vchunk; }
+
+static GemmProblem chunk_logits_problem(const HeadArgs& a, int c0) {
+  const int Vc = min(a.vchunk, a.V - c0);
+  return GemmProblem{a.normed, a.ldh, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
+                     a.n, Vc, a.D, 0, a.n_dev};
+}
+
+hipError_t head_stats(const HeadArgs& a, int c0, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  GemmProblem p{a.normed, a.ldh, a.W, (long)a.D, nullptr, 0, nullptr, 0,
-                a.n, a.V, a.D, 0, a.n_dev};
-  EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.V, a.logits, a.ldl};
-  return launch_gemm_cfg<256, CE_BN, 2, 2>(p, epi, s);
+  const int Vc = min(a.vchunk, a.V - c0);
+  EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, c0, Vc};
+  return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
 
 hipError_t head_reduce(const HeadArgs& a, hipStream_t s) {
@@ -215,13 +212,10 @@ hipError_t head_reduce(const HeadArgs& a, hipStream_t s) {
 }
 
 hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s) {
-  const int Nc = min(a.vchunk, a.V - c0), Nc8 = (Nc + 7) / 8 * 8;
-  const long items = (long)a.n * (Nc8 / 8);
-  if (items <= 0) return hipSuccess;
-  hipLaunchKernelGGL(ce_grad_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
-                     a.logits, a.ldl, a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0,
-                     Nc, Nc8, a.n, a.n_dev);
-  return hipGetLastError();
+  if (a.n <= 0) return hipSuccess;
+  const int Vc = min(a.vchunk, a.V - c0), Nc8 = (Vc + 7) / 8 * 8;
+  EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Vc, Nc8};
+  return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
 
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
@@ -229,13 +223,14 @@ hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
   GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, a.ldwt, nullptr, 0, nullptr, 0,
                 a.n, a.D, Nc8, 0, a.n_dev};
   EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
-  return launch_gemm(q, ef, s);
+  return launch_gemm(q, ef, s, a.gemm_cfg);
 }
 
 hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s) {
   hipError_t e;
   if (a.n <= 0) return hipSuccess;
-  if ((e = head_stats(a, s)) != hipSuccess) return e;
+  for (int c0 = 0; c0 < a.V; c0 += a.vchunk)
+    if ((e = head_stats(a, c0, s)) != hipSuccess) return e;
   if ((e = head_reduce(a, s)) != hipSuccess) return e;
   for (int c0 = 0; c0 < a.V; c0 += a.vchunk) {
     if ((e = head_chunk_grad(a, c0, s)) != hipSuccess) return e;

@@ -9,9 +9,13 @@ namespace dsb {
 // ---- norm_rope.hip
 hipError_t rmsnorm_fwd(const bf16* x, long ldx, const bf16* w, bf16* y, long ldy, int rows,
                        const int* rows_dev, int D, float eps, hipStream_t s);
+// out = bf16(o), o = rmsnorm_backward(x, g, w) + (resid | resid32), and the
+// fp32 o into out32 when set (resid and resid32 share the row stride ldr,
+// out and out32 the row stride ldo).
 hipError_t rmsnorm_bwd(const bf16* x, long ldx, const void* g, bool g_f32, long ldg,
                        const bf16* w, const bf16* resid, long ldr, bf16* out, long ldo,
-                       int rows, const int* rows_dev, int D, float eps, hipStream_t s);
+                       int rows, const int* rows_dev, int D, float eps, hipStream_t s,
+                       const float* resid32 = nullptr, float* out32 = nullptr);
 hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_freq,
                       int half, float* cosb, float* sinb, hipStream_t s);
 hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
@@ -130,18 +134,21 @@ struct HeadArgs {
   int n; const int* n_dev;
   int D, V;
   float2* stats;                  // [n_cap, ntn]
-  int ntn;
+  int ntn;                        // ceil(V / 256)
   float* tgt_logit;               // [n_cap]
   float* lse;                     // [n_cap]
   float* loss_row;                // [n_cap]
   float* loss_out;                // scalar: sum(loss_row)/n_valid
   const float* inv_nvalid;        // device scalar 1/n_valid (0 when none)
-  float* logits; long ldl;        // [n_cap, ldl] fp32, ldl = round_up(V, 8)
-  bf16* dlog; int vchunk;         // [n_cap, vchunk] bf16 scratch
+  bf16* dlog; int vchunk;         // [n_cap, vchunk] bf16 dlogits of one vocab chunk;
+                                  // vchunk a multiple of 256
   float* dH;                      // [n, D] fp32
+  int gemm_cfg;                   // tile of the dH product (-1: by shape)
 };
+// Chunk c0 (a multiple of vchunk) of pass 1 / pass 2; head_reduce between the passes.
+int head_num_chunks(const HeadArgs& a);
 hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s);
-hipError_t head_stats(const HeadArgs& a, hipStream_t s);
+hipError_t head_stats(const HeadArgs& a, int c0, hipStream_t s);
 hipError_t head_reduce(const HeadArgs& a, hipStream_t s);
 hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s);
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s);

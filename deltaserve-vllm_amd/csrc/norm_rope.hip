@@ -57,12 +57,15 @@ __global__ __launch_bounds__(NORM_NT) void rmsnorm_fwd_kernel(
   }
 }
 
-// out = bf16( rmsnorm_backward(x, g, w) + resid ), g fp32 or bf16.
+// o = rmsnorm_backward(x, g, w) + resid (g fp32 or bf16; resid bf16, fp32
+// resid32, or none) → out = bf16(o) and, when out32 is set, the fp32 o (the
+// residual-stream gradient the next layer adds to, kept unrounded).
 template <typename GT>
 __global__ __launch_bounds__(NORM_NT) void rmsnorm_bwd_kernel(
     const bf16* __restrict__ x, long ldx, const GT* __restrict__ g, long ldg,
-    const bf16* __restrict__ w, const bf16* __restrict__ resid, long ldr,
-    bf16* __restrict__ out, long ldo, int rows, const int* rows_dev, int D, float eps) {
+    const bf16* __restrict__ w, const bf16* __restrict__ resid,
+    const float* __restrict__ resid32, long ldr, bf16* __restrict__ out,
+    float* __restrict__ out32, long ldo, int rows, const int* rows_dev, int D, float eps) {
   int R = rows;
   if (rows_dev) R = min(R, *rows_dev);
   const int row = blockIdx.x;
@@ -121,8 +124,19 @@ __global__ __launch_bounds__(NORM_NT) void rmsnorm_bwd_kernel(
         unpack8(ldg128(resid + (long)row * ldr + c * 8), rf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] += rf[e];
+      } else if (resid32) {
+        const float* rp = resid32 + (long)row * ldr + c * 8;
+        const f32x4 a = *reinterpret_cast<const f32x4*>(rp);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(rp + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { o[e] += a[e]; o[e + 4] += b[e]; }
       }
       stg128(orow + c * 8, pack8(o));
+      if (out32) {
+        float* op = out32 + (long)row * ldo + c * 8;
+        *reinterpret_cast<f32x4*>(op) = f32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<f32x4*>(op + 4) = f32x4{o[4], o[5], o[6], o[7]};
+      }
     }
   }
 }
@@ -328,14 +342,17 @@ hipError_t rmsnorm_fwd(const bf16* x, long ldx, const bf16* w, bf16* y, long ldy
 
 hipError_t rmsnorm_bwd(const bf16* x, long ldx, const void* g, bool g_f32, long ldg,
                        const bf16* w, const bf16* resid, long ldr, bf16* out, long ldo,
-                       int rows, const int* rows_dev, int D, float eps, hipStream_t s) {
+                       int rows, const int* rows_dev, int D, float eps, hipStream_t s,
+                       const float* resid32, float* out32) {
   if (rows <= 0) return hipSuccess;
   if (g_f32)
     hipLaunchKernelGGL(rmsnorm_bwd_kernel<float>, dim3(rows), dim3(NORM_NT), 0, s, x, ldx,
-                       (const float*)g, ldg, w, resid, ldr, out, ldo, rows, rows_dev, D, eps);
+                       (const float*)g, ldg, w, resid, resid32, ldr, out, out32, ldo, rows,
+                       rows_dev, D, eps);
   else
     hipLaunchKernelGGL(rmsnorm_bwd_kernel<bf16>, dim3(rows), dim3(NORM_NT), 0, s, x, ldx,
-                       (const bf16*)g, ldg, w, resid, ldr, out, ldo, rows, rows_dev, D, eps);
+                       (const bf16*)g, ldg, w, resid, resid32, ldr, out, out32, ldo, rows,
+                       rows_dev, D, eps);
   return hipGetLastError();
 }
 

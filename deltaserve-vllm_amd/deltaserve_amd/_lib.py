@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 # timing); the in-tree build is the default.
 LIB_PATH = os.environ.get("DSB_LIB") or os.path.join(LIB_DIR, "libdsb.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
 ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
@@ -41,6 +41,7 @@ class DsbDesc(Structure):
         ("beta1", c_float), ("beta2", c_float), ("adam_eps", c_float),
         ("weight_decay", c_float), ("max_grad_norm", c_float),
         ("flags", c_uint32),
+        ("vocab_chunk", c_int32), ("gemm_tile", c_int32),
     ]
 
 
@@ -55,7 +56,15 @@ class DsbLoraTensors(Structure):
 
 class DsbActivations(Structure):
     _fields_ = [("layer_in", POINTER(c_void_p)), ("final_in", c_void_p),
-                ("input_ids", c_void_p), ("ld", c_int64)]
+                ("input_ids", c_void_p), ("ld", c_int64),
+                ("mlp_gate_up", POINTER(c_void_p)), ("ld_gate_up", c_int64)]
+
+
+class DsbDualPass(Structure):
+    _fields_ = [("G", c_void_p), ("ldg", c_int64), ("Z", c_void_p), ("ldz", c_int64),
+                ("BT", c_void_p), ("ldbt", c_int64), ("C", c_int32), ("scale", c_float),
+                ("gZ", c_void_p), ("ldgz", c_int64), ("gB", c_void_p),
+                ("transpose_out", c_int32)]
 
 
 class DsbCycleInfo(Structure):
@@ -122,15 +131,13 @@ _SIGS = {
                                 c_void_p, c_int64, c_void_p, c_int64, POINTER(c_int32),
                                 c_int, c_int, c_int, c_void_p]),
     "dsb_op_head": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, POINTER(c_int32), c_int,
-                            c_int, c_int, c_int, c_void_p, POINTER(c_float), POINTER(c_int),
-                            c_void_p]),
+                            c_int, c_int, c_int, c_int, c_void_p, POINTER(c_float),
+                            POINTER(c_int), c_void_p]),
     "dsb_op_lora_tn": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_int, c_int,
                                c_float, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "dsb_op_lora_skinny": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_int, c_int,
                                    c_void_p, c_int64, c_void_p]),
-    "dsb_op_lora_dual": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
-                                 c_int, c_int, c_int, c_float, c_void_p, c_int64, c_void_p,
-                                 c_int, c_void_p]),
+    "dsb_op_lora_dual": (c_int, [POINTER(DsbDualPass), c_int, c_int, c_int, c_int, c_void_p]),
     "dsb_op_clip_adamw": (c_int, [POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
                                   POINTER(c_void_p), POINTER(c_int32), POINTER(c_int32),
                                   c_int, c_int, c_float, c_float, c_float, c_float, c_float,

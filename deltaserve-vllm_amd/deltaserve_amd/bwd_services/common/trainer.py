@@ -28,6 +28,7 @@ from deltaserve_amd import _lib as L
 from deltaserve_amd import dprint
 from deltaserve_amd.bwd_services.base import BackwardService
 from deltaserve_amd.bwd_services.common.family import LORA_PROJS, Family
+from deltaserve_amd.checkpoint import AdapterCheckpointer, write_save_error
 from deltaserve_amd.ops import rope_inv_freq  # noqa: F401  (re-exported for callers)
 
 # PEFT adapter keys turned into fp32 masters (trainer.py:46-47, extended to the
@@ -35,7 +36,15 @@ from deltaserve_amd.ops import rope_inv_freq  # noqa: F401  (re-exported for cal
 _LORA_KEY_RE = re.compile(
     r"layers\.(\d+)\.(?:self_attn|mlp)\.(q|k|v|o|gate|up|down)_proj\.lora_([AB])\.weight")
 
-_DEFAULT_MAX_SEQS = 256
+
+def _graph_enabled(meta: dict) -> bool:
+    """One captured hipGraph per cycle unless the worker asked for eager
+    launches: this build's ``backward_hip_graph`` key when given, else the
+    reference config's ``backward_cuda_graph`` (config.py:94), else on."""
+    for key in ("backward_hip_graph", "backward_cuda_graph"):
+        if key in meta and meta[key] is not None:
+            return bool(meta[key])
+    return True
 
 
 class LoraSftTrainerService(BackwardService):
@@ -50,9 +59,7 @@ class LoraSftTrainerService(BackwardService):
         self.lora: dict = {}
         self._grads: dict = {}
         self._ft_keys: dict = {}
-        self._cycles_attempted = 0
-        self._last_cycle_epoch = None
-        self._pending_epoch_save = None
+        self._ckpt = AdapterCheckpointer(self)
         self._h = None
         self._act_key = None
         self._served_key = None
@@ -158,7 +165,7 @@ class LoraSftTrainerService(BackwardService):
 
         s_max = int(meta.get("max_saved_finetuning_tokens", 0) or 0)
         self._s_max = s_max
-        self._max_seqs = int(meta.get("backward_max_seqs", 0) or min(max(s_max, 1), _DEFAULT_MAX_SEQS))
+        self._ckpt.configure(meta)
         if s_max > 0:
             self._create_handle(s_max)
         dprint(f"[backward] {fam.name} built: {self.L} layers, {len(params)} LoRA tensors, "
@@ -184,11 +191,17 @@ class LoraSftTrainerService(BackwardService):
         d.rope_low_freq_factor = float(rs.get("low_freq_factor", 1.0))
         d.rope_high_freq_factor = float(rs.get("high_freq_factor", 1.0))
         d.rope_orig_max_pos = float(rs.get("original_max_position_embeddings", 1.0))
-        d.s_max, d.max_seqs = int(s_max), int(self._max_seqs)
+        meta = self.shared["meta"]
+        # every sequence of a cycle holds at least one of its s_max tokens, so
+        # s_max sequences admit any packing (backward_max_seqs may lower it:
+        # it only sizes the attention tile table)
+        d.s_max = int(s_max)
+        d.max_seqs = int(meta.get("backward_max_seqs") or s_max)
         d.beta1, d.beta2, d.adam_eps = 0.9, 0.999, 1e-8
         d.weight_decay, d.max_grad_norm = self.weight_decay, 1.0
-        meta = self.shared["meta"]
-        d.flags = L.FLAG_GRAPH if meta.get("backward_hip_graph", True) else 0
+        d.flags = L.FLAG_GRAPH if _graph_enabled(meta) else 0
+        d.vocab_chunk = int(meta.get("backward_vocab_chunk") or 0)
+        d.gemm_tile = int(meta.get("backward_gemm_tile") or 0)
         h = c_void_p()
         L.check(lib.dsb_create(byref(d), byref(h)), None, "dsb_create")
         self._h = h
@@ -213,6 +226,7 @@ class LoraSftTrainerService(BackwardService):
         li = activations["layer_in"]
         fi = activations["final_in"]
         ids = activations["concat_input_ids"]
+        gu = activations.get("mlp_gate_up")
         if len(li) != self.L:
             raise ValueError(f"activations carry {len(li)} layer inputs, the model has {self.L}")
         ld = fi.stride(0)
@@ -221,13 +235,32 @@ class LoraSftTrainerService(BackwardService):
                 raise TypeError("activation buffers must be bf16 CUDA [rows, D] with one row stride")
         if ids.dtype != torch.int64 or not ids.is_cuda:
             raise TypeError("concat_input_ids must be an int64 CUDA tensor")
-        key = (tuple(t.data_ptr() for t in li), fi.data_ptr(), ids.data_ptr(), ld)
+        ld_gu = 0
+        if gu is not None:
+            # the gate||up save point (accumulate.py:174, :210-212): used in place
+            # of the gate_up recompute (llama3.py:63-72, ffn.py:18-26)
+            if len(gu) != self.L:
+                raise ValueError(f"mlp_gate_up carries {len(gu)} layers, the model has {self.L}")
+            ld_gu = gu[0].stride(0)
+            for t in gu:
+                if (t.dtype != torch.bfloat16 or not t.is_cuda or t.stride(0) != ld_gu
+                        or t.stride(1) != 1 or t.shape[1] != 2 * self.inter):
+                    raise TypeError("mlp_gate_up buffers must be bf16 CUDA [rows, 2*intermediate] "
+                                    "with one row stride")
+        key = (tuple(t.data_ptr() for t in li), fi.data_ptr(), ids.data_ptr(), ld,
+               None if gu is None else tuple(t.data_ptr() for t in gu), ld_gu)
         if key == self._act_key:
             return
         ptrs = (c_void_p * self.L)(*[t.data_ptr() for t in li])
         self._act_ptrs = ptrs
+        gptrs = None
+        if gu is not None:
+            gptrs = (c_void_p * self.L)(*[t.data_ptr() for t in gu])
+        self._gu_ptrs = gptrs
         a = L.DsbActivations(ctypes.cast(ptrs, ctypes.POINTER(c_void_p)), fi.data_ptr(),
-                             ids.data_ptr(), ld)
+                             ids.data_ptr(), ld,
+                             None if gptrs is None else ctypes.cast(gptrs, ctypes.POINTER(c_void_p)),
+                             ld_gu)
         L.check(L.load().dsb_bind_activations(self._h, byref(a)), self._h, "dsb_bind_activations")
         self._act_key = key
 
@@ -239,7 +272,8 @@ class LoraSftTrainerService(BackwardService):
             raise RuntimeError(
                 f"{self.family.name} backward state not built (weights not shared)")
         self._last_mode = "graph"
-        seq_lens = [int(s) for s in sample_lens]
+        # zero-length samples hold no rows and predict nothing
+        seq_lens = [int(s) for s in sample_lens if int(s) > 0]
         n = int(n)
         if self._h is None:
             self._create_handle(int(activations["final_in"].shape[0]) - 1)
@@ -283,9 +317,10 @@ class LoraSftTrainerService(BackwardService):
         return self._gpu_grant is not None or bool(meta.get("backward_pause_boundaries"))
 
     def _run_segmented(self, lib, seq_lens, n, stream, loss, nv, info) -> int:
-        """trainer.py:503-678 with _maybe_pause before the cycle (:504) and at
-        every layer boundary (:577-581): segment 0 is the LM head, 1 .. L the
-        layers from the last, L + 1 the optimizer and publish."""
+        """trainer.py:503-678 with _maybe_pause before the cycle (:504), once
+        per vocab chunk in both LM-head passes (head.py:78-80, :92-94) and at
+        every layer boundary (:577-581); the last segment is the optimizer
+        and publish."""
         rc = lib.dsb_step_begin(self._h, L.i32_array(seq_lens), len(seq_lens), n,
                                 float(self.lr), int(self._opt_step), stream)
         if rc != 0:
@@ -293,7 +328,9 @@ class LoraSftTrainerService(BackwardService):
         run_ahead = self._run_ahead()
         nseg = lib.dsb_num_segments(self._h)
         for seg in range(nseg):
-            if seg <= self.L:
+            # a pause point before every head vocab chunk (both passes) and
+            # every layer; the optimizer segment runs straight after the last
+            if seg < nseg - 1:
                 self._maybe_pause()
             rc = lib.dsb_step_segment(self._h, seg, run_ahead)
             if rc != 0:
@@ -302,123 +339,82 @@ class LoraSftTrainerService(BackwardService):
         return rc if rc != 0 else rc_end
 
     # ------------------------------------------------------------ checkpoints
-    @torch.no_grad()
-    def _gather_adapter(self):
-        try:
-            local = {key: self.lora[k[0]][k[1]][k[2]].detach().to("cpu", copy=True)
-                     for k, key in self._ft_keys.items()}
-            return local, None
-        except Exception as e:  # noqa: BLE001
-            return None, f"rank 0: {type(e).__name__}: {e}"
-
-    def _snapshot(self, reason: str, epoch: int):
-        tensors, error = self._gather_adapter()
-        state = {"reason": reason, "epoch": int(epoch),
-                 "backward_cycles": int(self._cycles_attempted),
-                 "tokens_trained": int(self._total_tokens_trained),
-                 "last_loss": self._last_loss,
-                 "learning_rate": float(self.lr),
-                 "tp_size": 1,
-                 "source_adapter": self.shared["meta"].get("finetuning_lora_path")}
-        return tensors, error, state
-
-    def _write_adapter(self, out_dir: str, save_id: str, snap) -> None:
-        from deltaserve_amd.adapter_io import write_peft_adapter, write_save_error
-
-        tensors, error, state = snap
-        if error is None:
-            try:
-                write_peft_adapter(out_dir, tensors,
-                                   source_dir=self.shared["meta"].get("finetuning_lora_path"),
-                                   scaling=self.scaling, state={"save_id": save_id, **state})
-                dprint(f"[backward] adapter saved ({state['reason']}) → {out_dir}")
-                return
-            except Exception as e:  # noqa: BLE001
-                error = f"{type(e).__name__}: {e}"
-        dprint(f"[backward] adapter save ({state['reason']}) to {out_dir} FAILED: {error}")
-        write_save_error(out_dir, save_id, error)
+    def masters(self):
+        """(PEFT key, fp32 master) pairs of the adapter being trained."""
+        for (layer, proj, ab), key in self._ft_keys.items():
+            yield key, self.lora[layer][proj][ab]
 
     def save_adapter(self, out_dir: str, save_id: str, reason: str = "manual") -> None:
+        """A PEFT checkpoint of the current masters (trainer.py:386-391)."""
         if not self._built:
-            from deltaserve_amd.adapter_io import write_save_error
             write_save_error(out_dir, save_id, "trainer state not built")
             return
-        self._write_adapter(out_dir, save_id, self._snapshot(reason, self.current_epoch))
+        self._ckpt.write(out_dir, save_id, self._ckpt.snapshot(reason, self.current_epoch))
 
     def _handle_save_adapter(self, msg) -> None:
         self.save_adapter(str(msg.get("path")), str(msg.get("save_id")))
 
-    def _save_policy(self):
-        meta = self.shared.get("meta") or {}
-        return (meta.get("adapter_save_path"),
-                int(meta.get("adapter_save_every_backwards", 0) or 0),
-                bool(meta.get("adapter_save_every_epoch", False)),
-                int(meta.get("adapter_save_keep_last", 0) or 0))
-
     def _before_cycle(self, epoch: int, attempted: bool) -> None:
-        root, _, every_epoch, _ = self._save_policy()
-        if (attempted and root and every_epoch and self._built
-                and self._last_cycle_epoch is not None and epoch > self._last_cycle_epoch):
-            e = self._last_cycle_epoch
-            self._pending_epoch_save = (e, self._snapshot("epoch", e))
+        if attempted and self._built:
+            self._ckpt.before_cycle(epoch)
 
     def _after_cycle(self, epoch: int, attempted: bool) -> None:
-        if not attempted:
-            return
-        self._cycles_attempted += 1
-        self._last_cycle_epoch = epoch
-        root, every_n, _, keep_last = self._save_policy()
-        if self._pending_epoch_save is not None:
-            e, snap = self._pending_epoch_save
-            self._pending_epoch_save = None
-            self._write_adapter(os.path.join(root, f"epoch-{e}"), f"epoch-{e}", snap)
-        if root and every_n > 0 and self._built and self._cycles_attempted % every_n == 0:
-            name = f"backward-{self._cycles_attempted:06d}"
-            self._write_adapter(os.path.join(root, name), name,
-                                self._snapshot("every_backwards", epoch))
-            from deltaserve_amd.adapter_io import prune_checkpoints
-            prune_checkpoints(root, "backward-", keep_last)
+        if attempted:
+            if self._built:
+                self._ckpt.after_cycle(epoch)
+            else:
+                self._ckpt.schedule.cycle_done(epoch)
+
+    @property
+    def _cycles_attempted(self) -> int:
+        return self._ckpt.schedule.attempted
 
     # ------------------------------------------------------------ adapters
-    @staticmethod
-    def _key_of(key: str):
-        m = _LORA_KEY_RE.search(key)
-        return None if m is None else (int(m.group(1)), m.group(2), m.group(3))
-
     def export_lora_state(self) -> dict:
-        """trainer.py:749-754: the masters as {PEFT key: fp32 CPU tensor}."""
-        return {key: self.lora[layer][proj][ab].detach().float().cpu().clone()
-                for (layer, proj, ab), key in self._ft_keys.items()}
+        """trainer.py:749-754: the plain PEFT factors as fp32 CPU tensors."""
+        return {key: p.detach().float().cpu().clone() for key, p in self.masters()}
+
+    def _matched_adapter(self, ft: dict) -> dict:
+        """Pairs each master with the incoming adapter's tensor; ValueError
+        unless the adapter has exactly the launch adapter's LoRA tensors and
+        shapes (the rank and target modules are baked into the handle)."""
+        incoming = {}
+        for key, t in ft.items():
+            m = _LORA_KEY_RE.search(key)
+            if m is not None:
+                incoming[(int(m.group(1)), m.group(2), m.group(3))] = (key, t)
+        ours = {(layer, proj, ab): p for layer, projs in self.lora.items()
+                for proj, pair in projs.items() for ab, p in pair.items()}
+        if incoming.keys() != ours.keys():
+            raise ValueError(f"the adapter has {len(incoming)} LoRA tensors, the launch adapter "
+                             f"{len(ours)} (different target modules or layers)")
+        bad = [(k, tuple(incoming[k][1].shape), tuple(p.shape)) for k, p in ours.items()
+               if tuple(incoming[k][1].shape) != tuple(p.shape)]
+        if bad:
+            k, got, want = bad[0]
+            raise ValueError(f"LoRA tensor {k} has shape {got}, the launch adapter's is {want} "
+                             f"(different rank?)")
+        return {k: (ours[k], incoming[k][0], incoming[k][1]) for k in ours}
 
     def switch_adapter(self, ft: dict, hparams: dict) -> dict:
-        """trainer.py:680-742: copy another adapter into the masters in place
-        (graph and served slot stay valid), fresh optimizer and schedule."""
+        """trainer.py:680-742: train another adapter of the launch adapter's
+        shape. Its weights are copied into the existing masters (so the
+        handle, its graphs and the served slots stay valid), the optimizer
+        and schedule restart, and the new weights are published."""
         if not self._built:
             raise RuntimeError("the trainer was never built (no adapter at launch)")
-        scaling = float(hparams.get("lora_scaling", self.scaling))
-        if abs(scaling - self.scaling) > 1e-9:
-            raise ValueError(f"the adapter's alpha/r is {scaling}, the launch adapter's is "
+        alpha_r = float(hparams.get("lora_scaling", self.scaling))
+        if abs(alpha_r - self.scaling) > 1e-9:
+            raise ValueError(f"the adapter's alpha/r is {alpha_r}, the launch adapter's is "
                              f"{self.scaling}; they must match")
-        new = {}
-        for key, t in ft.items():
-            k = self._key_of(key)
-            if k is not None:
-                new[k] = t
-        have = {(layer, proj, ab): p for layer, d in self.lora.items()
-                for proj, dd in d.items() for ab, p in dd.items()}
-        if set(new) != set(have):
-            raise ValueError(f"the adapter has {len(new)} LoRA tensors, the launch adapter "
-                             f"{len(have)} (different target modules or layers)")
-        for k, p in have.items():
-            if tuple(new[k].shape) != tuple(p.shape):
-                raise ValueError(f"LoRA tensor {k} has shape {tuple(new[k].shape)}, the launch "
-                                 f"adapter's is {tuple(p.shape)} (different rank?)")
+        matched = self._matched_adapter(ft)
         if hparams.get("dry_run"):
-            return {"tensors": len(have), "dry_run": True}
+            return {"tensors": len(matched), "dry_run": True}
         with torch.no_grad():
-            for k, p in have.items():
-                p.copy_(new[k].to(p.device, torch.float32))
+            for k, (param, _, t) in matched.items():
+                param.copy_(t.to(param.device, torch.float32))
                 self._grads[k].zero_()
+        self._ft_keys = {k: key for k, (_, key, _) in matched.items()}
         self.lr = float(hparams["learning_rate"])
         self.weight_decay = float(hparams["weight_decay"])
         self.gamma = float(hparams["gamma"])
@@ -430,11 +426,10 @@ class LoraSftTrainerService(BackwardService):
         self._cur_epoch_seen = 0
         self._epoch_processed_tokens = 0
         self._total_tokens_per_epoch = int(hparams.get("total_tokens_per_epoch", 0))
-        self._ft_keys = {k: key for key in ft for k in [self._key_of(key)] if k is not None}
         self._publish_to_served()
-        dprint(f"[backward] switched to a new adapter: {len(have)} LoRA tensors, "
+        dprint(f"[backward] switched to a new adapter: {len(matched)} LoRA tensors, "
                f"lr={self.lr}, wd={self.weight_decay}, gamma={self.gamma}")
-        return {"tensors": len(have)}
+        return {"tensors": len(matched)}
 
     def _on_lora_buffers(self) -> None:
         self._served_key = None

@@ -190,8 +190,9 @@ def attn_backward(q, k, v, o32, lse, dout, seq_lens, Hq, Hkv):
 
 # ---------------------------------------------------------------- head
 
-def head_backward(normed, lm_w, ids, seq_lens):
-    """head.py:42-100 from the normed rows: (loss, n_valid, dH fp32 [n, D])."""
+def head_backward(normed, lm_w, ids, seq_lens, vocab_chunk=0):
+    """head.py:42-100 from the normed rows: (loss, n_valid, dH fp32 [n, D]),
+    streaming the vocabulary in chunks of ``vocab_chunk`` columns (0: 16384)."""
     _dev(normed, lm_w, ids)
     n, D = normed.shape
     V = lm_w.shape[0]
@@ -199,7 +200,8 @@ def head_backward(normed, lm_w, ids, seq_lens):
     loss = c_float(0.0)
     nv = c_int(0)
     L.check(L.load().dsb_op_head(_p(normed), _ld(normed), _p(lm_w), _p(ids), L.i32_array(seq_lens),
-                                 len(seq_lens), n, D, V, _p(dH), byref(loss), byref(nv), _stream()),
+                                 len(seq_lens), n, D, V, int(vocab_chunk), _p(dH), byref(loss),
+                                 byref(nv), _stream()),
             what="dsb_op_head")
     return loss.value, nv.value, dH
 
@@ -230,19 +232,37 @@ def lora_skinny(X, B):
     return Z
 
 
+def _dual_passes(passes):
+    arr = (L.DsbDualPass * len(passes))()
+    for i, (G, Z, BT, gZ, gB, scale, tr) in enumerate(passes):
+        _dev(G, Z, BT, gZ, gB)
+        arr[i] = L.DsbDualPass(G.data_ptr(), _ld(G), Z.data_ptr(), _ld(Z), BT.data_ptr(), _ld(BT),
+                               G.shape[1], float(scale), gZ.data_ptr(), _ld(gZ), gB.data_ptr(),
+                               int(tr))
+    return arr
+
+
+def lora_dual_batch(passes, n, n_alloc=None, entry="dsb_op_lora_dual"):
+    """One launch over 1-3 passes ``(G, Z, BT, gZ_out, gB_out, scale,
+    transpose_out)`` of the same rank over the first ``n`` rows (the row
+    count read from device memory, partials laid out for ``n_alloc``): per
+    pass gZ_out[:n] = bf16(G·BTᵀ) and gB_out = scale·Gᵀ·Z (ops.py:142, :144)."""
+    r = passes[0][2].shape[0]
+    arr = _dual_passes(passes)
+    L.check(getattr(L.load(), entry)(arr, len(passes), int(n), int(n_alloc or n), int(r),
+                                     _stream()), what=entry)
+
+
 def lora_dual(G, Z, BT, scale=1.0, transpose_out=True):
     """ops.py:142 and :144 from one pass over G [n, C]: returns
     (bf16(G·BTᵀ) [n, r], scale·Gᵀ·Z fp32 [C, r] (or [r, C])) for BT = (s·B)ᵀ
     [r, C]; with G = xin, BT = A, Z = grad_Z it gives Z and grad_A."""
-    _dev(G, Z, BT)
     n, C = G.shape
     r = BT.shape[0]
     gZ = torch.empty(n, r, dtype=BF16, device=G.device)
     shape = (C, r) if transpose_out else (r, C)
     gB = torch.empty(*shape, dtype=torch.float32, device=G.device)
-    L.check(L.load().dsb_op_lora_dual(_p(G), _ld(G), _p(Z), _ld(Z), _p(BT), _ld(BT), n, r, C,
-                                      float(scale), _p(gZ), _ld(gZ), _p(gB), int(transpose_out),
-                                      _stream()), what="dsb_op_lora_dual")
+    lora_dual_batch([(G, Z, BT, gZ, gB, scale, transpose_out)], n)
     return gZ, gB
 
 

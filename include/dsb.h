@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DSB_ABI_VERSION 1
+#define DSB_ABI_VERSION 2
 
 enum { DSB_FAMILY_LLAMA3 = 0, DSB_FAMILY_QWEN3 = 1 };
 enum { DSB_ROPE_DEFAULT = 0, DSB_ROPE_LINEAR = 1, DSB_ROPE_LLAMA3 = 2 };
@@ -39,7 +39,9 @@ typedef struct dsb_handle dsb_handle;
 
 /* Model and trainer constants: the backward `meta` dict of
  * deltaserve-plugin/deltaserve/ft_meta.py:131-213 plus the AdamW settings of
- * trainer.py:252-256. head_dim must be 128; lora_rank a multiple of 8. */
+ * trainer.py:252-256. head_dim must be 128; lora_rank a multiple of 8 in
+ * [8, 64] (the rank-r kernels tile r in 16-row MFMA tiles and keep up to 4
+ * of them per wave); hidden <= 8192. */
 typedef struct dsb_desc {
   int32_t abi_version;       /* DSB_ABI_VERSION */
   int32_t family;            /* DSB_FAMILY_* (Qwen3 adds per-head q/k RMSNorm) */
@@ -51,9 +53,12 @@ typedef struct dsb_desc {
   int32_t rope_type;         /* DSB_ROPE_* (ops.py:26-57) */
   float rope_factor, rope_low_freq_factor, rope_high_freq_factor, rope_orig_max_pos;
   int32_t s_max;             /* token capacity of one cycle (max_saved_finetuning_tokens) */
-  int32_t max_seqs;          /* sequence capacity of one cycle */
+  int32_t max_seqs;          /* sequence capacity of one cycle (s_max admits any packing) */
   float beta1, beta2, adam_eps, weight_decay, max_grad_norm;
   uint32_t flags;            /* DSB_FLAG_* */
+  int32_t vocab_chunk;       /* LM-head vocab columns per chunk and pause point, a multiple
+                                of 256 (0: 16384, the reference's VOCAB_CHUNK, head.py:25) */
+  int32_t gemm_tile;         /* dense-product tile: 0 by shape, else 256, 128 or 64 */
 } dsb_desc;
 
 /* Frozen bf16 base weights of one decoder layer, borrowed (the IPC-shared
@@ -80,12 +85,18 @@ typedef struct dsb_lora_tensors {
 
 /* The captured-activation store (accumulate.py:236-252): per-layer residual
  * inputs and the pre-final-norm residual, bf16 [s_max + 1, D] rows of stride
- * `ld`, and the token ids int64 [s_max]. Only rows [0, n) are read. */
+ * `ld`, and the token ids int64 [s_max]. Only rows [0, n) are read.
+ * mlp_gate_up (NULL when not captured): the optional per-layer gate‖up save
+ * point, bf16 [s_max + 1, 2·intermediate] (gate columns first) of row stride
+ * ld_gate_up; when bound, the cycle takes gate and up from it instead of
+ * recomputing the gate_up product (llama3.py:63-72, ffn.py:18-26). */
 typedef struct dsb_activations {
   const void* const* layer_in;  /* n_layers pointers */
   const void* final_in;
   const int64_t* input_ids;
   int64_t ld;
+  const void* const* mlp_gate_up;  /* n_layers pointers, or NULL */
+  int64_t ld_gate_up;
 } dsb_activations;
 
 /* Per-cycle device timing (ms), filled by dsb_step when requested. */
@@ -103,12 +114,16 @@ void dsb_destroy(dsb_handle* h);
 const char* dsb_last_error(const dsb_handle* h);
 
 /* Binds layer `layer`'s base weights (trainer.py:201-218). Makes the
- * transposed copies the dX products read, once. */
+ * transposed copies the dX products read, once, after waiting for all work
+ * already issued to the device (the weights may still be in flight on the
+ * caller's streams). */
 int dsb_bind_weights(dsb_handle* h, int layer, const dsb_layer_weights* w);
-/* Binds the LM head [vocab, D] and the final RMSNorm weight [D] (trainer.py:194-195). */
+/* Binds the LM head [vocab, D] and the final RMSNorm weight [D] (trainer.py:194-195);
+ * waits for the device like dsb_bind_weights. */
 int dsb_bind_head(dsb_handle* h, const void* lm_head, const void* final_norm);
-/* Binds one LoRA projection (trainer.py:231-243); proj is DSB_PROJ_*. q/k/v
- * must be bound together, and gate/up together. */
+/* Binds one LoRA projection (trainer.py:231-243); proj is DSB_PROJ_*. Any
+ * subset of the seven projections may be bound per layer (the reference's
+ * ld.get(proj) may be None, trainer.py:457-460); unbound ones stay frozen. */
 int dsb_bind_lora(dsb_handle* h, int layer, int proj, const dsb_lora_tensors* t);
 /* Binds the shared activation buffers (base.py:438-461 share_activations). */
 int dsb_bind_activations(dsb_handle* h, const dsb_activations* a);
@@ -124,9 +139,12 @@ int dsb_step(dsb_handle* h, const int32_t* seq_lens, int nseq, int n, float lr, 
 
 /* The same cycle in segments, for the GPU-yield contract of the reference's
  * BackwardService._maybe_pause (bwd_services/base.py:148-208), which the
- * reference calls at every layer boundary (llama3.py:342-344): segment 0 is
- * the LM head, segments 1 .. L the decoder layers from the last to the
- * first, segment L + 1 the clip, AdamW and publish. dsb_step_begin stages the
+ * reference calls once per vocab chunk in both LM-head passes (head.py:78-80,
+ * :92-94) and at every layer boundary (llama3.py:342-344). With C =
+ * ceil(vocab / vocab_chunk): segments 0 .. C-1 are the head's LSE pass, one
+ * vocab chunk each; C .. 2C-1 its gradient pass; 2C .. 2C+L-1 the decoder
+ * layers from the last to the first; 2C+L (the last) the clip, AdamW and
+ * publish. dsb_step_begin stages the
  * cycle (like dsb_step's first half); dsb_step_segment launches segment `seg`
  * (in order, each its own captured graph) and, when run_ahead > 0, keeps the
  * host at most run_ahead segments ahead of the GPU: the reference's
@@ -252,10 +270,12 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
                     int64_t lddv, const int32_t* seq_lens, int nseq, int Hq, int Hkv,
                     void* stream);
 /* head.py:42-100 from the normed rows: loss, n_valid and dH [n, D] fp32
- * (grad wrt the normed rows; the final-norm backward is dsb_op_rmsnorm_bwd). */
+ * (grad wrt the normed rows; the final-norm backward is dsb_op_rmsnorm_bwd),
+ * streaming the vocabulary in chunks of vocab_chunk columns (a multiple of
+ * 256; 0: 16384). */
 int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t* ids,
-                const int32_t* seq_lens, int nseq, int n, int D, int V, float* dH, float* loss,
-                int* n_valid, void* stream);
+                const int32_t* seq_lens, int nseq, int n, int D, int V, int vocab_chunk,
+                float* dH, float* loss, int* n_valid, void* stream);
 /* grad_A / grad_B of ops.py:143-144: out = scale · Pᵀ·X over n rows, P bf16
  * [n, R] (rows of out in groups of rg written to outs[j / rg]; transpose_out
  * writes out[c, j]). */
@@ -265,14 +285,27 @@ int dsb_op_lora_tn(const void* P, int64_t ldp, const void* X, int64_t ldx, int n
 /* Z / grad_Z of ops.py:141-142: Z = bf16(X·Bᵀ), X [n, K], B [R, K]. */
 int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, int n, int R, int K,
                        void* Z, int64_t ldz, void* stream);
-/* grad_Z and grad_B of ops.py:142 and :144 from one pass over gy = G [n, C]:
- * gZ = bf16(G·BTᵀ) with BT = (s·B)ᵀ [r, C] (ld ldbt), and gB[c, j] = scale ·
- * sum_t G[t, c]·Z[t, j] (fp32 [C, r], or [r, C] when transpose_out = 0; the
- * same pass over xin with BT = A and Z = grad_Z gives ops.py:141 Z and :143
- * grad_A). r in {16, 32}; C, ldg, ldbt multiples of 8. */
-int dsb_op_lora_dual(const void* G, int64_t ldg, const void* Z, int64_t ldz, const void* BT,
-                     int64_t ldbt, int n, int r, int C, float scale, void* gZ, int64_t ldgz,
-                     float* gB, int transpose_out, void* stream);
+/* One pass of dsb_op_lora_dual: grad_Z and grad_B of ops.py:142 and :144
+ * from one pass over gy = G [n, C]: gZ = bf16(G·BTᵀ) with BT = (s·B)ᵀ [r, C]
+ * (ld ldbt), and gB[c, j] = scale · sum_t G[t, c]·Z[t, j] (fp32 [C, r], or
+ * [r, C] when transpose_out = 0; the same pass over xin with BT = A and
+ * Z = grad_Z gives ops.py:141 Z and :143 grad_A). C, ldg, ldbt multiples of 8. */
+typedef struct dsb_dual_pass {
+  const void* G; int64_t ldg;
+  const void* Z; int64_t ldz;
+  const void* BT; int64_t ldbt;
+  int32_t C;
+  float scale;
+  void* gZ; int64_t ldgz;
+  float* gB;
+  int32_t transpose_out;
+} dsb_dual_pass;
+/* 1 to 3 passes of rank r in {16, 32} over n rows in one launch (the cycle
+ * batches q, k and v this way). The row count is read from device memory,
+ * as in the cycle, and the token-split partials are laid out for n_alloc >= n
+ * rows. Allocates its partial-sum workspace. */
+int dsb_op_lora_dual(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r,
+                     void* stream);
 /* trainer.py:624-636 + :668 on a flat tensor list: per-group clip then AdamW. */
 int dsb_op_clip_adamw(float* const* w, float* const* g, float* const* m, float* const* v,
                       const int32_t* numel, const int32_t* group, int ntensors, int ngroups,

@@ -6,8 +6,11 @@ the checker / the timed CPU baseline. The product path (libdsb.so and
 ``deltaserve_amd``) never calls it.
 
 Each function restates the reference's algorithm (paths relative to the
-reference checkout, under ``deltaserve-plugin/deltaserve/``) in float32 on
-CPU tensors. The reference trains LoRA on q/k/v/o only
+reference checkout, under ``deltaserve-plugin/deltaserve/``) in float32. The
+functions follow the device of their inputs: the pins and the small parity
+cases run them on CPU tensors; the BASELINE-width slices of the GPU tests run
+the same functions on float32 device tensors (torch's fp32 kernels, TF32 off)
+as the fp32 reference of those shapes. The reference trains LoRA on q/k/v/o only
 (``bwd_services/common/family.py:20``); this oracle extends the same
 ``proj``/``proj_backward`` rule to gate/up/down, which is what the MI355X
 build trains. How each function is pinned independently of this file is
@@ -111,10 +114,10 @@ def rope_inv_freq(head_dim: int, theta: float, rope_scaling: dict | None = None)
     raise NotImplementedError(f"RoPE type {rtype!r}")
 
 
-def rope_cos_sin(positions, head_dim, theta, rope_scaling=None):
+def rope_cos_sin(positions, head_dim, theta, rope_scaling=None, device=None):
     """ops.py:60-65 — (cos, sin) [n, head_dim/2] fp32."""
-    pos = torch.as_tensor(positions, dtype=torch.float32)
-    freqs = torch.outer(pos, rope_inv_freq(head_dim, theta, rope_scaling))
+    pos = torch.as_tensor(positions, dtype=torch.float32, device=device)
+    freqs = torch.outer(pos, rope_inv_freq(head_dim, theta, rope_scaling).to(pos.device))
     return freqs.cos(), freqs.sin()
 
 
@@ -174,8 +177,8 @@ def proj_backward(x, gy, W, A, B, s):
 # common/attention.py
 # --------------------------------------------------------------------------- #
 
-def _causal_mask(L):
-    return torch.triu(torch.ones(L, L, dtype=torch.bool), 1)
+def _causal_mask(L, device=None):
+    return torch.triu(torch.ones(L, L, dtype=torch.bool, device=device), 1)
 
 
 def attn_forward(qh, kh, vh, seq_lens, b_start, Hq, Hkv):
@@ -189,7 +192,7 @@ def attn_forward(qh, kh, vh, seq_lens, b_start, Hq, Hkv):
         k = kh[st:st + ln].transpose(0, 1).repeat_interleave(rep, 0)
         v = vh[st:st + ln].transpose(0, 1).repeat_interleave(rep, 0)
         sc = (q @ k.transpose(-1, -2)) * scale
-        sc = sc.masked_fill(_causal_mask(ln), -1e9)
+        sc = sc.masked_fill(_causal_mask(ln, qh.device), -1e9)
         p = torch.softmax(sc, dim=-1)
         out.append((p @ v).transpose(0, 1))
     n = qh.shape[0]
@@ -209,7 +212,7 @@ def attn_backward(qh, kh, vh, gctx, seq_lens, b_start, Hq, Hkv):
         q = qh[st:st + ln].transpose(0, 1)
         k = kh[st:st + ln].transpose(0, 1).repeat_interleave(rep, 0)
         v = vh[st:st + ln].transpose(0, 1).repeat_interleave(rep, 0)
-        mask = _causal_mask(ln)
+        mask = _causal_mask(ln, qh.device)
         p = torch.softmax(((q @ k.transpose(-1, -2)) * scale).masked_fill(mask, -1e9), dim=-1)
         g = g_all[st:st + ln].transpose(0, 1)
         dp = g @ v.transpose(-1, -2)
@@ -231,8 +234,11 @@ def _lora(lw, p):
     return lw.get(p + "A"), lw.get(p + "B")
 
 
-def layer_forward(x, lw, s, cos, sin, seq_lens, b_start, dims, eps, qk_norm=False):
-    """llama3.py:62-146 / qwen3.py:68-130 with ffn.py:18-26 (gate/up LoRA added)."""
+def layer_forward(x, lw, s, cos, sin, seq_lens, b_start, dims, eps, qk_norm=False,
+                  saved_gate_up=None):
+    """llama3.py:62-146 / qwen3.py:68-130 with ffn.py:18-26 (gate/up LoRA added).
+    ``saved_gate_up`` [n, 2I] (gate first): the captured pre-activations,
+    used instead of the gate/up recompute (ffn.py:21-24, llama3.py:142)."""
     Hq, Hkv, Hd = dims
     n = x.shape[0]
     xn1 = rmsnorm(x, lw["in_ln"], eps)
@@ -249,8 +255,12 @@ def layer_forward(x, lw, s, cos, sin, seq_lens, b_start, dims, eps, qk_norm=Fals
     ctx = attn_forward(qh, kh, vh, seq_lens, b_start, Hq, Hkv)
     resid_mid = x + proj(ctx, lw["o"], *_lora(lw, "o"), s)
     xn2 = rmsnorm(resid_mid, lw["post_ln"], eps)
-    gate = proj(xn2, lw["gate"], *_lora(lw, "gate"), s)
-    up = proj(xn2, lw["up"], *_lora(lw, "up"), s)
+    if saved_gate_up is not None:
+        inter = saved_gate_up.shape[-1] // 2
+        gate, up = saved_gate_up[:, :inter], saved_gate_up[:, inter:]
+    else:
+        gate = proj(xn2, lw["gate"], *_lora(lw, "gate"), s)
+        up = proj(xn2, lw["up"], *_lora(lw, "up"), s)
     return {"x": x, "xn1": xn1, "q_pre": q_pre, "k_pre": k_pre, "qh": qh, "kh": kh,
             "vh": vh, "ctx": ctx, "resid_mid": resid_mid, "xn2": xn2,
             "gate": gate, "up": up}
@@ -314,15 +324,19 @@ def head_backward(final_in, lm_w, norm_w, eps, ids, seq_lens):
     n = final_in.shape[0]
     if n_valid == 0:
         return 0.0, 0, torch.zeros_like(final_in)
+    dev = final_in.device
+    rows = torch.as_tensor(rows, dtype=torch.long, device=dev)
+    tgt = torch.as_tensor(tgt, dtype=torch.long, device=dev)
     normed = rmsnorm(final_in, norm_w, eps)
     h = normed[rows]
-    t = ids[tgt].long()
+    t = ids.to(dev)[tgt].long()
     logits = h @ lm_w.t()
     loss = F.cross_entropy(logits, t, reduction="sum")
     p = torch.softmax(logits, dim=-1)
-    p[torch.arange(n_valid), t] -= 1.0
+    del logits
+    p[torch.arange(n_valid, device=dev), t] -= 1.0
     p /= n_valid
-    gn = torch.zeros(n, final_in.shape[1], dtype=final_in.dtype)
+    gn = torch.zeros(n, final_in.shape[1], dtype=final_in.dtype, device=dev)
     gn[rows] = p @ lm_w
     return float(loss.item() / n_valid), n_valid, rmsnorm_backward(final_in, gn, norm_w, eps)
 
@@ -374,20 +388,29 @@ class Model:
         return self.meta.get("family", "llama3") == "qwen3"
 
 
-def forward_capture(model: Model, ids, seq_lens):
+def forward_capture(model: Model, ids, seq_lens, save_gate_up=False):
     """Full forward → the activation dict process_backward consumes
-    (tests/bwd_harness.py:242-258): layer_in[i], final_in, concat_input_ids."""
+    (tests/bwd_harness.py:242-258): layer_in[i], final_in, concat_input_ids,
+    and with ``save_gate_up`` the per-layer gate‖up projection outputs of the
+    ``mlp_gate_up`` save point (accumulate.py:134-135, :174)."""
     m = model.meta
     b_start, positions, *_ = pack(seq_lens)
-    cos, sin = rope_cos_sin(positions, m["head_dim"], m["rope_theta"], m.get("rope_scaling"))
+    dev = model.embed.device
+    cos, sin = rope_cos_sin(positions, m["head_dim"], m["rope_theta"], m.get("rope_scaling"),
+                            device=dev)
     s, eps = m["lora_scaling"], m["rms_norm_eps"]
-    x = model.embed[ids.long()]
-    layer_in = []
+    x = model.embed[ids.to(dev).long()]
+    layer_in, gate_up = [], []
     for lw in model.layers:
         layer_in.append(x)
         c = layer_forward(x, lw, s, cos, sin, seq_lens, b_start, model.dims, eps, model.qk_norm)
+        if save_gate_up:
+            gate_up.append(torch.cat([c["gate"], c["up"]], dim=1))
         x = layer_output(c, lw, s)
-    return {"layer_in": layer_in, "final_in": x, "concat_input_ids": ids}
+    out = {"layer_in": layer_in, "final_in": x, "concat_input_ids": ids}
+    if save_gate_up:
+        out["mlp_gate_up"] = gate_up
+    return out
 
 
 def process_backward(model: Model, activations, seq_lens, n, lr, step, clip=True,
@@ -400,16 +423,21 @@ def process_backward(model: Model, activations, seq_lens, n, lr, step, clip=True
     m = model.meta
     seq_lens = [int(x) for x in seq_lens]
     b_start, positions, *_ = pack(seq_lens)
-    cos, sin = rope_cos_sin(positions, m["head_dim"], m["rope_theta"], m.get("rope_scaling"))
+    dev = activations["final_in"].device
+    cos, sin = rope_cos_sin(positions, m["head_dim"], m["rope_theta"], m.get("rope_scaling"),
+                            device=dev)
     s, eps = m["lora_scaling"], m["rms_norm_eps"]
     ids = activations["concat_input_ids"][:n]
+    saved_gu = activations.get("mlp_gate_up")
     loss, n_valid, g = head_backward(activations["final_in"][:n].float(), model.lm_w,
                                      model.norm_w, eps, ids, seq_lens)
     grads = [None] * len(model.layers)
     for i in reversed(range(len(model.layers))):
         lw = model.layers[i]
         x = activations["layer_in"][i][:n].float()
-        c = layer_forward(x, lw, s, cos, sin, seq_lens, b_start, model.dims, eps, model.qk_norm)
+        gu = None if saved_gu is None else saved_gu[i][:n].float()
+        c = layer_forward(x, lw, s, cos, sin, seq_lens, b_start, model.dims, eps, model.qk_norm,
+                          saved_gate_up=gu)
         g, gr = layer_backward(g, c, lw, s, cos, sin, seq_lens, b_start, model.dims, eps,
                                model.qk_norm)
         if clip and gr:
@@ -429,8 +457,8 @@ def process_backward(model: Model, activations, seq_lens, n, lr, step, clip=True
 # Synthetic models (seeded per tensor name; BASELINE configs' init rules)
 # --------------------------------------------------------------------------- #
 
-def _gen(seed, name):
-    g = torch.Generator()
+def _gen(seed, name, device="cpu"):
+    g = torch.Generator(device=device)
     g.manual_seed((hash_name(name) + 1000003 * int(seed)) % (2 ** 63 - 1))
     return g
 
@@ -444,11 +472,13 @@ def hash_name(name: str) -> int:
 
 
 def make_model(meta: dict, seed: int = 0, projs=PROJS, w_std=0.02, b_std=0.01,
-               norm_jitter=0.0, bf16_round=True) -> Model:
+               norm_jitter=0.0, bf16_round=True, device="cpu") -> Model:
     """Random-init model of the given dims: linear weights N(0, w_std), norms 1
     (+ optional |N(0, jitter)|), LoRA A kaiming-uniform(a=√5) = U(±1/√in),
     B N(0, b_std). ``bf16_round`` rounds frozen weights to bf16 values (what
-    the GPU sees), so the fp32 oracle and the bf16 path share inputs."""
+    the GPU sees), so the fp32 oracle and the bf16 path share inputs.
+    ``device`` is where the tensors are drawn (each device's generator gives
+    its own seeded values) and kept."""
     D, Hq, Hkv, Hd = meta["hidden_size"], meta["num_attention_heads"], \
         meta["num_key_value_heads"], meta["head_dim"]
     I, V, r, L = meta["intermediate_size"], meta["vocab_size"], meta["lora_rank"], \
@@ -456,13 +486,14 @@ def make_model(meta: dict, seed: int = 0, projs=PROJS, w_std=0.02, b_std=0.01,
     q, kv = Hq * Hd, Hkv * Hd
 
     def rnd(name, *shape, std):
-        t = torch.randn(*shape, generator=_gen(seed, name)) * std
+        t = torch.randn(*shape, generator=_gen(seed, name, device), device=device) * std
         return t.to(torch.bfloat16).float() if bf16_round else t
 
     def norm(name, n):
-        t = torch.ones(n)
+        t = torch.ones(n, device=device)
         if norm_jitter:
-            t = t + torch.randn(n, generator=_gen(seed, name)).abs() * norm_jitter
+            t = t + torch.randn(n, generator=_gen(seed, name, device), device=device).abs() \
+                * norm_jitter
         return t.to(torch.bfloat16).float() if bf16_round else t
 
     shapes = {"q": (q, D), "k": (kv, D), "v": (kv, D), "o": (D, q),
@@ -479,8 +510,10 @@ def make_model(meta: dict, seed: int = 0, projs=PROJS, w_std=0.02, b_std=0.01,
         for pr in projs:
             out, inp = shapes[pr]
             bound = 1.0 / math.sqrt(inp)
-            lw[pr + "A"] = (torch.rand(r, inp, generator=_gen(seed, p + pr + "A")) * 2 - 1) * bound
-            lw[pr + "B"] = torch.randn(out, r, generator=_gen(seed, p + pr + "B")) * b_std
+            lw[pr + "A"] = (torch.rand(r, inp, generator=_gen(seed, p + pr + "A", device),
+                                       device=device) * 2 - 1) * bound
+            lw[pr + "B"] = torch.randn(out, r, generator=_gen(seed, p + pr + "B", device),
+                                       device=device) * b_std
         layers.append(lw)
     embed = rnd("embed", V, D, std=w_std)
     lm_w = embed if meta.get("tie_word_embeddings") else rnd("lm_head", V, D, std=w_std)

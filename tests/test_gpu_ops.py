@@ -191,15 +191,22 @@ def test_attention(seq_lens, Hq, Hkv):
         assert cosine(got, want) > 0.999
 
 
-@pytest.mark.parametrize("V", [1000, 211, 1027])
-def test_head(V):
+@pytest.mark.parametrize("V,vchunk", [(1000, 0), (211, 0), (1027, 0), (1027, 256), (5000, 768),
+                                      (2304, 512)])
+def test_head(V, vchunk):
+    """The streamed head against fp32 logits/softmax, with the vocabulary in
+    one chunk or several (including a last chunk that is not a multiple of
+    256 or of 8 columns)."""
     from deltaserve_amd import ops
     seq_lens = [5, 1, 64, 300]
     n, D = sum(seq_lens), 256
     normed = _bf(_rnd(n, D, seed=41))
     W = _bf(_rnd(V, D, seed=42) * 0.05)
     ids = torch.randint(0, V, (n,), generator=torch.Generator().manual_seed(43))
-    loss, nv, dH = ops.head_backward(normed.to(DEV), W.to(DEV), ids.to(DEV), seq_lens)
+    # targets in the first and last vocab columns too
+    ids[1], ids[6] = 0, V - 1
+    loss, nv, dH = ops.head_backward(normed.to(DEV), W.to(DEV), ids.to(DEV), seq_lens,
+                                     vocab_chunk=vchunk)
     _, _, rows, tgt, n_valid = O.pack(seq_lens)
     logits = normed.float()[rows] @ W.float().t()
     ref_loss = torch.nn.functional.cross_entropy(logits, ids[tgt], reduction="sum").item() / n_valid
@@ -263,6 +270,33 @@ def test_lora_dual(n, r, C):
     # the same pass over xin for Z and grad_A ([r, C])
     _, gA = ops.lora_dual(G, Z, BT, scale=1.0, transpose_out=False)
     assert max_rel(gA, Zc.t() @ Gc) < 1e-5
+
+
+@pytest.mark.parametrize("r", [16, 32])
+def test_lora_dual_batched_passes(r):
+    """The cycle's batched q/k/v launch: three passes in one launch, each
+    reading a column slice of one strided [n, q + 2kv] gradient, with Z and
+    grad_Z interleaved at a row stride of 3r, the live row count read from
+    device memory and the partials laid out for n_alloc > n rows."""
+    from deltaserve_amd import ops
+    n, n_alloc, q, kv = 1000, 1500, 1024, 256
+    W3 = q + 2 * kv
+    G = _bf(_rnd(n_alloc, W3, seed=58)).to(DEV)
+    Zall = _bf(_rnd(n_alloc, 3 * r, seed=59)).to(DEV)
+    BTs = [_bf(_rnd(r, c, seed=60 + i) * 0.1).to(DEV) for i, c in enumerate((q, kv, kv))]
+    gZall = torch.full((n_alloc, 3 * r), 7.0, dtype=torch.bfloat16, device=DEV)
+    cols = [(0, q), (q, kv), (q + kv, kv)]
+    gBs = [torch.empty(c, r, device=DEV) for _, c in cols]
+    passes = [(G[:, c0:c0 + c], Zall[:, i * r:(i + 1) * r], BTs[i], gZall[:, i * r:(i + 1) * r],
+               gBs[i], 2.0, True) for i, (c0, c) in enumerate(cols)]
+    ops.lora_dual_batch(passes, n, n_alloc)
+    Gc, Zc = G.float().cpu()[:n], Zall.float().cpu()[:n]
+    for i, (c0, c) in enumerate(cols):
+        Gi, Zi = Gc[:, c0:c0 + c], Zc[:, i * r:(i + 1) * r]
+        assert max_rel(gZall[:n, i * r:(i + 1) * r], Gi @ BTs[i].float().cpu().t()) < 8e-3
+        assert max_rel(gBs[i], 2.0 * (Gi.t() @ Zi)) < 1e-5
+    # rows past the live count are not written
+    assert (gZall[n:].float() == 7.0).all()
 
 
 def test_clip_adamw():

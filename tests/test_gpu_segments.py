@@ -1,8 +1,9 @@
 """Pause points and the served-slot publish on the GPU.
 
 * The segmented cycle (dsb_step_begin / dsb_step_segment / dsb_step_end, one
-  captured graph per segment, the reference's _maybe_pause at every layer
-  boundary, base.py:148-208) computes exactly what the single-graph cycle
+  captured graph per segment, the reference's _maybe_pause once per LM-head
+  vocab chunk in both passes and at every layer boundary, head.py:78-80,
+  :92-94, base.py:148-208) computes exactly what the single-graph cycle
   computes: same kernels in the same order, so loss, gradients and updated
   masters agree bit for bit, for any run-ahead bound.
 * A cleared GPU grant holds the cycle at a boundary until it is set again.
@@ -30,8 +31,8 @@ def _dev():
 SEQ = [37, 128, 1, 200, 64]
 
 
-def _setup(family="llama3", seed=5):
-    meta = tiny_meta(family=family, L=2)
+def _setup(family="llama3", seed=5, vocab_chunk=0):
+    meta = tiny_meta(family=family, L=2, vocab_chunk=vocab_chunk)
     model = O.make_model(meta, seed=seed, w_std=0.05, b_std=0.02, norm_jitter=0.2)
     n = sum(SEQ)
     ids = torch.randint(0, meta["vocab_size"], (n,), generator=torch.Generator().manual_seed(seed))
@@ -44,9 +45,10 @@ def _state(svc):
             for i, d in svc.lora.items() for p, dd in d.items() for ab, t in dd.items()}
 
 
-@pytest.mark.parametrize("family,run_ahead", [("llama3", 0), ("llama3", 2), ("qwen3", 1)])
-def test_segmented_cycle_equals_single_graph(family, run_ahead):
-    meta, model, gacts = _setup(family)
+@pytest.mark.parametrize("family,run_ahead,vchunk", [("llama3", 0, 0), ("llama3", 2, 256),
+                                                     ("qwen3", 1, 512)])
+def test_segmented_cycle_equals_single_graph(family, run_ahead, vchunk):
+    meta, model, gacts = _setup(family, vocab_chunk=vchunk)
     n = sum(SEQ)
     one = build_service(model, family)
     seg = build_service(model, family)
@@ -65,6 +67,26 @@ def test_segmented_cycle_equals_single_graph(family, run_ahead):
     finally:
         one.close()
         seg.close()
+
+
+def test_pause_points_per_vocab_chunk_and_layer():
+    """With V = 1000 in chunks of 256 (4 chunks) and 2 layers, the cycle
+    checks the grant before each of the 4 + 4 head segments and the 2 layer
+    segments (plus once on entry, trainer.py:504), not before the optimizer."""
+    from deltaserve_amd import _lib as L
+
+    meta, model, gacts = _setup(vocab_chunk=256)
+    n = sum(SEQ)
+    svc = build_service(model, "llama3")
+    svc.shared["meta"]["backward_pause_boundaries"] = True
+    calls = []
+    svc._maybe_pause = lambda: calls.append(1)
+    try:
+        svc.process_backward(gacts, SEQ, n, epoch=0)
+        assert L.load().dsb_num_segments(svc._h) == 2 * 4 + 2 + 1
+        assert len(calls) == 1 + 2 * 4 + 2
+    finally:
+        svc.close()
 
 
 def test_cleared_grant_holds_the_cycle_until_set():

@@ -54,7 +54,7 @@ def test_struct_layout_matches_header(tmp_path):
     L, _ = _lib()
     structs = {"dsb_desc": L.DsbDesc, "dsb_layer_weights": L.DsbLayerWeights,
                "dsb_lora_tensors": L.DsbLoraTensors, "dsb_activations": L.DsbActivations,
-               "dsb_cycle_info": L.DsbCycleInfo}
+               "dsb_cycle_info": L.DsbCycleInfo, "dsb_dual_pass": L.DsbDualPass}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dsb.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} . %zu\\n", sizeof({cname}));')
@@ -75,6 +75,26 @@ def test_struct_layout_matches_header(tmp_path):
         assert got[(cname, ".")] == ctypes.sizeof(cls), cname
         for f, _ in cls._fields_:
             assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
+
+
+def test_create_rejects_bad_descriptors():
+    """Argument checks of dsb_create run before any device call."""
+    L, lib = _lib()
+
+    def desc(**kw):
+        d = L.DsbDesc(abi_version=L.ABI_VERSION, family=0, n_layers=1, hidden=256, n_heads=2,
+                      n_kv_heads=1, head_dim=128, intermediate=512, vocab=1000, lora_rank=16,
+                      lora_scaling=2.0, rms_eps=1e-5, rope_theta=5e5, s_max=64, max_seqs=64)
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return d
+
+    h = ctypes.c_void_p()
+    for bad in (dict(abi_version=1), dict(head_dim=64), dict(lora_rank=12), dict(lora_rank=72),
+                dict(vocab_chunk=300), dict(vocab_chunk=-256), dict(gemm_tile=96),
+                dict(n_heads=3), dict(s_max=0)):
+        assert lib.dsb_create(ctypes.byref(desc(**bad)), ctypes.byref(h)) != 0, bad
+        assert L.last_error()
 
 
 def test_abi_version_constant():

@@ -548,6 +548,36 @@ def test_cycle_vs_transformers_qwen3_tied():
     check_cycle(O.process_backward, "qwen3")
 
 
+def check_saved_gate_up(capture=O.forward_capture):
+    """Saved shortcut == recompute (the reference's test_llama3_backward.py:
+    140-149): the cycle fed the forward's own gate‖up through the
+    mlp_gate_up save point gives the recompute cycle's loss and gradients
+    (the recompute path is pinned to transformers above)."""
+    meta = tiny_meta(L=2, D=128, Hq=2, Hkv=1, I=160, V=97, r=4)
+    model = O.make_model(meta, seed=12, w_std=0.08, b_std=0.05)
+    seq_lens = [6, 11]
+    ids = torch.randint(0, 97, (17,), generator=torch.Generator().manual_seed(3))
+    acts = capture(model, ids, seq_lens, save_gate_up=True)
+    plain = {k: v for k, v in acts.items() if k != "mlp_gate_up"}
+    l1, n1, g1 = O.process_backward(model, plain, seq_lens, 17, lr=0.0, step=1, update=False)
+    l2, n2, g2 = O.process_backward(model, acts, seq_lens, 17, lr=0.0, step=1, update=False)
+    assert n1 == n2 and abs(l1 - l2) < 1e-6 * abs(l1)
+    for a, b in zip(g1, g2):
+        for k in a:
+            assert _rel(b[k], a[k]) < 1e-5, k
+
+
+def test_saved_gate_up_equals_recompute():
+    check_saved_gate_up()
+
+
+def _bad_capture_gate_up(model, ids, seq_lens, save_gate_up=False):  # halves stored up‖gate
+    acts = O.forward_capture(model, ids, seq_lens, save_gate_up=save_gate_up)
+    I = acts["mlp_gate_up"][0].shape[1] // 2
+    acts["mlp_gate_up"] = [torch.cat([t[:, I:], t[:, :I]], 1) for t in acts["mlp_gate_up"]]
+    return acts
+
+
 def test_cycle_clip_and_update_compose():
     """process_backward(clip, update) == unclipped grads → per-layer
     clip_grad_norm_ → torch AdamW, on the same model."""
@@ -732,6 +762,7 @@ PLANTED = {
     "head_targets": lambda: check_head(_bad_head),
     "adamw_bias_correction": lambda: check_adamw(_bad_adamw),
     "cycle_lora_scale": lambda: check_cycle(_bad_cycle, "llama3", projs=("q", "v")),
+    "saved_gate_up_order": lambda: check_saved_gate_up(_bad_capture_gate_up),
 }
 
 

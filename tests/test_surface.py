@@ -1,12 +1,11 @@
 """Host-side surface of the drop-in backward child, on the CPU: service
-registry (registry.py:15-49), backward meta (ft_meta.py:24-213), PEFT adapter
-checkpoints (adapter_io.py:95-159), the parent's bwd_log row
-(coordinator.py:1079-1109), the pipe protocol and per-cycle wrapper of
-BackwardService (base.py:297-408, :468-633) and the workload configs."""
+registry (registry.py:15-49), PEFT adapter checkpoints and their periodic
+schedule (adapter_io.py:95-159, trainer.py:336-437), the pipe protocol and
+per-cycle wrapper of BackwardService (base.py:297-408, :468-633) and the
+workload configs."""
 
 from __future__ import annotations
 
-import csv
 import json
 import os
 import types
@@ -14,7 +13,8 @@ import types
 import pytest
 import torch
 
-from deltaserve_amd import adapter_io, bwd_log, configs, ft_meta
+from deltaserve_amd import checkpoint as adapter_io
+from deltaserve_amd import configs
 from deltaserve_amd.bwd_services import registry
 from deltaserve_amd.bwd_services.base import BackwardService
 
@@ -33,63 +33,6 @@ def test_registry_resolves_architectures():
 def test_registry_unknown_lists_supported():
     with pytest.raises(NotImplementedError, match="LlamaForCausalLM"):
         registry.get_service("MistralForCausalLM")
-
-
-# ------------------------------------------------------------------ meta
-
-def _cfg(**kw):
-    base = dict(num_attention_heads=32, num_key_value_heads=8, hidden_size=4096,
-                intermediate_size=14336, num_hidden_layers=32, vocab_size=128256,
-                rms_norm_eps=1e-5)
-    base.update(kw)
-    return types.SimpleNamespace(**base)
-
-
-def test_rope_scaling_normalisation():
-    assert ft_meta.rope_scaling_of(_cfg(rope_parameters={"rope_type": "default",
-                                                         "rope_theta": 5e5})) is None
-    rs = ft_meta.rope_scaling_of(_cfg(rope_scaling={"type": "llama3", "factor": 8,
-                                                    "low_freq_factor": 1, "high_freq_factor": 4,
-                                                    "original_max_position_embeddings": 8192}))
-    assert rs == {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
-                  "high_freq_factor": 4.0, "original_max_position_embeddings": 8192.0}
-    assert ft_meta.rope_scaling_of(_cfg(rope_scaling={"rope_type": "linear",
-                                                      "factor": 2})) == {"rope_type": "linear",
-                                                                          "factor": 2.0}
-
-
-@pytest.mark.parametrize("rp", [{"rope_type": "yarn", "factor": 4.0},
-                                {"rope_type": "default", "partial_rotary_factor": 0.5},
-                                {"rope_type": "default", "mrope_section": [16, 24, 24]},
-                                {"rope_type": "llama3", "factor": 8.0}])
-def test_rope_scaling_rejects_what_the_backward_cannot_reproduce(rp):
-    with pytest.raises(ValueError):
-        ft_meta.rope_scaling_of(_cfg(rope_parameters=rp))
-
-
-def test_rope_theta_sources():
-    assert ft_meta.rope_theta_of(_cfg(rope_parameters={"rope_theta": 1e6})) == 1e6
-    assert ft_meta.rope_theta_of(_cfg(rope_theta=5e5)) == 5e5
-    assert ft_meta.rope_theta_of(_cfg()) == 10000.0
-
-
-def test_lora_scaling_from_adapter_config(tmp_path):
-    assert ft_meta.read_lora_scaling(None) == 1.0
-    assert ft_meta.read_lora_scaling(str(tmp_path)) == 1.0
-    (tmp_path / "adapter_config.json").write_text(json.dumps({"r": 16, "lora_alpha": 32}))
-    assert ft_meta.read_lora_scaling(str(tmp_path)) == 2.0
-
-
-def test_backward_meta_keys():
-    ft = types.SimpleNamespace(learning_rate=2e-4, max_saved_finetuning_tokens=8192,
-                               backward_max_seqs=32)
-    m = ft_meta.build_backward_meta(_cfg(rope_parameters={"rope_theta": 5e5}), ft,
-                                    lm_head_key="lm_head.weight",
-                                    embed_weight_key="model.embed_tokens.weight",
-                                    has_final_norm=True, lora_scaling=2.0)
-    assert m["head_dim"] == 128 and m["rope_theta"] == 5e5 and m["rope_scaling"] is None
-    assert m["learning_rate"] == 2e-4 and m["max_saved_finetuning_tokens"] == 8192
-    assert m["norm_weight_key"] == "model.norm.weight" and m["tp_size"] == 1
 
 
 # ------------------------------------------------------------------ adapter files
@@ -122,7 +65,8 @@ def test_write_peft_adapter_roundtrip(tmp_path):
     res = adapter_io.read_save_result(str(out), "s1")
     assert res["saved"] is True
     assert adapter_io.read_save_result(str(out), "other") is None
-    assert not [f for f in os.listdir(out) if ".tmp-" in f]
+    assert sorted(os.listdir(out)) == sorted([adapter_io.WEIGHTS_FILE, adapter_io.CONFIG_FILE,
+                                              adapter_io.STATE_FILE])
 
 
 def test_adapter_config_copied_from_source(tmp_path):
@@ -146,17 +90,57 @@ def test_save_error_and_prune(tmp_path):
     assert sorted(os.listdir(tmp_path)) == ["e", "step-10", "step-3", "step-x"]
 
 
-# ------------------------------------------------------------------ bwd_log
+class _Owner:
+    """The attributes AdapterCheckpointer reads from a trainer."""
 
-def test_bwd_log_rows(tmp_path):
-    path = tmp_path / "m" / "bwd_log.csv"
-    log = bwd_log.BwdLog(str(path))
-    log.write_row(0, 100, 2.5)
-    log.write_row(1, 50, None)
-    rows = list(csv.reader(open(path)))
-    assert rows[0] == bwd_log.HEADER
-    assert rows[1][1:] == ["0", "1", "100", "2.5", "100"]
-    assert rows[2][1:] == ["1", "2", "50", "", "150"]
+    def __init__(self, root):
+        self.scaling = 2.0
+        self.lr = 1e-4
+        self._total_tokens_trained = 0
+        self._last_loss = None
+        self.shared = {"meta": {"adapter_save_path": str(root),
+                                "adapter_save_every_backwards": 2,
+                                "adapter_save_every_epoch": True,
+                                "adapter_save_keep_last": 2}}
+        self.w = torch.zeros(4, 8)
+
+    def masters(self):
+        yield "base_model.model.model.layers.0.self_attn.q_proj.lora_A.weight", self.w
+
+
+def test_checkpoint_schedule(tmp_path):
+    """trainer.py:405-437: the epoch checkpoint holds the state left by the
+    previous epoch's last cycle (captured when the next epoch's first cycle
+    starts, written after it); every 2nd attempted cycle writes
+    backward-NNNNNN, keeping the newest 2."""
+    from safetensors.torch import load_file
+
+    o = _Owner(tmp_path)
+    ck = adapter_io.AdapterCheckpointer(o)
+    ck.configure(o.shared["meta"])
+    for cycle, epoch in enumerate([0, 0, 0, 1, 1, 1], start=1):
+        ck.before_cycle(epoch)
+        o.w += 1.0  # the cycle's update
+        o._total_tokens_trained += 10
+        ck.after_cycle(epoch)
+    assert sorted(os.listdir(tmp_path)) == ["backward-000004", "backward-000006", "epoch-0"]
+    ep = json.loads((tmp_path / "epoch-0" / adapter_io.STATE_FILE).read_text())
+    assert ep["reason"] == "epoch" and ep["epoch"] == 0 and ep["backward_cycles"] == 3
+    assert ep["tokens_trained"] == 30 and ep["save_id"] == "epoch-0"
+    w = load_file(str(tmp_path / "epoch-0" / adapter_io.WEIGHTS_FILE))
+    assert float(next(iter(w.values()))[0, 0]) == 3.0  # after cycle 3, not cycle 4
+    last = json.loads((tmp_path / "backward-000006" / adapter_io.STATE_FILE).read_text())
+    assert last["reason"] == "every_backwards" and last["backward_cycles"] == 6
+
+
+def test_checkpoint_schedule_off_without_root(tmp_path):
+    o = _Owner(tmp_path)
+    ck = adapter_io.AdapterCheckpointer(o)
+    ck.configure({})
+    for epoch in (0, 1, 2):
+        ck.before_cycle(epoch)
+        ck.after_cycle(epoch)
+    assert os.listdir(tmp_path) == [] and ck.schedule.attempted == 3
 
 
 # ------------------------------------------------------------------ pipe protocol
