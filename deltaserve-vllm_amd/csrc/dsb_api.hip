@@ -1989,6 +1989,67 @@ int dual_setup(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r
 
 extern "C" {
 
+}  // extern "C"
+
+// ---- the allocation-free variant of dsb_op_lora_dual
+//
+// Its partial-sum workspace is this file-scope device array. Each GPU the
+// library runs on holds its own copy (64 MiB) until the process ends; host
+// code never uses the array's name as an address (on the host it is only a
+// stand-in): the device address is looked up once per device with
+// hipGetSymbolAddress and kept in scratch_dev.
+namespace {
+constexpr long kScratchFloats = 16L << 20;  // 64 MiB
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) float scratch[kScratchFloats];
+float* scratch_dev[kMaxDevices] = {};
+std::mutex scratch_mu;
+
+// This device's scratch address, looked up on its first use (with the device
+// current); null with the error set if the lookup fails.
+float* scratch_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("dsb_op_lora_dual_noalloc: no current HIP device (or device index >= %d)",
+              kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("dsb_op_lora_dual_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    scratch_dev[dev] = static_cast<float*>(p);
+  }
+  return scratch_dev[dev];
+}
+}  // namespace
+
+extern "C" {
+
+int dsb_op_lora_dual_noalloc(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r,
+                             void* stream) {
+  DualArgs a[3];
+  long elems = 0;
+  if (dual_setup(passes, count, n, n_alloc, r, nullptr, a, &elems,
+                 "dsb_op_lora_dual_noalloc"))
+    return -1;
+  if (elems > kScratchFloats)
+    return fail(nullptr, "dsb_op_lora_dual_noalloc: the partial sums of this request need more "
+                         "than the 64 MiB scratch array (fewer rows or columns per call)");
+  float* work = scratch_for_current_device();
+  if (!work) return -1;
+  if (n == 0) return 0;
+  // every partial is written before the reductions read it: nothing to clear
+  for (int i = 0; i < count; ++i) a[i].work = work + reinterpret_cast<long>(a[i].work);
+  OPCK(lora_dual(a, count, (hipStream_t)stream));
+  return 0;
+}
+
 int dsb_op_lora_dual(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r,
                      void* stream) {
   DualArgs a[3];

@@ -138,6 +138,8 @@ _SIGS = {
     "dsb_op_lora_skinny": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_int, c_int,
                                    c_void_p, c_int64, c_void_p]),
     "dsb_op_lora_dual": (c_int, [POINTER(DsbDualPass), c_int, c_int, c_int, c_int, c_void_p]),
+    "dsb_op_lora_dual_noalloc": (c_int, [POINTER(DsbDualPass), c_int, c_int, c_int, c_int,
+                                         c_void_p]),
     "dsb_op_clip_adamw": (c_int, [POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
                                   POINTER(c_void_p), POINTER(c_int32), POINTER(c_int32),
                                   c_int, c_int, c_float, c_float, c_float, c_float, c_float,

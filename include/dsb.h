@@ -306,6 +306,15 @@ typedef struct dsb_dual_pass {
  * rows. Allocates its partial-sum workspace. */
 int dsb_op_lora_dual(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r,
                      void* stream);
+/* dsb_op_lora_dual without any allocation, for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops). No
+ * counterpart in the reference. The row count n is a launch argument, the
+ * partial sums live in a 64 MiB device array of the library (one per GPU,
+ * held until the process ends; a request needing more fails with an error),
+ * and the call only enqueues on `stream` (no synchronisation). Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU race. */
+int dsb_op_lora_dual_noalloc(const dsb_dual_pass* passes, int count, int n, int n_alloc, int r,
+                             void* stream);
 /* trainer.py:624-636 + :668 on a flat tensor list: per-group clip then AdamW. */
 int dsb_op_clip_adamw(float* const* w, float* const* g, float* const* m, float* const* v,
                       const int32_t* numel, const int32_t* group, int ntensors, int ngroups,

@@ -192,3 +192,16 @@ def test_capture_entry_points_reject_bad_input():
         x = torch.zeros(4, 8, dtype=torch.bfloat16)
         i = torch.zeros(4, dtype=torch.int64)
         capture.save_rows(x, None, torch.zeros(5, 8, dtype=torch.bfloat16), i, i)
+
+
+def test_noalloc_dual_rejects_oversized_requests():
+    """The argument and size checks of dsb_op_lora_dual_noalloc run before any
+    device call: a request whose partial sums exceed the 64 MiB scratch array
+    fails with a message."""
+    L, lib = _lib()
+    fake = 1 << 20  # aligned stand-in addresses; never dereferenced
+    p = L.DsbDualPass(fake, 20480, fake, 32, fake, 20480, 20480, 1.0, fake, 32, fake, 1)
+    rc = lib.dsb_op_lora_dual_noalloc(ctypes.byref(p), 1, 100000, 100000, 32, None)
+    assert rc != 0 and "64 MiB" in L.last_error()
+    bad = L.DsbDualPass(fake, 20480, fake, 32, fake, 20480, 20480, 1.0, fake, 32, fake, 1)
+    assert lib.dsb_op_lora_dual_noalloc(ctypes.byref(bad), 1, 10, 10, 24, None) != 0  # rank 24
