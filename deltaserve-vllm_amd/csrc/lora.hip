@@ -187,7 +187,9 @@ __global__ __launch_bounds__(256, 2) void lora_tn_partial_kernel(TnArgs a) {
       const int bytes = rv > 0 ? (int)((((long)(rv - 1) * a.ldp) + R) * 2) : 0;
       const u32x4 rs = make_rsrc(rv > 0 ? Pg + (long)t * a.ldp : Pg, bytes);
       const int voff = row < 32 ? (int)(((long)row * a.ldp + ch * 8) * 2) : 0x7ff00000;
-      lds_dma16(rs, voff, lds_addr(d + XT + w * 512));
+      const bool live = w * 64 / per_row < rv;  // the wave's first row is valid
+      lds_dma16(pick_rsrc(live, rs, zero_rsrc()), live ? voff : lane * 16,
+                lds_addr(d + XT + w * 512));
     }
   };
   f32x4 acc[2][RB];
@@ -337,7 +339,10 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
       for (int j = 0; j < RB2; ++j) {
         const int row = 16 * j + (lane & 15), col = c0 + 32 * ks + 8 * (lane >> 4);
         const int off = col < a.C ? (int)(((long)row * a.ldw + col) * 2) : 0x7ff00000;
-        wf[ks][j] = __builtin_bit_cast(bf16x8, buf_load16(wr, off));
+        // a load with no column in range is not issued (it would complete
+        // out of order with the compiler-counted loads before it)
+        wf[ks][j] = c0 + 32 * ks < a.C ? __builtin_bit_cast(bf16x8, buf_load16(wr, off))
+                                       : bf16x8{};
       }
   }
   const bool pw = w < RB1;
@@ -357,7 +362,9 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
       const int bytes = rv > 0 ? (int)((((long)(rv - 1) * a.ldp) + R1) * 2) : 0;
       const u32x4 rs = make_rsrc(rv > 0 ? a.P + (long)t * a.ldp : a.P, bytes);
       const int voff = row < 32 ? (int)(((long)row * a.ldp + ch * 8) * 2) : 0x7ff00000;
-      lds_dma16(rs, voff, lds_addr(d + XT + w * 512));
+      const bool live = w * 64 / per_row < rv;  // the wave's first row is valid
+      lds_dma16(pick_rsrc(live, rs, zero_rsrc()), live ? voff : lane * 16,
+                lds_addr(d + XT + w * 512));
     }
   };
   f32x4 accT[8][RB1];
@@ -385,25 +392,16 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
 
 #pragma unroll
   for (int k = 0; k < NS - 1; ++k) issue(k, k);
-  // Skinny partials of chunk j are stored by the waves with (w - 2j) % 4 < 2,
-  // RB2 buffer stores each, always issued (rows past tb fall outside the
-  // descriptor and are dropped), so the vector-memory count is exact: after
-  // the loads of chunk k come the stores of chunks k-3 .. k-1 and the loads of
-  // chunks k+1 and k+2; the wait leaves exactly those outstanding.
-  auto stores_at = [&](int j) { return j >= 0 && ((w - 2 * j) & 3) < 2 ? 1 : 0; };
+  // Skinny partials of chunk j are stored by the waves with (w - 2j) % 4 < 2
+  // (RB2 buffer stores each; rows past tb fall outside the descriptor). The
+  // ring wait counts the loads of chunks k+1 .. k+NS-2 only: loads complete in
+  // issue order (none is wholly out of bounds), so it holds whatever order
+  // the stores complete in; a store still pending only makes it wait longer.
   const __amdgpu_buffer_rsrc_t yr =
       make_brsrc(workY + (long)cb * a.n_alloc * R2, tb * R2 * 4);
   for (int k = 0; k < nk; ++k) {
-    const int sa = stores_at(k - 3) + stores_at(k - 2) + stores_at(k - 1);  // uniform, 0..2
-    if (pw) {
-      if (sa == 0) wait_vm<(NS - 2) * (LPS + 1)>();
-      else if (sa == 1) wait_vm<(NS - 2) * (LPS + 1) + RB2>();
-      else wait_vm<(NS - 2) * (LPS + 1) + 2 * RB2>();
-    } else {
-      if (sa == 0) wait_vm<(NS - 2) * LPS>();
-      else if (sa == 1) wait_vm<(NS - 2) * LPS + RB2>();
-      else wait_vm<(NS - 2) * LPS + 2 * RB2>();
-    }
+    if (pw) wait_vm<(NS - 2) * (LPS + 1)>();
+    else wait_vm<(NS - 2) * LPS>();
     lds_barrier();  // chunk k visible; the slot of chunk k-1 is free
     issue(k + NS - 1, (k + NS - 1) % NS);
     const char* st = reinterpret_cast<const char*>(smem + (k % NS) * SE);

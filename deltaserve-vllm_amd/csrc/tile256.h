@@ -69,23 +69,26 @@ DSB_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }  // v_exp
 
 // Direct-to-LDS load of a ROWS × 128 bf16 tile: rows r < rows_valid of `base`
 // (row stride ld elements), columns < cols_valid (a multiple of 8); the rest
-// of the tile is zero-filled without touching memory. 256 threads issue
-// ROWS/16 loads each: load i of wave w covers tile rows 4·(4i + w) .. +3 and
-// lane l fills slot l%16 of row l/16 with chunk (l%16) ^ f(row).
+// of the tile is zero-filled. 256 threads issue ROWS/16 loads each: load i of
+// wave w covers tile rows 4·(4i + w) .. +3 and lane l fills slot l%16 of row
+// l/16 with chunk (l%16) ^ f(row). A load with no valid row (or no valid
+// column) reads the zero page, so every load touches memory and the loads of
+// a ring complete in issue order.
 template <int ROWS>
 DSB_DEV void tile256_dma(const bf16* base, long ld, int rows_valid, int cols_valid, bf16* tile,
                          int wave, int lane) {
   static_assert(ROWS % 16 == 0, "4 waves x 4 rows per load");
   const int bytes =
       rows_valid > 0 && cols_valid > 0 ? (int)(((long)(rows_valid - 1) * ld + cols_valid) * 2) : 0;
-  const u32x4 rs = make_rsrc(base, bytes);
+  const u32x4 rs = make_rsrc(base, bytes), zs = zero_rsrc();
   const int rl = lane >> 4, s = lane & 15;
 #pragma unroll
   for (int i = 0; i < ROWS / 16; ++i) {
-    const int r = 4 * (4 * i + wave) + rl;
+    const int r0 = 4 * (4 * i + wave), r = r0 + rl;  // r0: wave-uniform
     const int c = s ^ aswz(r);
+    const bool live = r0 < rows_valid && cols_valid > 0;  // row r0 has chunk 0 in bounds
     const int voff = c * 8 < cols_valid ? (int)(((long)r * ld + c * 8) * 2) : 0x7ff00000;
-    lds_dma16(rs, voff, lds_addr(tile + 4 * (4 * i + wave) * 128));
+    lds_dma16(pick_rsrc(live, rs, zs), live ? voff : lane * 16, lds_addr(tile + r0 * 128));
   }
 }
 
