@@ -156,26 +156,32 @@ class ActivationStore:
 
     ``layer_in[i]`` and ``final_in`` are bf16 ``[max_saved + 1, hidden]``
     (row ``max_saved`` is the scratch row), ``concat_input_ids`` is int64
-    ``[max_saved]``. The slot table has the reference's 7 slots per layer plus
-    the final norm's; slots of activations that the backward recomputes
-    (residual mid-point, gate/up, q/k/v, attention context) hold no buffer,
-    so their save calls are no-ops, as in the reference when those saves are
-    switched off.
+    ``[max_saved]``. With ``intermediate_size`` > 0 (the reference saves it
+    whenever the MLP's gate_up modules exist, accumulate.py:174, :210-212)
+    ``mlp_gate_up[i]`` is bf16 ``[max_saved + 1, 2·intermediate]``, the gate‖up
+    projection output the backward then reads instead of recomputing it. The
+    slot table has the reference's 7 slots per layer plus the final norm's;
+    slots of activations that the backward recomputes (residual mid-point,
+    q/k/v, attention context) hold no buffer, so their save calls are no-ops,
+    as in the reference when those saves are switched off.
     """
 
     STAGES = 4  # pinned staging slots for the index refresh (accumulate.py:262)
 
-    def __init__(self, num_layers: int, hidden_size: int, max_saved: int, device="cuda"):
-        if max_saved <= 0 or num_layers <= 0 or hidden_size <= 0:
+    def __init__(self, num_layers: int, hidden_size: int, max_saved: int, device="cuda",
+                 intermediate_size: int = 0):
+        if max_saved <= 0 or num_layers <= 0 or hidden_size <= 0 or intermediate_size < 0:
             raise ValueError("ActivationStore: sizes must be positive")
         self.num_layers, self.hidden_size, self.max_saved = num_layers, hidden_size, max_saved
+        self.intermediate_size = intermediate_size
         self.device = torch.device(device)
 
-        def buf():
-            return torch.zeros(max_saved + 1, hidden_size, dtype=torch.bfloat16,
-                               device=self.device)
+        def buf(width=hidden_size):
+            return torch.zeros(max_saved + 1, width, dtype=torch.bfloat16, device=self.device)
 
         self.layer_in = [buf() for _ in range(num_layers)]
+        self.mlp_gate_up = ([buf(2 * intermediate_size) for _ in range(num_layers)]
+                            if intermediate_size > 0 else [])
         self.final_in = buf()
         self.concat_input_ids = torch.zeros(max_saved, dtype=torch.int64, device=self.device)
         self.ft_src = torch.zeros(max_saved, dtype=torch.int64, device=self.device)
@@ -187,6 +193,8 @@ class ActivationStore:
         bufs: list = [None] * (SLOTS_PER_LAYER * num_layers + 1)
         for i in range(num_layers):
             bufs[SLOTS_PER_LAYER * i + SLOT_LAYER_IN] = self.layer_in[i]
+            if self.mlp_gate_up:
+                bufs[SLOTS_PER_LAYER * i + SLOT_GATE_UP] = self.mlp_gate_up[i]
         bufs[SLOTS_PER_LAYER * num_layers] = self.final_in
         self.op_bufs = bufs
         self.marker = torch.zeros(1, dtype=torch.int32, device=self.device)
@@ -281,7 +289,7 @@ class ActivationStore:
         n = min(n, self.max_saved - off)
         if n <= 0:
             return
-        for b in self.layer_in + [self.final_in]:
+        for b in self.layer_in + self.mlp_gate_up + [self.final_in]:
             b[off:off + n].zero_()
         self.concat_input_ids[off:off + n].zero_()
 
@@ -295,8 +303,11 @@ class ActivationStore:
     def activations(self) -> dict:
         """The activation dict a backward cycle takes (the ``buffers`` of the
         share_activations message, base.py:460-470)."""
-        return {"layer_in": self.layer_in, "final_in": self.final_in,
-                "concat_input_ids": self.concat_input_ids}
+        out = {"layer_in": self.layer_in, "final_in": self.final_in,
+               "concat_input_ids": self.concat_input_ids}
+        if self.mlp_gate_up:
+            out["mlp_gate_up"] = self.mlp_gate_up
+        return out
 
 
 def _register_torch_op():

@@ -247,3 +247,56 @@ def test_store_filled_by_the_op_trains_like_a_direct_handoff():
     finally:
         one.close()
         two.close()
+
+
+def test_gate_up_slot_feeds_the_saved_path():
+    """A store built with the intermediate size has the reference's default
+    mlp_gate_up save point (accumulate.py:174, :210-212): the gate‖up
+    projection output saved through the op lands bit-exact in its buffer,
+    ``activations()`` hands it to the backward, and the cycle on the store
+    equals the same activations (gate‖up included) handed over directly; the
+    saved path's loss agrees with the recompute path's."""
+    C = _capture()
+    meta = tiny_meta(family="llama3", L=2)
+    model = O.make_model(meta, seed=4, w_std=0.05, b_std=0.02, norm_jitter=0.2)
+    S, D, Lyr, inter = (meta["max_saved_finetuning_tokens"], meta["hidden_size"], 2,
+                        meta["intermediate_size"])
+    n = sum(SEQ)
+    ids = torch.randint(0, meta["vocab_size"], (n,), generator=torch.Generator().manual_seed(4))
+    acts = O.forward_capture(model, ids, SEQ, save_gate_up=True)
+    store = C.ActivationStore(Lyr, D, S, intermediate_size=inter)
+    assert len(store.mlp_gate_up) == Lyr and store.mlp_gate_up[0].shape == (S + 1, 2 * inter)
+    st = store.arm_op_step(list(range(n)), n, 0)
+    with C.active_state(st):
+        for i in range(Lyr):
+            C.dserve_save_rows(acts["layer_in"][i].to(torch.bfloat16).cuda(), None,
+                               store.marker, store.slot(i))
+            C.dserve_save_rows(acts["mlp_gate_up"][i].to(torch.bfloat16).cuda(), None,
+                               store.marker, store.slot(i, C.SLOT_GATE_UP))
+        C.dserve_save_rows(acts["final_in"].to(torch.bfloat16).cuda(), None, store.marker,
+                           store.final_slot)
+    store.save_final_ids(ids.cuda(), st)
+    torch.cuda.synchronize()
+    for i in range(Lyr):
+        assert torch.equal(store.mlp_gate_up[i][:n].cpu(), acts["mlp_gate_up"][i].to(torch.bfloat16))
+        assert not store.mlp_gate_up[i][n:S].any()
+    got = store.activations()
+    assert "mlp_gate_up" in got
+
+    direct = gpu_activations(acts, S)
+    recompute = {k: v for k, v in direct.items() if k != "mlp_gate_up"}
+    one, two, three = (build_service(model, "llama3") for _ in range(3))
+    try:
+        l1, n1 = one.process_backward(got, SEQ, n, epoch=0)
+        l2, n2 = two.process_backward(direct, SEQ, n, epoch=0)
+        l3, n3 = three.process_backward(recompute, SEQ, n, epoch=0)
+        assert n1 == n2 == n3 and l1 == l2, (l1, l2)
+        assert abs(l1 - l3) / abs(l3) < 1e-3, (l1, l3)
+        for i, d in one.lora.items():
+            for p, dd in d.items():
+                for ab, t in dd.items():
+                    assert torch.equal(t.grad, two.lora[i][p][ab].grad)
+    finally:
+        one.close()
+        two.close()
+        three.close()
