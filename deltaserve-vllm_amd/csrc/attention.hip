@@ -1,16 +1,18 @@
 // Packed varlen causal GQA attention (head_dim 128) on gfx950 MFMA:
 // forward recompute (ctx, optional fp32 ctx copy, row log-sum-exp) and the
-// FA2-style backward split into a dK/dV pass (one block per 128 keys of one kv
-// head, summing its q-head group in registers, no atomics) and a dQ pass
-// (forward and dQ blocks: 4 waves of 32 queries sharing one kv head, see
-// q_block). Softmax statistics, P and dS stay fp32 in registers; P and dS are
+// FA2-style backward split into a dQ pass (forward and dQ blocks: 4 waves of
+// 32 queries sharing one kv head, see q_block), which also forms
+// dsum = rowsum(dO∘O) for its rows, and a dK/dV pass that runs after it (one
+// block per 128 keys of one kv head, summing its q-head group in registers, no
+// atomics). Softmax statistics, P and dS stay fp32 in registers; P and dS are
 // rounded to bf16 only as MFMA operands.
 //
 // Semantics: deltaserve-plugin/deltaserve/bwd_services/common/attention.py
 //   attn_forward_core   :20-45   (scale 1/sqrt(Hd), causal mask, fp32 softmax)
 //   attn_backward_core  :48-112  (dS = P∘(dP − rowsum(dP∘P)), GQA group sums)
-// rowsum(dP∘P) is computed as rowsum(dO∘O), with the fp32 O of the forward
-// when it wrote one, else with the bf16 ctx (the backward cycle).
+// rowsum(dP∘P) is computed as rowsum(dO∘O), with the fp32 O copy of the
+// forward when the caller passes one (the backward cycle does), else with the
+// bf16 ctx.
 // The reference fills masked scores with −1e9 before the softmax; exp of that
 // underflows to exactly 0, so skipping masked pairs is the same arithmetic.
 //
@@ -257,40 +259,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
-// dsum[h, t] = sum_d dO[t, h*128 + d] * O[t, h*128 + d], O from the fp32
-// copy when the forward wrote one (FP32 = true), else from the bf16 ctx (the
-// backward cycle: O rounded to bf16, as flash-attention backwards take it;
-// it saves the 4-byte copy's write and re-read). 16 lanes per (token, head)
-// row, each reading 8 dims; 4 rows per wave, 16 per block.
-template <bool FP32>
-__global__ __launch_bounds__(256) void attn_dsum_kernel(AttnArgs a) {
-  int N = a.n;
-  if (a.n_dev) N = min(N, *a.n_dev);
-  const long item = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (item >= (long)N * a.Hq) return;
-  const int t = (int)(item / a.Hq), h = (int)(item % a.Hq), l = threadIdx.x & 15;
-  const bf16* d = a.dout + (long)t * a.lddo + h * HD + 8 * l;
-  float dv[8], ov[8];
-  unpack8(ldg128(d), dv);
-  if (FP32) {
-    const float* o = a.o32 + (long)t * a.ldo32 + h * HD + 8 * l;
-    const f32x4 o0 = *reinterpret_cast<const f32x4*>(o);
-    const f32x4 o1 = *reinterpret_cast<const f32x4*>(o + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ov[i] = o0[i];
-      ov[4 + i] = o1[i];
-    }
-  } else {
-    unpack8(ldg128(a.ctx + (long)t * a.ldc + h * HD + 8 * l), ov);
-  }
-  float v = dv[0] * ov[0] + dv[1] * ov[1] + dv[2] * ov[2] + dv[3] * ov[3] + dv[4] * ov[4] +
-            dv[5] * ov[5] + dv[6] * ov[6] + dv[7] * ov[7];
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
-  if (l == 0) a.dsum[(long)h * a.ld_stat + t] = v;
-}
-
 // ---------------------------------------------------------------- dQ
 // Block: 4 waves × 32 queries (q_block layout) of one kv head's q-heads;
 // streams the kv head's K/V tiles. dQ = scale · dS·K.
@@ -308,7 +276,35 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   load_row_frags(a.q, a.ldq, st + qpos, h * HD, qok, lh, qf);
   load_row_frags(a.dout, a.lddo, st + qpos, h * HD, qok, lh, df_);
   const float lse2 = qok ? a.lse[(long)h * a.ld_stat + st + qpos] : 0.f;
-  const float dsum = qok ? a.dsum[(long)h * a.ld_stat + st + qpos] : 0.f;
+  // dsum = rowsum(dO∘O) of the wave's rows: the lane's 64 dims of dO (df_)
+  // against the same dims of O (fp32 copy when the forward wrote one, else the
+  // bf16 ctx), the two halves of a row joined across lanes l and l^32; the dK/dV
+  // pass that runs next reads it from a.dsum.
+  float dsum = 0.f;
+  {
+    const long orow = (long)(st + (qok ? qpos : 0));
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int d0 = h * HD + kk * 16 + lh * 8;
+      float ov[8];
+      if (a.o32) {
+        const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.o32 + orow * a.ldo32 + d0);
+        const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.o32 + orow * a.ldo32 + d0 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ov[e] = o0[e];
+          ov[4 + e] = o1[e];
+        }
+      } else {
+        unpack8(ldg128(a.ctx + orow * a.ldc + d0), ov);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum += (float)df_[kk][e] * ov[e];
+    }
+    dsum += __shfl_xor(dsum, 32, 64);
+    if (!qok) dsum = 0.f;
+    if (qok && lh == 0) a.dsum[(long)h * a.ld_stat + st + qpos] = dsum;
+  }
 
   f32x16 dq[4];
 #pragma unroll
@@ -603,17 +599,6 @@ hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t attn_bwd_prep(const AttnArgs& a, hipStream_t s) {
-  if (a.n <= 0) return hipSuccess;
-  const long items = (long)a.n * a.Hq;
-  const dim3 grid((unsigned)((items + 15) / 16));
-  if (a.o32)
-    hipLaunchKernelGGL(attn_dsum_kernel<true>, grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(attn_dsum_kernel<false>, grid, dim3(256), 0, s, a);
-  return hipGetLastError();
-}
-
 hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
   if (a.max_tiles <= 0) return hipSuccess;
   hipLaunchKernelGGL(attn_dkdv_kernel, dim3(a.max_tiles, a.Hkv), dim3(256), 0, s, a);
@@ -627,11 +612,11 @@ hipError_t attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// dQ first: it computes dsum, which the dK/dV pass reads.
 hipError_t attn_bwd(const AttnArgs& a, hipStream_t s) {
   hipError_t e;
-  if ((e = attn_bwd_prep(a, s)) != hipSuccess) return e;
-  if ((e = attn_bwd_dkdv(a, s)) != hipSuccess) return e;
-  return attn_bwd_dq(a, s);
+  if ((e = attn_bwd_dq(a, s)) != hipSuccess) return e;
+  return attn_bwd_dkdv(a, s);
 }
 
 }  // namespace dsb

@@ -1014,17 +1014,13 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       if (dual_o) CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      // per token: dO (bf16) and O (fp32) rows read, Hq fp32 sums written
-      KScope ks(h, st, "attn_dsum", 0, 0, 0, 6.0 * q + 4.0 * Hq, 0, 0);
-      LK(attn_bwd_prep(at, st));
+      // dQ first: it also forms dsum = rowsum(dO∘O) (reads the fp32 O rows)
+      KScope ks(h, st, "attn_dq", 0, au, 0, arow + 2.0 * q + 2.0 * q + 4.0 * q + 4.0 * Hq, 0, 0);
+      LK(attn_bwd_dq(at, st));
     }
     {
       KScope ks(h, st, "attn_dkdv", 0, 4.0 * au, 0, arow + 2.0 * q + 4.0 * kv, 0, 0);
       LK(attn_bwd_dkdv(at, st));
-    }
-    {
-      KScope ks(h, st, "attn_dq", 0, au, 0, arow + 2.0 * q + 2.0 * q, 0, 0);
-      LK(attn_bwd_dq(at, st));
     }
     {
       KScope ks(h, st, "rope_bwd", 0, 0, 0, 4.0 * (q + kv) + 512.0, 0, 0);

@@ -42,7 +42,7 @@ struct AttnArgs {
                              // and dsum takes O from the bf16 ctx
   long ldo32;
   float* lse;                // [Hq, ld_stat] log2-domain row log-sum-exp
-  float* dsum;               // [Hq, ld_stat] rowsum(dO ∘ O)
+  float* dsum;               // [Hq, ld_stat] rowsum(dO ∘ O), written by the dQ pass
   long ld_stat;
   const bf16* dout; long lddo;  // bwd in: grad of ctx
   bf16* dq; long lddq;       // bwd out
@@ -53,12 +53,11 @@ struct AttnArgs {
   const int* ntiles_dev;
   int max_tiles;
   int Hq, Hkv;
-  const int* n_dev;  // live token count (for the dsum prep)
+  const int* n_dev;  // live token count (unused by the attention kernels)
   int n;
 };
 hipError_t attn_fwd(const AttnArgs& a, hipStream_t s);
 hipError_t attn_bwd(const AttnArgs& a, hipStream_t s);
-hipError_t attn_bwd_prep(const AttnArgs& a, hipStream_t s);
 hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s);
 hipError_t attn_bwd_dq(const AttnArgs& a, hipStream_t s);
 
