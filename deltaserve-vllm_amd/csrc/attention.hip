@@ -105,6 +105,17 @@ DSB_DEV QBlock q_block(const AttnArgs& a, int w) {
   return r;
 }
 
+// acc += mfma(a, b) with the accumulator held in AGPRs (inline asm): the
+// dK/dV pass keeps its 128 long-lived accumulators there, while this
+// translation unit is compiled with MFMA results in VGPRs
+// (-amdgpu-mfma-vgpr-form), so the S/dP scores the softmax reads need no
+// AGPR-to-VGPR copies. The leading s_nop gives the VALU writes of a and b
+// (the bf16 packs of P and dS) their wait states before the MFMA reads them;
+// accumulations into one register tuple are at least 8 MFMAs apart.
+DSB_DEV void mfma32_acc(f32x16& acc, bf16x8 a, bf16x8 b) {
+  asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
 DSB_DEV bf16x8 pack_chunk(const f32x16& s, int c) {
   bf16x8 b;
 #pragma unroll
@@ -481,8 +492,15 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     // tile's queries gets an all-masked tile (zero contributions). Skipping it
     // would not shorten the block, whose waves meet at the next barrier, and
     // a skip path makes the compiler copy the accumulators each iteration.
-    // The two 32-query halves run one after the other through S, dP, the
-    // softmax terms and the dV/dK products, so only one half's scores are live.
+    //
+    // The tile's two 32-query halves run as a software pipeline of four MFMA
+    // phases, so the softmax arithmetic of one half (VALU) issues between the
+    // MFMAs of the next phase instead of idling the matrix pipe:
+    //   A: S/dP of half 0
+    //   B: S/dP of half 1   + P, dS of half 0 (one element per MFMA)
+    //   C: dV/dK of half 0  + P, dS of half 1
+    //   D: dV/dK of half 1
+    // sched_barrier pins each (MFMA + companions) group in place.
     {
       const char* cQ = reinterpret_cast<const char*>(sQ);
       const char* cO = reinterpret_cast<const char*>(sO);
@@ -495,76 +513,129 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
       const int base = q0 + 4 * lh;
       const int lo = key - base;
       const int hi = kok ? L - base : lo;
-#pragma unroll
-      for (int qf = 0; qf < 2; ++qf) {
-        // lane: key row; r: queries qf·32 + 8(r/4) + 4·lh + r%4
-        // S = Q·Kᵀ and dP = dO·Vᵀ over the 8 dim chunks. The fragment reads
-        // run two chunks ahead of the MFMAs (sched_barrier pins the order), so
-        // the LDS latency hides under the MFMAs instead of stalling each pair.
-        f32x16 s = {}, dp = {};
-        {
-          bf16x8 qfr[8], ofr[8];
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            qfr[kk] = row_frag(cQ, fo, qf * 32, kk);
-            ofr[kk] = row_frag(cO, fo, qf * 32, kk);
-          }
-#pragma unroll
-          for (int kk = 0; kk < 8; ++kk) {
-            __builtin_amdgcn_sched_barrier(0);
-            if (kk + 2 < 8) {
-              qfr[kk + 2] = row_frag(cQ, fo, qf * 32, kk + 2);
-              ofr[kk + 2] = row_frag(cO, fo, qf * 32, kk + 2);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            s = mfma32(qfr[kk], kf_[kk], s);
-            dp = mfma32(ofr[kk], vf_[kk], dp);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        if (masked) {
-          keep_branch();
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int off = qf * 32 + 8 * (r >> 2) + (r & 3);
-            if (off < lo || off >= hi) s[r] = -INFINITY;
-          }
-        }
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
+      {
+        // lane: key row; element r of half qf: query qf·32 + 8(r/4) + 4·lh + r%4
+        f32x16 s0 = {}, d0 = {}, s1 = {}, d1 = {};
+        // lse (log2) and dsum of the lane's queries, one group of 4 elements
+        // ahead of its use
+        f32x4 l4[2], g4[2];
+        auto stats = [&](int qf, int r4, int slot) {
           const int qi = qf * 32 + 8 * r4 + 4 * lh;
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&sLD[sidx][0][qi]);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sLD[sidx][1][qi]);
+          l4[slot] = *reinterpret_cast<const f32x4*>(&sLD[sidx][0][qi]);
+          g4[slot] = *reinterpret_cast<const f32x4*>(&sLD[sidx][1][qi]);
+        };
+        float pv[8], ds[8];          // P and dS of the 16-query chunk in flight
+        bf16x8 pb[2][2], sb[2][2];   // [half][16-query chunk] MFMA operands
+        // P and dS of element r of half qf from its scores sc and dP values dd;
+        // after the chunk's eighth element, its bf16 operands
+        auto soft = [&](const f32x16& sc, const f32x16& dd, int qf, int r) {
+          if ((r & 3) == 0 && (r >> 2) + 1 < 4) stats(qf, (r >> 2) + 1, ((r >> 2) + 1) & 1);
+          else if ((r & 3) == 0 && qf == 0) stats(1, 0, 0);
+          const float x = sc[r];
+          const int sl = (r >> 2) & 1, e = r & 3;
+          const float pp = fast_exp2(x * sl2 - l4[sl][e]);
+          pv[r & 7] = pp;
+          ds[r & 7] = pp * (dd[r] - g4[sl][e]);
+          if ((r & 7) == 7) {
+            bf16x8 a, b;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float p = fast_exp2(s[4 * r4 + e] * sl2 - l4[e]);
-            s[4 * r4 + e] = p;
-            dp[4 * r4 + e] = p * (dp[4 * r4 + e] - d4[e]);
-          }
-        }
-        // dV += Pᵀ·dO and dK += dSᵀ·Q over the two 16-query chunks of the
-        // half; the transposed reads of a dim block go one block ahead.
-        {
-          const bf16x8 pb[2] = {pack_chunk(s, 0), pack_chunk(s, 1)};
-          const bf16x8 sb[2] = {pack_chunk(dp, 0), pack_chunk(dp, 1)};
-          bf16x8 ot[8], qt[8];  // [chunk·4 + d4]
-          ot[0] = tr_frag(cO, fo, (2 * qf) * 16, 0);
-          qt[0] = tr_frag(cQ, fo, (2 * qf) * 16, 0);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int c = i >> 2, d4 = i & 3;
-            __builtin_amdgcn_sched_barrier(0);
-            if (i + 1 < 8) {
-              const int c1 = (i + 1) >> 2, e1 = (i + 1) & 3;
-              ot[i + 1] = tr_frag(cO, fo, (2 * qf + c1) * 16, e1);
-              qt[i + 1] = tr_frag(cQ, fo, (2 * qf + c1) * 16, e1);
+            for (int k = 0; k < 8; ++k) {
+              a[k] = (bf16)pv[k];
+              b[k] = (bf16)ds[k];
             }
-            __builtin_amdgcn_sched_barrier(0);
-            dv[d4] = mfma32(ot[i], pb[c], dv[d4]);
-            dk[d4] = mfma32(qt[i], sb[c], dk[d4]);
+            pb[qf][r >> 3] = a;
+            sb[qf][r >> 3] = b;
           }
+        };
+        bf16x8 qf_[8], of_[8];
+        // Phase A: S/dP of half 0, fragment reads two chunks ahead; the last
+        // two steps read the first chunks of half 1
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          qf_[kk] = row_frag(cQ, fo, 0, kk);
+          of_[kk] = row_frag(cO, fo, 0, kk);
+        }
+        stats(0, 0, 0);
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          __builtin_amdgcn_sched_barrier(0);
+          const int nk = (kk + 2) & 7, nr = kk + 2 < 8 ? 0 : 32;
+          qf_[nk] = row_frag(cQ, fo, nr, nk);
+          of_[nk] = row_frag(cO, fo, nr, nk);
+          __builtin_amdgcn_sched_barrier(0);
+          s0 = mfma32(qf_[kk], kf_[kk], s0);
+          d0 = mfma32(of_[kk], vf_[kk], d0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        auto mask = [&](f32x16& sc, int qf) {
+          if (masked) {
+            keep_branch();
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int off = qf * 32 + 8 * (r >> 2) + (r & 3);
+              if (off < lo || off >= hi) sc[r] = -INFINITY;
+            }
+          }
+        };
+        mask(s0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // Phase B: S/dP of half 1; P, dS of half 0 one element after each MFMA
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (kk + 2 < 8) {
+            qf_[kk + 2] = row_frag(cQ, fo, 32, kk + 2);
+            of_[kk + 2] = row_frag(cO, fo, 32, kk + 2);
+          }
+          s1 = mfma32(qf_[kk], kf_[kk], s1);
+          soft(s0, d0, 0, 2 * kk);
+          __builtin_amdgcn_sched_barrier(0);
+          d1 = mfma32(of_[kk], vf_[kk], d1);
+          soft(s0, d0, 0, 2 * kk + 1);
           __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        mask(s1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        // Phase C: dV += Pᵀ·dO and dK += dSᵀ·Q of half 0 over its two 16-query
+        // chunks (transposed reads one block ahead); P, dS of half 1 between
+        bf16x8 ot[2], qt[2];
+        ot[0] = tr_frag(cO, fo, 0, 0);
+        qt[0] = tr_frag(cQ, fo, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int c = i >> 2, d4 = i & 3;
+          __builtin_amdgcn_sched_barrier(0);
+          if (i + 1 < 8) {
+            const int c1 = (i + 1) >> 2, e1 = (i + 1) & 3;
+            ot[(i + 1) & 1] = tr_frag(cO, fo, c1 * 16, e1);
+            qt[(i + 1) & 1] = tr_frag(cQ, fo, c1 * 16, e1);
+          } else {
+            ot[0] = tr_frag(cO, fo, 32, 0);
+            qt[0] = tr_frag(cQ, fo, 32, 0);
+          }
+          mfma32_acc(dv[d4], ot[i & 1], pb[0][c]);
+          soft(s1, d1, 1, 2 * i);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma32_acc(dk[d4], qt[i & 1], sb[0][c]);
+          soft(s1, d1, 1, 2 * i + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // Phase D: dV/dK of half 1
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int c = i >> 2, d4 = i & 3;
+          __builtin_amdgcn_sched_barrier(0);
+          if (i + 1 < 8) {
+            const int c1 = (i + 1) >> 2, e1 = (i + 1) & 3;
+            ot[(i + 1) & 1] = tr_frag(cO, fo, 32 + c1 * 16, e1);
+            qt[(i + 1) & 1] = tr_frag(cQ, fo, 32 + c1 * 16, e1);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          mfma32_acc(dv[d4], ot[i & 1], pb[1][c]);
+          mfma32_acc(dk[d4], qt[i & 1], sb[1][c]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (it + 1 < nit && tid < TR) {
@@ -573,6 +644,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     }
   }
 
+  // the last accumulating MFMAs (inline asm, unseen by the compiler's hazard
+  // checks) complete before their AGPRs are read
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   if (kok) {
     const long row = st + key;
 #pragma unroll
