@@ -10,9 +10,10 @@
 // Semantics: deltaserve-plugin/deltaserve/bwd_services/common/attention.py
 //   attn_forward_core   :20-45   (scale 1/sqrt(Hd), causal mask, fp32 softmax)
 //   attn_backward_core  :48-112  (dS = P∘(dP − rowsum(dP∘P)), GQA group sums)
-// rowsum(dP∘P) is computed as rowsum(dO∘O), with the fp32 O copy of the
-// forward when the caller passes one (the backward cycle does), else with the
-// bf16 ctx.
+// rowsum(dP∘P) is computed as rowsum(dO∘O) with O from the forward: in the
+// backward cycle as ctx + bf16(O − ctx), the bf16 rounding residual the
+// forward writes next to ctx (about 16 significant bits, half the bytes of an
+// fp32 copy); at op level as the fp32 copy the caller passes, else the bf16 ctx.
 // The reference fills masked scores with −1e9 before the softmax; exp of that
 // underflows to exactly 0, so skipping masked pairs is the same arithmetic.
 //
@@ -265,6 +266,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
         }
         *reinterpret_cast<bf16x4*>(a.ctx + row * a.ldc + h * HD + dim) = ob;
         if (a.o32) *reinterpret_cast<f32x4*>(a.o32 + row * a.ldo32 + h * HD + dim) = of;
+        if (a.ores) {
+          bf16x4 rb;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) rb[t] = (bf16)(of[t] - (float)ob[t]);
+          *reinterpret_cast<bf16x4*>(a.ores + row * a.ldc + h * HD + dim) = rb;
+        }
       }
     if (lh == 0) a.lse[(long)h * a.ld_stat + row] = m_i + log2f(l_i);
   }
@@ -288,9 +295,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   load_row_frags(a.dout, a.lddo, st + qpos, h * HD, qok, lh, df_);
   const float lse2 = qok ? a.lse[(long)h * a.ld_stat + st + qpos] : 0.f;
   // dsum = rowsum(dO∘O) of the wave's rows: the lane's 64 dims of dO (df_)
-  // against the same dims of O (fp32 copy when the forward wrote one, else the
-  // bf16 ctx), the two halves of a row joined across lanes l and l^32; the dK/dV
-  // pass that runs next reads it from a.dsum.
+  // against the same dims of O (ctx + its rounding residual, or the fp32 copy,
+  // when the forward wrote one, else the bf16 ctx), the two halves of a row
+  // joined across lanes l and l^32; the dK/dV pass that runs next reads it
+  // from a.dsum.
   float dsum = 0.f;
   {
     const long orow = (long)(st + (qok ? qpos : 0));
@@ -298,7 +306,13 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
     for (int kk = 0; kk < 8; ++kk) {
       const int d0 = h * HD + kk * 16 + lh * 8;
       float ov[8];
-      if (a.o32) {
+      if (a.ores) {
+        float rv[8];
+        unpack8(ldg128(a.ctx + orow * a.ldc + d0), ov);
+        unpack8(ldg128(a.ores + orow * a.ldc + d0), rv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ov[e] += rv[e];
+      } else if (a.o32) {
         const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.o32 + orow * a.ldo32 + d0);
         const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.o32 + orow * a.ldo32 + d0 + 4);
 #pragma unroll

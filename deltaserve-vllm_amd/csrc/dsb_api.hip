@@ -269,7 +269,7 @@ struct dsb_handle {
   // post-attention residual's): rounding it to bf16 at every layer would
   // compound over the layers
   float *g32[2], *grm32;
-  float* o32;  // fp32 attention output: rowsum(dO∘O) of the backward from unrounded O
+  bf16* ores;  // bf16 rounding residual of the attention output: rowsum(dO∘O) from ctx + ores
   bf16 *normed, *dlog;
   float2* stats;
   float *tgt_logit, *lse_h, *loss_row, *dH;
@@ -432,7 +432,7 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->g32[0], NN * D));
   CKR(dalloc(h, &h->g32[1], NN * D));
   CKR(dalloc(h, &h->grm32, NN * D));
-  CKR(dalloc(h, &h->o32, NN * q));
+  CKR(dalloc(h, &h->ores, NN * q));
   CKR(dalloc(h, &h->normed, NN * D));
   CKR(dalloc(h, &h->stats, NN * h->ntn));
   CKR(dalloc(h, &h->tgt_logit, NN));
@@ -841,7 +841,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     at.q = h->qk; at.ldq = q + kv;
     at.k = h->qk + q; at.ldk = q + kv;
     at.v = h->qkv_pre + q + kv; at.ldv = W3;
-    at.ctx = h->ctx; at.ldc = q; at.o32 = h->o32; at.ldo32 = q;
+    at.ctx = h->ctx; at.ldc = q; at.ores = h->ores;
     at.lse = h->lse; at.dsum = h->dsum; at.ld_stat = N + 1;
     at.dout = h->gctx; at.lddo = q;
     at.dq = h->gqkv; at.lddq = W3;
@@ -887,7 +887,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
                   h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     {
-      KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 6.0 * q + 4.0 * Hq, 0, 0);
+      KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 4.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_fwd(at, st));
     }
     if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Zo_b, r, st));
@@ -1014,7 +1014,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       if (dual_o) CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      // dQ first: it also forms dsum = rowsum(dO∘O) (reads the fp32 O rows)
+      // dQ first: it also forms dsum = rowsum(dO∘O) (reads ctx and its residual)
       KScope ks(h, st, "attn_dq", 0, au, 0, arow + 2.0 * q + 2.0 * q + 4.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_bwd_dq(at, st));
     }

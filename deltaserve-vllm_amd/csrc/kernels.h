@@ -38,9 +38,11 @@ struct AttnArgs {
   const bf16* k; long ldk;   // [n, Hkv*128] (post-RoPE)
   const bf16* v; long ldv;   // [n, Hkv*128]
   bf16* ctx; long ldc;       // fwd out [n, Hq*128]
-  float* o32;                // fwd out fp32 copy of ctx, ld = ldo32; null: none,
-                             // and dsum takes O from the bf16 ctx
+  float* o32;                // fwd out fp32 copy of ctx, ld = ldo32; null: none
   long ldo32;
+  bf16* ores;                // fwd out bf16(O − bf16(O)), the rounding residual of
+                             // ctx (ld = ldc); dsum then takes O = ctx + ores.
+                             // With neither copy dsum takes O from the bf16 ctx.
   float* lse;                // [Hq, ld_stat] log2-domain row log-sum-exp
   float* dsum;               // [Hq, ld_stat] rowsum(dO ∘ O), written by the dQ pass
   long ld_stat;
