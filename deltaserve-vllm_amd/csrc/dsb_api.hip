@@ -276,6 +276,7 @@ struct dsb_handle {
   float* sink = nullptr;  // gradient outputs of unbound projections of a LoRA group
   float* tn_work;
   long tn_work_elems;
+  std::vector<TnArgs> tn_pending;  // TN passes of the current layer (see tn_flush)
   float *cosb, *sinb, *inv_freq;
   int* labels;
   // step staging
@@ -668,23 +669,63 @@ int skinny(dsb_handle* h, const bf16* X, long ldx, const bf16* B, int R, int K, 
   return 0;
 }
 
+// A TN pass (grad_A = grad_Zᵀ·X or grad_B = s·Gᵀ·Z) of the layer being
+// processed. Nothing in the layer reads these gradients (the optimizer does,
+// after the last layer) and their inputs stay valid until the next layer's
+// recompute, so the layer's passes are collected here and issued together
+// by tn_flush at the end of the layer: one partial launch and one reduction
+// for all of them instead of two launches each.
 int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, int C,
-       float* o0, float* o1, float* o2, int rg, int transpose, float scale, hipStream_t s) {
+       float* o0, float* o1, float* o2, int rg, int transpose, float scale, hipStream_t) {
   TnArgs a{};
   a.P = P; a.ldp = ldp; a.X = X; a.ldx = ldx; a.R = R; a.C = C;
-  a.n = h->N; a.n_dev = &h->d_hdr->n; a.work = h->tn_work;
-  // 128-column blocks × token splits: about one block per CU (measured best
-  // at C3 shapes; the grid runs in one round)
-  const int cb = (C + 127) / 128;
-  int ns = std::max(1, 256 / cb);
-  ns = std::min(ns, 32);
-  ns = std::min<long>(ns, h->tn_work_elems / ((long)R * C));
-  ns = std::min(ns, std::max(1, h->N / 64));
-  a.nsplit = std::max(ns, 1);
+  a.n = h->N; a.n_dev = &h->d_hdr->n;
   a.outs[0] = o0; a.outs[1] = o1; a.outs[2] = o2;
   a.rg = rg; a.transpose_out = transpose; a.scale = scale;
-  KScope ks(h, s, "lora_tn", 2.0 * R * C, 0, 0, 2.0 * C + 2.0 * R, 0, 4.0 * R * C);
-  LK(lora_tn(a, s));
+  h->tn_pending.push_back(a);
+  return 0;
+}
+
+int tn_flush(dsb_handle* h, hipStream_t s) {
+  std::vector<TnArgs>& pend = h->tn_pending;
+  for (size_t i0 = 0; i0 < pend.size(); i0 += kTnBatch) {
+    const int cnt = (int)std::min<size_t>(kTnBatch, pend.size() - i0);
+    TnArgs* a = pend.data() + i0;
+    long blocks = 0, cols = 0;
+    double fa = 0, ba = 0, bc = 0;
+    for (int i = 0; i < cnt; ++i) {
+      blocks += (long)((a[i].C + 127) / 128) * ((a[i].R + 63) / 64);
+      cols += (long)a[i].R * a[i].C;
+      fa += 2.0 * a[i].R * a[i].C;
+      ba += 2.0 * a[i].C + 2.0 * a[i].R;
+      bc += 4.0 * a[i].R * a[i].C;
+    }
+    // (column block, rank group) blocks × token splits: about one block per
+    // CU over the whole batch
+    int ns = (int)std::max<long>(1, 256 / std::max<long>(blocks, 1));
+    ns = std::min(ns, 32);
+    ns = std::min(ns, std::max(1, h->N / 64));
+    ns = (int)std::max<long>(1, std::min<long>(ns, h->tn_work_elems / std::max<long>(cols, 1)));
+    if ((long)ns * cols > h->tn_work_elems) {
+      pend.clear();
+      return fail(h, "tn: partial sums exceed the workspace");
+    }
+    float* w = h->tn_work;
+    for (int i = 0; i < cnt; ++i) {
+      a[i].nsplit = ns;
+      a[i].work = w;
+      w += (long)ns * a[i].R * a[i].C;
+    }
+    KScope ks(h, s, "lora_tn", fa, 0, 0, ba, 0, bc);
+    const hipError_t e = lora_tn_batch(a, cnt, s);
+    if (e != hipSuccess) {
+      pend.clear();
+      set_error("lora_tn_batch: %s", hipGetErrorString(e));
+      h->err = get_error();
+      return -1;
+    }
+  }
+  pend.clear();
   return 0;
 }
 
@@ -831,6 +872,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
   }
   if (seg < 2 * C + h->L) {
     const int lo = seg - 2 * C;  // layers done before this one in the cycle
+    h->tn_pending.clear();
     const int li = h->L - 1 - lo;
     // the incoming gradient alternates between the two g buffers layer by layer
     bf16* g = (lo & 1) ? h->g1 : h->g0;
@@ -1066,6 +1108,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       LK(rmsnorm_bwd(x, ldx, h->gxn1, false, D, (const bf16*)ls.w.in_ln, nullptr, D, gnext, D,
                      N, nd, D, eps, st, h->grm32, gnext32));
     }
+    CKR(tn_flush(h, st));
     return 0;
   }
   // ---- per-layer clip + AdamW (trainer.py:624-636, :668)

@@ -99,6 +99,16 @@ struct TnArgs {
   float scale;
 };
 hipError_t lora_tn(const TnArgs& a, hipStream_t s);
+// Up to kTnBatch TN passes (each its own P, X, R, C, outputs and work region;
+// one token-split count) in one launch plus one reduction launch.
+constexpr int kTnBatch = 12;
+struct TnBatch {
+  TnArgs a[kTnBatch];
+  int count;
+  int b0[kTnBatch + 1];
+  long r0[kTnBatch + 1];
+};
+hipError_t lora_tn_batch(const TnArgs* a, int count, hipStream_t s);
 // One pass over G [n, C] for the two rank-r products that read it
 // (ops.py:142 grad_Z = gy @ (s·B) and ops.py:144 grad_B = s · gy.t() @ Z):
 //   Y[t, j] = bf16(sum_c G[t, c]·W[j, c])          (W = (s·B)ᵀ [R2, C])

@@ -156,22 +156,32 @@ hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s) {
 // both are read transposed with ds_read_b64_tr_b16 (16×16×32 pattern: lane j
 // of group g points at row 8g + j/4 (+4), column c0 + 4(j%4)); wave w owns
 // columns 32w .. 32w+31 (2 column tiles) × RB rank tiles.
+// A launch covers up to kTnBatch passes (with one token-split count):
+// grid.x runs over the (column block, rank group) blocks of every pass,
+// b0[i] .. b0[i+1]-1 being those of pass i (rank group g = x / cb_i, column
+// block x % cb_i); the reduction covers the passes' R·C outputs in order.
 template <int RB>
-__global__ __launch_bounds__(256, 2) void lora_tn_partial_kernel(TnArgs a) {
+__global__ __launch_bounds__(256, 2) void lora_tn_partial_kernel(TnBatch b) {
   constexpr int XT = 32 * 128, PT = 32 * 16 * RB, SE = XT + PT;
   constexpr int NS = (40 * 1024) / SE < 8 ? (40 * 1024) / SE : 8;  // SE elements = 2·SE bytes
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kTnBatch; ++i)
+    if (i < b.count && (int)blockIdx.x >= b.b0[i]) pi = i;  // uniform
+  const TnArgs& a = b.a[pi];
+  const int bx = blockIdx.x - b.b0[pi], cbs = (a.C + 127) / 128;
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
   __shared__ __attribute__((aligned(16))) bf16 smem[NS * SE];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int c0 = blockIdx.x * 128, sp = blockIdx.y;
+  const int c0 = (bx % cbs) * 128, sp = blockIdx.y;
   int per = (N + a.nsplit - 1) / a.nsplit;
   per = (per + 31) & ~31;
   const int ta = min(N, sp * per), tb = min(N, ta + per);
   const int nk = (tb - ta + 31) / 32;
   const int cv = min(a.C - c0, 128);
-  // ranks j0 .. j0 + R - 1 of this block (groups of 64 on grid.z)
-  const int j0 = blockIdx.z * 64, R = min(a.R - j0, 64);
+  // ranks j0 .. j0 + R - 1 of this block (groups of 64)
+  const int j0 = (bx / cbs) * 64, R = min(a.R - j0, 64);
   const bf16* Pg = a.P + j0;
   // P chunk loads: 32 rows × R ranks = 4·RB loads of 1 KB; wave w issues the
   // ones with index ≡ w (mod 4), so waves 0 .. RB-1 issue one each per stage.
@@ -252,9 +262,15 @@ __global__ __launch_bounds__(256, 2) void lora_tn_partial_kernel(TnArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnArgs a) {
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (long)a.R * a.C) return;
+__global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnBatch b) {
+  long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= b.r0[b.count]) return;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kTnBatch; ++i)
+    if (i < b.count && idx >= b.r0[i]) pi = i;
+  const TnArgs& a = b.a[pi];
+  idx -= b.r0[pi];
   const int c = (int)(idx / a.R), j = (int)(idx % a.R);
   float s = 0.f;
 #pragma unroll 8
@@ -268,22 +284,45 @@ __global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnArgs a) {
     o[(long)jj * a.C + c] = s;
 }
 
-hipError_t lora_tn(const TnArgs& a, hipStream_t s) {
-  if (a.R <= 0 || a.C <= 0) return hipSuccess;
-  const dim3 grid((a.C + 127) / 128, a.nsplit, (a.R + 63) / 64);
-  switch ((std::min(a.R, 64) + 15) / 16) {
-    case 1: hipLaunchKernelGGL(lora_tn_partial_kernel<1>, grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(lora_tn_partial_kernel<2>, grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(lora_tn_partial_kernel<3>, grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(lora_tn_partial_kernel<4>, grid, dim3(256), 0, s, a); break;
+hipError_t lora_tn_batch(const TnArgs* a, int count, hipStream_t s) {
+  if (count < 1 || count > kTnBatch) return hipErrorInvalidValue;
+  TnBatch b{};
+  b.b0[0] = 0;
+  b.r0[0] = 0;
+  int rb = 1, n = 0;
+  for (int i = 0; i < count; ++i) {
+    const TnArgs& x = a[i];
+    if (x.R <= 0 || x.C <= 0 || x.nsplit != a[0].nsplit) return hipErrorInvalidValue;
+    b.a[n] = x;
+    b.b0[n + 1] = b.b0[n] + ((x.C + 127) / 128) * ((x.R + 63) / 64);
+    b.r0[n + 1] = b.r0[n] + (long)x.R * x.C;
+    rb = std::max(rb, (std::min(x.R, 64) + 15) / 16);
+    ++n;
+  }
+  b.count = n;
+  for (int i = n; i < kTnBatch; ++i) {
+    b.b0[i + 1] = b.b0[n];
+    b.r0[i + 1] = b.r0[n];
+  }
+  const dim3 grid(b.b0[n], a[0].nsplit);
+  switch (rb) {
+    case 1: hipLaunchKernelGGL(lora_tn_partial_kernel<1>, grid, dim3(256), 0, s, b); break;
+    case 2: hipLaunchKernelGGL(lora_tn_partial_kernel<2>, grid, dim3(256), 0, s, b); break;
+    case 3: hipLaunchKernelGGL(lora_tn_partial_kernel<3>, grid, dim3(256), 0, s, b); break;
+    case 4: hipLaunchKernelGGL(lora_tn_partial_kernel<4>, grid, dim3(256), 0, s, b); break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const long tot = (long)a.R * a.C;
+  const long tot = b.r0[n];
   hipLaunchKernelGGL(lora_tn_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
-                     s, a);
+                     s, b);
   return hipGetLastError();
+}
+
+hipError_t lora_tn(const TnArgs& a, hipStream_t s) {
+  if (a.R <= 0 || a.C <= 0) return hipSuccess;
+  return lora_tn_batch(&a, 1, s);
 }
 
 // ------------------------------------------------------------------ dual
