@@ -141,6 +141,55 @@ DSB_DEV void for_each_row8(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, i
   }
 }
 
+// for_each_row8 for epilogues that also read global memory per output chunk
+// (a residual, or the fp32 output they accumulate into): `load(m, n)` issues
+// that read for the chunk (row m, columns n .. n+7) and `f(m, n, v, x)` gets
+// its result x. The reads of the next 32-row block are issued before the
+// current block is staged and stored, two blocks in registers, so their
+// latency is spent under the epilogue's other work instead of stalling every
+// row (reading them in `f` left one global-load latency per 4 rows).
+template <int FM, int FN, class L, class F>
+DSB_DEV void for_each_row8_pf(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
+                              int wave, void* smem, L&& load, F&& f) {
+  constexpr int TN = FN * 32, PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG, IT = 32 / RPI;
+  static_assert(64 % CG == 0, "row groups");
+  using T = decltype(load(0, 0));
+  float* buf = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int rsub = lane / CG, cg = lane % CG;
+  T pf[2][IT];
+  auto issue = [&](int fm, T (&dst)[IT]) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int m = mw + fm * 32 + it * RPI + rsub;
+      dst[it] = m < M ? load(m, nw + cg * 8) : T{};
+    }
+  };
+  if (mw < M) issue(0, pf[0]);
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    if (mw + fm * 32 >= M) break;  // uniform: the rest of the wave tile is past M
+    if (fm + 1 < FM && mw + (fm + 1) * 32 < M) issue(fm + 1, pf[(fm + 1) & 1]);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                         acc[fm][fn][4 * g + 3]};
+        *reinterpret_cast<f32x4*>(buf + lr * PITCH + fn * 32 + 8 * g + 4 * lh) = v;
+      }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int row = it * RPI + rsub;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
+      float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      const int m = mw + fm * 32 + row;
+      if (m < M) f(m, nw + cg * 8, v, pf[fm & 1][it]);
+    }
+  }
+}
+
 // 8 values to bf16 at p[0 .. min(8, lim)); 16-byte store when whole and aligned.
 // The 16-byte store is non-temporal: the outputs of a whole wave of tiles land
 // at once, and streaming them keeps them from evicting the A/B panels the
@@ -432,12 +481,34 @@ struct EpiBF16 {
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
-    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
-      const int lim = N - n;
-      if (lim <= 0) return;
-      if (R) add8_bf16(v, R + (long)m * ldr + n, lim);
-      store8_bf16(C + (long)m * ldc + n, v, lim);
-    });
+    if (!R) {
+      for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+        const int lim = N - n;
+        if (lim <= 0) return;
+        store8_bf16(C + (long)m * ldc + n, v, lim);
+      });
+      return;
+    }
+    // residual rows read ahead (whole aligned chunks; others read in place)
+    auto whole = [&](int m, int n) {
+      return N - n >= 8 && (((unsigned long)(R + (long)m * ldr + n)) & 15) == 0;
+    };
+    for_each_row8_pf(
+        acc, mw, nw, M, lane, wave, smem,
+        [&](int m, int n) { return whole(m, n) ? ldg128(R + (long)m * ldr + n) : u32x4{}; },
+        [&](int m, int n, float* v, const u32x4& r) {
+          const int lim = N - n;
+          if (lim <= 0) return;
+          if (whole(m, n)) {
+            float rf[8];
+            unpack8(r, rf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] += rf[i];
+          } else {
+            add8_bf16(v, R + (long)m * ldr + n, lim);
+          }
+          store8_bf16(C + (long)m * ldc + n, v, lim);
+        });
   }
 };
 
@@ -511,22 +582,45 @@ struct EpiF32 {
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
-    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
-      const int lim = N - n;
-      if (lim <= 0) return;
-      float* c = C + (long)m * ldc + n;
-      if (lim >= 8 && ((unsigned long)c & 15) == 0) {
-        f32x4 o0 = {v[0], v[1], v[2], v[3]}, o1 = {v[4], v[5], v[6], v[7]};
-        if (accumulate) {
-          o0 += *reinterpret_cast<const f32x4*>(c);
-          o1 += *reinterpret_cast<const f32x4*>(c + 4);
+    auto whole = [&](int m, int n) {
+      return N - n >= 8 && (((unsigned long)(C + (long)m * ldc + n)) & 15) == 0;
+    };
+    if (!accumulate) {
+      for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
+        const int lim = N - n;
+        if (lim <= 0) return;
+        float* c = C + (long)m * ldc + n;
+        if (whole(m, n)) {
+          *reinterpret_cast<f32x4*>(c) = f32x4{v[0], v[1], v[2], v[3]};
+          *reinterpret_cast<f32x4*>(c + 4) = f32x4{v[4], v[5], v[6], v[7]};
+        } else {
+          for (int i = 0; i < 8 && i < lim; ++i) c[i] = v[i];
         }
-        *reinterpret_cast<f32x4*>(c) = o0;
-        *reinterpret_cast<f32x4*>(c + 4) = o1;
-      } else {
-        for (int i = 0; i < 8 && i < lim; ++i) c[i] = accumulate ? c[i] + v[i] : v[i];
-      }
-    });
+      });
+      return;
+    }
+    // the fp32 values accumulated into, read ahead as for a residual
+    struct F8 {
+      f32x4 a, b;
+    };
+    for_each_row8_pf(
+        acc, mw, nw, M, lane, wave, smem,
+        [&](int m, int n) {
+          if (!whole(m, n)) return F8{};
+          const float* c = C + (long)m * ldc + n;
+          return F8{*reinterpret_cast<const f32x4*>(c), *reinterpret_cast<const f32x4*>(c + 4)};
+        },
+        [&](int m, int n, float* v, const F8& x) {
+          const int lim = N - n;
+          if (lim <= 0) return;
+          float* c = C + (long)m * ldc + n;
+          if (whole(m, n)) {
+            *reinterpret_cast<f32x4*>(c) = f32x4{v[0], v[1], v[2], v[3]} + x.a;
+            *reinterpret_cast<f32x4*>(c + 4) = f32x4{v[4], v[5], v[6], v[7]} + x.b;
+          } else {
+            for (int i = 0; i < 8 && i < lim; ++i) c[i] = c[i] + v[i];
+          }
+        });
   }
 };
 
