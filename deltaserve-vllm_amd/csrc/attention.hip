@@ -72,6 +72,13 @@ DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool 
 // flattened into selects that every tile would pay for (the masks below).
 DSB_DEV void keep_branch() { asm volatile(""); }
 
+// An empty volatile asm that takes x as an operand: x is computed before it,
+// and volatile asm statements keep their order, so a value pinned between two
+// inline-asm MFMAs is computed there. Without it the compiler sinks softmax
+// arithmetic whose results are only used later past the following branch,
+// out of the MFMA phase it was interleaved with.
+DSB_DEV void pin(float& x) { asm volatile("" : "+v"(x)); }
+
 // Query-side block layout (forward and dQ passes). A 128-row tile of the
 // table holds 4 subtiles of 32 queries; with G = Hq / Hkv q-heads per kv
 // head its 4·G (subtile, head) pairs are taken subtile-major, heaviest
@@ -550,6 +557,8 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
           const float pp = fast_exp2(x * sl2 - l4[sl][e]);
           pv[r & 7] = pp;
           ds[r & 7] = pp * (dd[r] - g4[sl][e]);
+          pin(pv[r & 7]);
+          pin(ds[r & 7]);
           if ((r & 7) == 7) {
             bf16x8 a, b;
 #pragma unroll
