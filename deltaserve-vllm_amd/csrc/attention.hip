@@ -124,6 +124,42 @@ DSB_DEV void mfma32_acc(f32x16& acc, bf16x8 a, bf16x8 b) {
   asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
+// Store a wave's 32 rows × 128 columns, held in the 32×32 accumulator layout
+// (lane l: row l%32, columns 32·d4 + 8·(e/4) + 4·(l/32) + e%4 of acc[d4][e]),
+// as bf16(scale·x) through the wave's LDS region `buf` (32 rows at a pitch of
+// kRowPitch elements): the lanes write their pieces there, then read back 16
+// contiguous bytes each and store whole 256-byte rows, four rows per store
+// instruction (storing the 8-byte pieces directly scatters every instruction
+// over 32 rows). Rows r >= nvalid are not stored. With `res`, the bf16
+// rounding residual bf16(x − bf16(x)) goes to res (same row stride) after.
+constexpr int kRowPitch = 136;  // 272 bytes: rows 16 apart share LDS banks, at most 2-way
+DSB_DEV void store_rows32(const f32x16 (&acc)[4], float scale, bf16* buf, bf16* out, long ld,
+                          int nvalid, int lane, bf16* res = nullptr) {
+  const int lr = lane & 31, lh = lane >> 5;
+  for (int pass = 0; pass < (res ? 2 : 1); ++pass) {
+#pragma unroll
+    for (int d4 = 0; d4 < 4; ++d4)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float x = acc[d4][4 * g + t] * scale;
+          const bf16 b = (bf16)x;
+          v[t] = pass == 0 ? b : (bf16)(x - (float)b);
+        }
+        *reinterpret_cast<bf16x4*>(buf + lr * kRowPitch + d4 * 32 + 8 * g + 4 * lh) = v;
+      }
+    bf16* dst = pass == 0 ? out : res;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = lane + 64 * i, r = c >> 4, col = (c & 15) * 8;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(buf + r * kRowPitch + col);
+      if (r < nvalid) *reinterpret_cast<bf16x8*>(dst + (long)r * ld + col) = v;
+    }
+  }
+}
+
 DSB_DEV bf16x8 pack_chunk(const f32x16& s, int c) {
   bf16x8 b;
 #pragma unroll
@@ -256,6 +292,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   }
   for (int t = nt_w; t < nt; ++t) advance(t);
 
+  if (!a.o32) {
+    // ctx and its rounding residual as whole rows through the stages, which
+    // every wave is done reading
+    __syncthreads();
+    if (nt_w > 0) {
+      const long r0 = (long)(st + qb.q0) * a.ldc + h * HD;
+      store_rows32(o, 1.f / l_i, smem + w * 32 * kRowPitch, a.ctx + r0, a.ldc, L - qb.q0, lane,
+                   a.ores ? a.ores + r0 : nullptr);
+    }
+    if (qok && lh == 0) a.lse[(long)h * a.ld_stat + st + qpos] = m_i + log2f(l_i);
+    return;
+  }
   if (qok) {
     const float inv_l = 1.f / l_i;
     const long row = st + qpos;
@@ -423,19 +471,11 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   }
   for (int t = nt_w; t < nt; ++t) advance(t);
 
-  if (qok) {
-    const long row = st + qpos;
-#pragma unroll
-    for (int d4 = 0; d4 < 4; ++d4)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int dim = d4 * 32 + 8 * g + 4 * lh;
-        bf16x4 ob;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) ob[t] = (bf16)(dq[d4][4 * g + t] * kScale);
-        *reinterpret_cast<bf16x4*>(a.dq + row * a.lddq + h * HD + dim) = ob;
-      }
-  }
+  // every wave is past its last tile read: the stages take the staged rows
+  __syncthreads();
+  if (nt_w > 0)
+    store_rows32(dq, kScale, smem + w * 32 * kRowPitch, a.dq + (long)(st + qb.q0) * a.lddq + h * HD,
+                 a.lddq, L - qb.q0, lane);
 }
 
 // ---------------------------------------------------------------- dK / dV
@@ -670,22 +710,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   // the last accumulating MFMAs (inline asm, unseen by the compiler's hazard
   // checks) complete before their AGPRs are read
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-  if (kok) {
-    const long row = st + key;
-#pragma unroll
-    for (int d4 = 0; d4 < 4; ++d4)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int dim = d4 * 32 + 8 * g + 4 * lh;
-        bf16x4 kb, vb;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          kb[t] = (bf16)(dk[d4][4 * g + t] * kScale);
-          vb[t] = (bf16)dv[d4][4 * g + t];
-        }
-        *reinterpret_cast<bf16x4*>(a.dk + row * a.lddk + kvh * HD + dim) = kb;
-        *reinterpret_cast<bf16x4*>(a.dv + row * a.lddv + kvh * HD + dim) = vb;
-      }
+  // dK and dV as whole rows through the stages, which every wave is done
+  // reading
+  __syncthreads();
+  if (wk_first < L) {
+    bf16* buf = smem + w * 32 * kRowPitch;
+    const long row0 = st + wk_first;
+    store_rows32(dk, kScale, buf, a.dk + row0 * a.lddk + kvh * HD, a.lddk, L - wk_first, lane);
+    store_rows32(dv, 1.f, buf, a.dv + row0 * a.lddv + kvh * HD, a.lddv, L - wk_first, lane);
   }
 }
 
