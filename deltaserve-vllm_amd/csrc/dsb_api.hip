@@ -276,6 +276,8 @@ struct dsb_handle {
   float* sink = nullptr;  // gradient outputs of unbound projections of a LoRA group
   float* tn_work;
   long tn_work_elems;
+  float* part = nullptr;  // split-K partials of the products with too few 256×256 tiles
+  long part_elems = 0;
   std::vector<TnArgs> tn_pending;  // TN passes of the current layer (see tn_flush)
   float *cosb, *sinb, *inv_freq;
   int* labels;
@@ -444,6 +446,18 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->sink, (size_t)r * std::max(std::max(D, q), I)));
   h->tn_work_elems = 32L << 20;
   CKR(dalloc(h, &h->tn_work, h->tn_work_elems));
+  {
+    // split-K partials: the largest ks·M·N over the cycle's bf16/fp32 products
+    // (output width, reduction depth) that gemm_split_count splits
+    const int shapes[][2] = {{W3, D}, {D, q}, {I, D}, {D, 2 * I}, {q, D}, {D, W3}, {D, h->vchunk}};
+    long need = 0;
+    for (const auto& sh : shapes) {
+      const int ks = gemm_split_count(N, sh[0], sh[1]);
+      if (ks > 1) need = std::max(need, (long)ks * N * sh[0]);
+    }
+    h->part_elems = need;
+    if (need > 0) CKR(dalloc(h, &h->part, need));
+  }
   CKR(dalloc(h, &h->cosb, NN * 64));
   CKR(dalloc(h, &h->sinb, NN * 64));
   CKR(dalloc(h, &h->inv_freq, 64));
@@ -652,8 +666,20 @@ const char* cfg_name(int cfg) {
 template <class Epi>
 int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hipStream_t st,
          double ob, double xrow) {
-  const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(p.M, p.N);
   const double K = (double)p.K1 + p.K2;
+  if constexpr (std::is_same<Epi, EpiBF16>::value) {
+    // too few 256×256 tiles for the chip: split K (unless a tile is forced)
+    const int ksplit = h->gemm_cfg >= 0 ? 1 : gemm_split_count(p.M, p.N, p.K1 + p.K2);
+    if (ksplit > 1 && (long)ksplit * p.M * p.N <= h->part_elems) {
+      KScope ks(h, st, std::string("gemm256sk_") + epi, 2.0 * p.N * K, 0, 0,
+                2.0 * K + ob * p.N + xrow, 0, 2.0 * p.N * K);
+      GemmProblem q = p;
+      q.part = h->part;
+      LK(launch_gemm_split(q, e, ksplit, st));
+      return 0;
+    }
+  }
+  const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(p.M, p.N);
   KScope ks(h, st, std::string(cfg_name(cfg)) + "_" + epi, 2.0 * p.N * K, 0, 0,
             2.0 * K + ob * p.N + xrow, 0, 2.0 * p.N * K);
   LK(launch_gemm(p, e, st, cfg));
@@ -793,6 +819,7 @@ HeadArgs head_args(dsb_handle* h) {
   ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
   ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
   ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH; ha.gemm_cfg = h->gemm_cfg;
+  ha.part = h->part; ha.part_elems = h->part_elems;
   return ha;
 }
 
@@ -859,8 +886,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     {
       const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(N, D);
-      KScope ks(h, st, std::string(cfg_name(cfg)) + "_f32", 2.0 * Vc * D, 0, 0,
-                2.0 * Vc + 8.0 * D, 0, 2.0 * Vc * D);
+      const bool split = head_dh_split(ha, c0) > 1;
+      KScope ks(h, st, std::string(split ? "gemm256sk" : cfg_name(cfg)) + "_f32", 2.0 * Vc * D, 0,
+                0, 2.0 * Vc + 8.0 * D, 0, 2.0 * Vc * D);
       LK(head_chunk_dh(ha, c0, st));
     }
     if (c == C - 1) {
@@ -1734,6 +1762,20 @@ int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const vo
   hipStream_t s = (hipStream_t)stream;
   GemmProblem p{(const bf16*)A, lda, (const bf16*)B, ldb, (const bf16*)A2, lda2,
                 (const bf16*)B2, ldb2, M, N, K1, K2, nullptr};
+  // cfg -2: split K as the cycle does for problems with too few 256-wide
+  // tiles (partials in a buffer allocated for the call); by shape otherwise
+  const int ks = cfg == -2 ? gemm_split_count(M, N, K1 + K2) : 1;
+  if (cfg == -2) cfg = -1;
+  if (ks > 1) {
+    OPCK(hipMalloc((void**)&p.part, sizeof(float) * (size_t)ks * M * N));
+    hipError_t e1;
+    if (out_f32) e1 = launch_gemm_split(p, EpiF32{(float*)C, ldc, N, accumulate}, ks, s);
+    else e1 = launch_gemm_split(p, EpiBF16{(bf16*)C, ldc, N, (const bf16*)R, ldr}, ks, s);
+    const hipError_t e2 = e1 == hipSuccess ? hipStreamSynchronize(s) : e1;
+    (void)hipFree(p.part);
+    OPCK(e2);
+    return 0;
+  }
   if (out_f32) {
     EpiF32 e{(float*)C, ldc, N, accumulate};
     OPCK(launch_gemm(p, e, s, cfg));

@@ -39,6 +39,7 @@
 // contiguous run of tiles, grouped 4 deep along M for L2 reuse.
 #pragma once
 
+#include <algorithm>
 #include <type_traits>
 
 #include "dsb_common.h"
@@ -62,6 +63,11 @@ struct GemmProblem {
   // up features of the same f, so an epilogue sees both halves of a feature
   // (EpiGLU). N = 2·glu_half; glu_half a multiple of BN/2.
   int glu_half = 0;
+  // Split K (launch_gemm_split): block row z of the grid's y dimension
+  // computes K tiles [z·kc, (z+1)·kc) of the K1+K2 range and stores its fp32
+  // partial to part + z·M·N (row stride N) instead of running the epilogue;
+  // gemm_split_reduce then sums the partials in order and applies it.
+  float* part = nullptr;
 };
 
 DSB_DEV void tile_map(int bid, int nbm, int nbn, int& pm, int& pn) {
@@ -221,6 +227,16 @@ DSB_DEV void add8_bf16(float* v, const bf16* r, int lim) {
 // hit distinct banks for a fixed logical chunk.
 DSB_DEV int lds_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
+// The fp32 partial-sum epilogue of a split-K block (defined below), named
+// through a dependent type so the kernel template can use it before then.
+struct EpiF32;
+struct EpiBF16;
+template <class E>
+struct SplitPart {
+  using type = EpiF32;
+  static constexpr bool enabled = std::is_same<E, EpiBF16>::value || std::is_same<E, EpiF32>::value;
+};
+
 template <int BM, int BN, int WM, int WN, class Epi>
 __global__ __launch_bounds__(WM* WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel(GemmProblem p, Epi epi) {
@@ -251,6 +267,9 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   const int nk1 = (p.K1 + BK - 1) / BK;
   const int nk2 = p.K2 > 0 ? (p.K2 + BK - 1) / BK : 0;
   const int nk = nk1 + nk2;
+  // this block's K tiles (all of them unless K is split over the grid's y)
+  const int kc = (nk + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int kt0 = min(nk, (int)blockIdx.y * kc), kt1 = min(nk, kt0 + kc);
 
   // Loader geometry: lane fills slot (lane & 7) of row (lane >> 3) of its
   // 8-row block; block b = wave + j·NW starts at row 8b, whose bit 3 is the
@@ -424,19 +443,19 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   // one step and the first slice of the next.
   constexpr int H1 = IAB / 2;
   {
-    const Fill f = make_fill(0, 0);
+    const Fill f = make_fill(kt0, 0);
 #pragma unroll
     for (int j = 0; j < IAB; ++j) issue_one(f, j);
   }
   wait_vm<0>();
   lds_barrier();
   read(smem, 0, 0);
-  Fill fn = make_fill(1, 1);
+  Fill fn = make_fill(kt0 + 1, 1);
 #pragma unroll
   for (int j = 0; j < H1; ++j) issue_one(fn, j);
 
   auto step = [&](int kt, auto&& mk) {
-    const int cur = kt & 1;
+    const int cur = (kt - kt0) & 1;
     const bf16* b = smem + cur * SE;
     __builtin_amdgcn_sched_barrier(0);
     mma(0, b, 1, 1, fn, H1, IAB - H1);
@@ -456,17 +475,29 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   };
   // Steps whose prefetch (tile kt+2) stays in segment 1 use the invariant
   // segment-1 fill; the last few steps select the segment per tile.
-  const int nfast = max(0, min(nk, nk1 - 2));
-  int kt = 0;
+  // (tiles past this block's range that the last steps prefetch are other
+  // blocks' tiles or zero fills past K: loaded, never multiplied)
+  const int nfast = max(kt0, min(kt1, nk1 - 2));
+  int kt = kt0;
   for (; kt < nfast; ++kt) step(kt, make_fill1);
-  for (; kt < nk; ++kt) step(kt, make_fill);
-  // the last step's loads (zero fills past K) land before the epilogue
-  // reuses the LDS
+  for (; kt < kt1; ++kt) step(kt, make_fill);
+  // the last step's loads land before the epilogue reuses the LDS
   wait_vm<0>();
   lds_barrier();
 
-  epi.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
-                                   (void*)smem);
+  if constexpr (SplitPart<Epi>::enabled) {
+    if (p.part) {
+      const typename SplitPart<Epi>::type ep{p.part + (long)blockIdx.y * p.M * p.N, (long)p.N,
+                                             p.N, 0};
+      ep.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
+                                      (void*)smem);
+      return;
+    }
+  }
+  {
+    epi.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
+                                     (void*)smem);
+  }
 }
 
 // ---------------------------------------------------------------- epilogues
@@ -478,6 +509,13 @@ struct EpiBF16 {
   int N;
   const bf16* R;
   long ldr;
+  // the epilogue of one 8-column chunk (split-K reduction)
+  DSB_DEV void apply8(int m, int n, float* v) const {
+    const int lim = N - n;
+    if (lim <= 0) return;
+    if (R) add8_bf16(v, R + (long)m * ldr + n, lim);
+    store8_bf16(C + (long)m * ldc + n, v, lim);
+  }
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
@@ -579,6 +617,11 @@ struct EpiF32 {
   long ldc;
   int N;
   int accumulate;
+  DSB_DEV void apply8(int m, int n, const float* v) const {
+    const int lim = N - n;
+    float* c = C + (long)m * ldc + n;
+    for (int i = 0; i < 8 && i < lim; ++i) c[i] = accumulate ? c[i] + v[i] : v[i];
+  }
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
@@ -649,6 +692,32 @@ struct EpiLoraZ {
 // lane). Mid: 128×128, 4 waves of 64×64. Skinny: 64×64, 4 waves of 32×32.
 enum GemmCfg { GEMM_BIG = 0, GEMM_MID = 1, GEMM_SKINNY = 2 };
 
+// Sum of the split-K partials of p (in split order, so the result does not
+// depend on scheduling) through epi.apply8, 8 columns per thread, live rows
+// only. N must be a multiple of 8.
+template <class Epi>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmProblem p, int ks, Epi epi) {
+  int M = p.M;
+  if (p.M_dev) M = min(M, *p.M_dev);
+  const int n8 = p.N / 8;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const int m = (int)(idx / n8), n = (int)(idx % n8) * 8;
+  if (m >= M) return;
+  const long plane = (long)p.M * p.N;
+  const float* src = p.part + (long)m * p.N + n;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < ks; ++z) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src + z * plane);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + z * plane + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] += a[i];
+      v[4 + i] += b[i];
+    }
+  }
+  epi.apply8(m, n, v);
+}
+
 template <int BM, int BN, int WM, int WN, class Epi>
 hipError_t launch_gemm_cfg(const GemmProblem& p, const Epi& e, hipStream_t s) {
   const int nbm = (p.M + BM - 1) / BM, nbn = (p.N + BN - 1) / BN;
@@ -680,6 +749,33 @@ hipError_t launch_gemm(const GemmProblem& p, const Epi& e, hipStream_t s, int cf
       default: return launch_gemm_cfg<64, 64, 2, 2>(p, e, s);
     }
   }
+}
+
+// K split over the grid's y dimension for problems with too few 256×256
+// tiles to fill the chip: `ks` blocks per tile each store the fp32 partial
+// of a slice of K to p.part ([ks, M, N]), then one reduction launch sums them
+// and applies the epilogue. EpiBF16 and EpiF32 only; N a multiple of 8.
+inline int gemm_split_count(int M, int N, int K) {
+  const long tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
+  const int nk = (K + 63) / 64;
+  if (tiles >= 192 || N % 8 != 0 || nk < 8) return 1;
+  int ks = (int)((256 + tiles - 1) / tiles);
+  ks = std::min(ks, std::min(8, nk / 4));
+  return std::max(ks, 1);
+}
+template <class Epi>
+hipError_t launch_gemm_split(const GemmProblem& p, const Epi& e, int ks, hipStream_t s) {
+  static_assert(std::is_same<Epi, EpiBF16>::value || std::is_same<Epi, EpiF32>::value,
+                "split-K epilogues");
+  const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
+  if (nbm == 0 || nbn == 0) return hipSuccess;
+  if (!p.part || p.N % 8 != 0 || ks < 2) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(nbm * nbn, ks), dim3(256), 0, s,
+                     p, e);
+  const long n = (long)p.M * (p.N / 8);
+  hipLaunchKernelGGL(gemm_split_reduce_kernel<Epi>, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, s, p, ks, e);
+  return hipGetLastError();
 }
 
 }  // namespace dsb

@@ -218,11 +218,23 @@ hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s) {
   return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
 
+int head_dh_split(const HeadArgs& a, int c0) {
+  if (a.gemm_cfg >= 0 || !a.part) return 1;
+  const int Nc8 = (min(a.vchunk, a.V - c0) + 7) / 8 * 8;
+  const int ks = gemm_split_count(a.n, a.D, Nc8);
+  return ks > 1 && (long)ks * a.n * a.D <= a.part_elems ? ks : 1;
+}
+
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
   const int Nc8 = (min(a.vchunk, a.V - c0) + 7) / 8 * 8;
   GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, a.ldwt, nullptr, 0, nullptr, 0,
                 a.n, a.D, Nc8, 0, a.n_dev};
   EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
+  const int ks = head_dh_split(a, c0);
+  if (ks > 1) {
+    q.part = a.part;
+    return launch_gemm_split(q, ef, ks, s);
+  }
   return launch_gemm(q, ef, s, a.gemm_cfg);
 }
 

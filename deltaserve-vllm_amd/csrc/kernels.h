@@ -155,6 +155,8 @@ struct HeadArgs {
                                   // vchunk a multiple of 256
   float* dH;                      // [n, D] fp32
   int gemm_cfg;                   // tile of the dH product (-1: by shape)
+  float* part = nullptr;          // split-K partials for the dH product (null: no split)
+  long part_elems = 0;
 };
 // Chunk c0 (a multiple of vchunk) of pass 1 / pass 2; head_reduce between the passes.
 int head_num_chunks(const HeadArgs& a);
@@ -163,6 +165,8 @@ hipError_t head_stats(const HeadArgs& a, int c0, hipStream_t s);
 hipError_t head_reduce(const HeadArgs& a, hipStream_t s);
 hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s);
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s);
+// K splits head_chunk_dh uses for chunk c0 (1: none)
+int head_dh_split(const HeadArgs& a, int c0);
 
 // ---- optim.hip
 struct OptTensor {

@@ -37,10 +37,13 @@ def _lib():
     L.load()
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("cfg", [0, 1, 2, -2])
 @pytest.mark.parametrize("M,N,K,K2", [(300, 520, 264, 24), (64, 64, 64, 0), (513, 260, 1024, 16),
-                                      (1, 8, 8, 8)])
+                                      (1, 8, 8, 8), (513, 264, 1024, 16), (200, 1024, 4096, 64),
+                                      (1, 8, 512, 8)])
 def test_gemm_nt(cfg, M, N, K, K2):
+    """cfg -2 splits K (the last three shapes: 4, 8 and 2 K slices, the
+    slices crossing into the second K segment) and sums the fp32 partials."""
     from deltaserve_amd import ops
     A = _bf(_rnd(M, K, seed=1))
     B = _bf(_rnd(N, K, seed=2))
