@@ -755,13 +755,16 @@ hipError_t launch_gemm(const GemmProblem& p, const Epi& e, hipStream_t s, int cf
 // tiles to fill the chip: `ks` blocks per tile each store the fp32 partial
 // of a slice of K to p.part ([ks, M, N]), then one reduction launch sums them
 // and applies the epilogue. EpiBF16 and EpiF32 only; N a multiple of 8.
+// Splits so the tiles × splits blocks fit one round of the 256 CUs (a second,
+// partly filled round costs more than it spreads), at least 4 K tiles each;
+// 1 when the problem has more than 128 tiles (the fp32 partials' traffic
+// would buy no more parallelism).
 inline int gemm_split_count(int M, int N, int K) {
   const long tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
   const int nk = (K + 63) / 64;
-  if (tiles >= 192 || N % 8 != 0 || nk < 8) return 1;
-  int ks = (int)((256 + tiles - 1) / tiles);
-  ks = std::min(ks, std::min(8, nk / 4));
-  return std::max(ks, 1);
+  if (tiles > 128 || N % 8 != 0 || nk < 8) return 1;
+  const int ks = std::min((int)(256 / tiles), std::min(8, nk / 4));
+  return ks >= 2 ? ks : 1;
 }
 template <class Epi>
 hipError_t launch_gemm_split(const GemmProblem& p, const Epi& e, int ks, hipStream_t s) {
