@@ -385,25 +385,52 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
       }
   }
   const bool pw = w < RB1;
-  auto issue = [&](int k, int slot) {
-    const int t = ta + k * 32, rv = max(min(tb - t, 32), 0);
-    bf16* d = smem + slot * SE;
+  // Chunk loads. Everything but the chunk's row offset is set up once per
+  // block: one descriptor over the block's rows [ta, tb) and columns
+  // [c0, c0 + 512) ∩ [0, C) (rows past tb fall outside it and load zeros),
+  // the lanes' byte offsets of the 8 tile loads (load 2q + i: sub-tile q,
+  // tile rows 4·(4i + w) + lane/16, chunk (lane%16) ^ f(row), as in
+  // tile256_dma) and of the P load. A load with no valid row or column reads
+  // the zero page instead, so every load touches memory and the ring's loads
+  // complete in issue order. (Computing all of this per chunk made the issue
+  // of a chunk's loads take longer than streaming it.)
+  const u32x4 zs = zero_rsrc();
+  const int cvb = min(a.C - c0, 512);
+  const u32x4 rx = make_rsrc(tb > ta ? a.X + (long)ta * a.ldx + c0 : a.X,
+                             tb > ta ? (int)(((long)(tb - ta - 1) * a.ldx + cvb) * 2) : 0);
+  int xl[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int cc = c0 + 128 * q, cv = max(min(a.C - cc, 128), 0);
-      tile256_dma<32>(rv > 0 && cv > 0 ? a.X + (long)t * a.ldx + cc : a.X, a.ldx,
-                      cv > 0 ? rv : 0, cv, d + q * 32 * 128, w, lane);
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = 4 * (4 * i + w) + (lane >> 4);
+      const int col = 128 * q + (((lane & 15) ^ aswz(r)) << 3);
+      xl[2 * q + i] = col < cvb ? (int)(((long)r * a.ldx + col) * 2) : 0x7ff00000;
     }
+  const int per_row = R1 / 8, prow = (w * 64 + lane) / per_row, pch = (w * 64 + lane) % per_row;
+  const u32x4 rp = make_rsrc(tb > ta ? a.P + (long)ta * a.ldp : a.P,
+                             tb > ta ? (int)(((long)(tb - ta - 1) * a.ldp + R1) * 2) : 0);
+  const int po0 = prow < 32 ? (int)(((long)prow * a.ldp + pch * 8) * 2) : 0x7ff00000;
+  const unsigned lds0 = lds_addr(smem);
+  auto issue = [&](int k, int slot) {
+    const int rv = max(min(tb - ta - k * 32, 32), 0);  // valid rows of the chunk (uniform)
+    const int xk = (int)((long)k * 32 * a.ldx * 2), pk = (int)((long)k * 32 * a.ldp * 2);
+    const unsigned d = lds0 + (unsigned)(slot * SE * 2);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r0 = 4 * (4 * i + w);
+        const bool live = r0 < rv && 128 * q < cvb;
+        lds_dma16(live ? rx : zs, live ? xl[2 * q + i] + xk : lane * 16,
+                  d + (unsigned)((q * 32 * 128 + r0 * 128) * 2));
+      }
     if (pw) {
-      // P rows of R1 ranks: lane q of load w covers row q / (R1/8), ranks 8·(q % (R1/8))
-      const int qq = w * 64 + lane, per_row = R1 / 8;
-      const int row = qq / per_row, ch = qq % per_row;
-      const int bytes = rv > 0 ? (int)((((long)(rv - 1) * a.ldp) + R1) * 2) : 0;
-      const u32x4 rs = make_rsrc(rv > 0 ? a.P + (long)t * a.ldp : a.P, bytes);
-      const int voff = row < 32 ? (int)(((long)row * a.ldp + ch * 8) * 2) : 0x7ff00000;
+      // P rows of R1 ranks: lane l of load w covers row (64w + l) / (R1/8),
+      // ranks 8·((64w + l) % (R1/8))
       const bool live = w * 64 / per_row < rv;  // the wave's first row is valid
-      lds_dma16(pick_rsrc(live, rs, zero_rsrc()), live ? voff : lane * 16,
-                lds_addr(d + XT + w * 512));
+      lds_dma16(live ? rp : zs, live ? po0 + pk : lane * 16,
+                d + (unsigned)((XT + w * 512) * 2));
     }
   };
   f32x4 accT[8][RB1];
