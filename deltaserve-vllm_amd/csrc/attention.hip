@@ -47,14 +47,36 @@ constexpr int TILE = TR * HD;      // elements per tile (16 KB)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kScale = 0.08838834764831845f;  // 1/sqrt(128)
 
-// Rows t0 .. t0+63 (those below L) of a sequence starting at global row st,
-// columns col0 .. col0+127, into a swizzled tile (4 loads per lane).
-DSB_DEV void tile_dma(const bf16* mat, long ld, int st, int t0, int L, int col0, bf16* tile,
-                      int wave, int lane) {
-  const int rows = min(max(L - t0, 0), TR);
-  tile256_dma<TR>(rows > 0 ? mat + (long)(st + t0) * ld + col0 : mat, ld, rows, 128, tile, wave,
-                  lane);
-}
+// Direct-to-LDS loads of one sequence's 64-row × 128-column tiles of a
+// [rows, ld] operand, set up once per block: one descriptor over the
+// sequence's rows (rows from L on fall outside it and load zeros; the
+// kernels wait for all their loads at once, so the loads' completion order
+// does not matter) and the lane's byte offset. The tile layout is the one
+// row_frag / tr_frag read (tile256.h: chunk c of row r in slot c ^ aswz(r)).
+// The four loads a wave issues per tile (tile rows 4·(4i + w) + lane/16,
+// i = 0..3) share the lane's chunk, since aswz(r) depends only on r modulo
+// 16, so load i is the lane's first offset plus 16·i rows. Setting up a
+// descriptor and lane offsets per load (a lane-to-scalar move for every
+// descriptor word) made the loads' issue a large share of each tile step.
+struct SeqTiles {
+  u32x4 rs;
+  int off0;  // bytes: row 4w + lane/16, the lane's chunk
+  int ldb;   // row stride in bytes
+  DSB_DEV SeqTiles(const bf16* mat, long ld, int st, int L, int wave, int lane) {
+    rs = make_rsrc(mat + (long)st * ld, (int)((long)max(L, 0) * ld * 2));
+    const int r = 4 * wave + (lane >> 4);
+    off0 = (int)(((long)r * ld + (((lane & 15) ^ aswz(r)) << 3)) * 2);
+    ldb = (int)(ld * 2);
+  }
+  // tile rows t0 .. t0+63, columns col0 .. col0+127, to the tile at LDS byte
+  // address `tile`
+  DSB_DEV void load(int t0, int col0, unsigned tile, int wave) const {
+    const int base = t0 * ldb + col0 * 2;
+#pragma unroll
+    for (int i = 0; i < TR / 16; ++i)
+      lds_dma16(rs, off0 + base + 16 * i * ldb, tile + (unsigned)((4 * (4 * i + wave)) * 256));
+  }
+};
 
 // Row fragments of one global row (lane's row, 8 × 16 columns) straight to registers.
 DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool ok, int lh,
@@ -195,8 +217,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int nt = qb.nt;
 
   const FragOffs fo(lane);
-  tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
-  tile_dma(a.v, a.ldv, st, 0, L, kvh * HD, smem + TILE, w, lane);
+  const SeqTiles tk(a.k, a.ldk, st, L, w, lane), tv(a.v, a.ldv, st, L, w, lane);
+  const unsigned lds0 = lds_addr(smem);
+  tk.load(0, kvh * HD, lds0, w);
+  tv.load(0, kvh * HD, lds0 + TILE * 2, w);
   // The wave computes the tiles with a key at or before its last query
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
@@ -206,9 +230,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     wait_vm<0>();
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
     if (t + 1 < nt) {
-      bf16* nxt = smem + ((t + 1) & 1) * 2 * TILE;
-      tile_dma(a.k, a.ldk, st, (t + 1) * TR, L, kvh * HD, nxt, w, lane);
-      tile_dma(a.v, a.ldv, st, (t + 1) * TR, L, kvh * HD, nxt + TILE, w, lane);
+      const unsigned nxt = lds0 + (unsigned)(((t + 1) & 1) * 2 * TILE * 2);
+      tk.load((t + 1) * TR, kvh * HD, nxt, w);
+      tv.load((t + 1) * TR, kvh * HD, nxt + TILE * 2, w);
     }
   };
   for (int t = 0; t < nt_w; ++t) {
@@ -395,8 +419,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   const int nt = qb.nt;
 
   const FragOffs fo(lane);
-  tile_dma(a.k, a.ldk, st, 0, L, kvh * HD, smem, w, lane);
-  tile_dma(a.v, a.ldv, st, 0, L, kvh * HD, smem + TILE, w, lane);
+  const SeqTiles tk(a.k, a.ldk, st, L, w, lane), tv(a.v, a.ldv, st, L, w, lane);
+  const unsigned lds0 = lds_addr(smem);
+  tk.load(0, kvh * HD, lds0, w);
+  tv.load(0, kvh * HD, lds0 + TILE * 2, w);
   // The wave computes the tiles with a key at or before its last query
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
@@ -406,9 +432,9 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
     wait_vm<0>();
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
     if (t + 1 < nt) {
-      bf16* nxt = smem + ((t + 1) & 1) * 2 * TILE;
-      tile_dma(a.k, a.ldk, st, (t + 1) * TR, L, kvh * HD, nxt, w, lane);
-      tile_dma(a.v, a.ldv, st, (t + 1) * TR, L, kvh * HD, nxt + TILE, w, lane);
+      const unsigned nxt = lds0 + (unsigned)(((t + 1) & 1) * 2 * TILE * 2);
+      tk.load((t + 1) * TR, kvh * HD, nxt, w);
+      tv.load((t + 1) * TR, kvh * HD, nxt + TILE * 2, w);
     }
   };
   for (int t = 0; t < nt_w; ++t) {
@@ -523,12 +549,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     nl = ok ? a.lse[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
     nd = ok ? a.dsum[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
   };
+  const SeqTiles tq(a.q, a.ldq, st, L, w, lane), to(a.dout, a.lddo, st, L, w, lane);
+  const unsigned lds0 = lds_addr(smem);
   auto stage = [&](int it, int sidx) {
     const int hq = kvh * G + it / nq;
     const int q0 = (qt0 + it % nq) * TR;
-    bf16* d = smem + sidx * 2 * TILE;
-    tile_dma(a.q, a.ldq, st, q0, L, hq * HD, d, w, lane);
-    tile_dma(a.dout, a.lddo, st, q0, L, hq * HD, d + TILE, w, lane);
+    const unsigned d = lds0 + (unsigned)(sidx * 2 * TILE * 2);
+    tq.load(q0, hq * HD, d, w);
+    to.load(q0, hq * HD, d + TILE * 2, w);
   };
   if (nit > 0) {
     load_ld(0);
