@@ -72,11 +72,36 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   // ranks j0 .. j0 + Rg - 1 of this block (groups of 64 on grid.y)
   const int j0 = blockIdx.y * 64, Rg = min(a.R - j0, 64);
   const bf16* Bg = a.B + (long)j0 * a.ldb;
+  // Chunk loads (the tile256_dma layout), set up once per block: one
+  // descriptor per operand over its rows, the lane's offsets; per chunk only
+  // the column advance, the lane's column test (past K: zeros) and, for a
+  // load with no valid row or column, the zero page (so every load touches
+  // memory and the ring's counted waits hold).
+  const u32x4 zs = zero_rsrc();
+  const u32x4 rx = make_rsrc(X0, (int)(((long)(rows - 1) * a.ldx + a.K) * 2));
+  const u32x4 rb = make_rsrc(Bg, Rg > 0 ? (int)(((long)(Rg - 1) * a.ldb + a.K) * 2) : 0);
+  const int lr4 = 4 * w + (lane >> 4);                  // load 0's row; load i adds 16·i
+  const int lcol = ((lane & 15) ^ aswz(lr4)) << 3;      // aswz(r) depends on r % 16 only
+  const int xl = (int)(((long)lr4 * a.ldx + lcol) * 2), bl = (int)(((long)lr4 * a.ldb + lcol) * 2);
+  const unsigned lds0 = lds_addr(smem);
   auto issue = [&](int c, int slot) {
-    const int k0 = c * 128, cv = max(min(a.K - k0, 128), 0);
-    bf16* d = smem + slot * SE;
-    tile256_dma<TR>(cv > 0 ? X0 + k0 : X0, a.ldx, rows, cv, d, w, lane);
-    tile256_dma<16 * RB>(cv > 0 ? Bg + k0 : Bg, a.ldb, Rg, cv, d + XT, w, lane);
+    const int k0 = c * 128;
+    const bool kin = k0 < a.K;          // uniform
+    const bool cin = k0 + lcol < a.K;   // the lane's chunk
+    const unsigned d = lds0 + (unsigned)(slot * SE * 2);
+#pragma unroll
+    for (int i = 0; i < TR / 16; ++i) {
+      const bool live = kin && 4 * (4 * i + w) < rows;
+      const int v = cin ? xl + (int)((long)16 * i * a.ldx * 2) + k0 * 2 : 0x7ff00000;
+      lds_dma16(live ? rx : zs, live ? v : lane * 16, d + (unsigned)((4 * (4 * i + w)) * 256));
+    }
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const bool live = kin && 4 * (4 * i + w) < Rg;
+      const int v = cin ? bl + (int)((long)16 * i * a.ldb * 2) + k0 * 2 : 0x7ff00000;
+      lds_dma16(live ? rb : zs, live ? v : lane * 16,
+                d + (unsigned)((XT + (4 * (4 * i + w)) * 128) * 2));
+    }
   };
   constexpr int LPS = TT + RB;  // loads per lane per stage
   f32x4 acc[TT][RB];
@@ -186,20 +211,40 @@ __global__ __launch_bounds__(256, 2) void lora_tn_partial_kernel(TnBatch b) {
   // P chunk loads: 32 rows × R ranks = 4·RB loads of 1 KB; wave w issues the
   // ones with index ≡ w (mod 4), so waves 0 .. RB-1 issue one each per stage.
   const bool pw = w < RB;
+  // Chunk loads, set up once per block as in lora_dual: descriptors over the
+  // block's rows [ta, tb) of X (columns c0 .. c0+cv) and of P, lane offsets;
+  // per chunk only the row advance and, for a load with no valid row, the
+  // zero page.
+  const u32x4 zs = zero_rsrc();
+  const u32x4 rx = make_rsrc(tb > ta ? a.X + (long)ta * a.ldx + c0 : a.X,
+                             tb > ta ? (int)(((long)(tb - ta - 1) * a.ldx + cv) * 2) : 0);
+  int xl[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 4 * (4 * i + w) + (lane >> 4);
+    const int col = ((lane & 15) ^ aswz(r)) << 3;
+    xl[i] = col < cv ? (int)(((long)r * a.ldx + col) * 2) : 0x7ff00000;
+  }
+  const int per_row = R / 8, prow = (w * 64 + lane) / per_row, pch = (w * 64 + lane) % per_row;
+  const u32x4 rp = make_rsrc(tb > ta ? Pg + (long)ta * a.ldp : Pg,
+                             tb > ta ? (int)(((long)(tb - ta - 1) * a.ldp + R) * 2) : 0);
+  const int po0 = prow < 32 ? (int)(((long)prow * a.ldp + pch * 8) * 2) : 0x7ff00000;
+  const unsigned lds0 = lds_addr(smem);
   auto issue = [&](int k, int slot) {
-    const int t = ta + k * 32, rv = max(min(tb - t, 32), 0);
-    bf16* d = smem + slot * SE;
-    tile256_dma<32>(rv > 0 ? a.X + (long)t * a.ldx + c0 : a.X, a.ldx, rv, cv, d, w, lane);
+    const int rv = max(min(tb - ta - k * 32, 32), 0);  // valid rows of the chunk (uniform)
+    const int xk = (int)((long)k * 32 * a.ldx * 2), pk = (int)((long)k * 32 * a.ldp * 2);
+    const unsigned d = lds0 + (unsigned)(slot * SE * 2);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = 4 * (4 * i + w);
+      const bool live = r0 < rv && cv > 0;
+      lds_dma16(live ? rx : zs, live ? xl[i] + xk : lane * 16, d + (unsigned)(r0 * 256));
+    }
     if (pw) {
-      // P rows of R ranks: lane q of load w covers row q / (R/8), ranks 8·(q % (R/8))
-      const int q = w * 64 + lane, per_row = R / 8;
-      const int row = q / per_row, ch = q % per_row;
-      const int bytes = rv > 0 ? (int)((((long)(rv - 1) * a.ldp) + R) * 2) : 0;
-      const u32x4 rs = make_rsrc(rv > 0 ? Pg + (long)t * a.ldp : Pg, bytes);
-      const int voff = row < 32 ? (int)(((long)row * a.ldp + ch * 8) * 2) : 0x7ff00000;
+      // P rows of R ranks: lane l of load w covers row (64w + l) / (R/8),
+      // ranks 8·((64w + l) % (R/8))
       const bool live = w * 64 / per_row < rv;  // the wave's first row is valid
-      lds_dma16(pick_rsrc(live, rs, zero_rsrc()), live ? voff : lane * 16,
-                lds_addr(d + XT + w * 512));
+      lds_dma16(live ? rp : zs, live ? po0 + pk : lane * 16, d + (unsigned)((XT + w * 512) * 2));
     }
   };
   f32x4 acc[2][RB];
