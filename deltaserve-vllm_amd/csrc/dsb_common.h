@@ -143,15 +143,6 @@ DSB_DEV u32x4 make_rsrc(const void* base, int bytes) {
 // (64 lanes × 16 B), so the loads of a pipelined loop complete in order.
 static __device__ __align__(256) bf16 zero_page[512];
 DSB_DEV u32x4 zero_rsrc() { return make_rsrc(zero_page, (int)sizeof(zero_page)); }
-// Descriptor a or b by a wave-uniform condition, chosen word by word so the
-// choice stays in scalar registers.
-DSB_DEV u32x4 pick_rsrc(bool first, u32x4 a, u32x4 b) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_readfirstlane(first ? a[i] : b[i]);
-  return r;
-}
-
 // Buffer descriptor for plain (register-destination) buffer loads: same
 // fields as make_rsrc; loads at or beyond `bytes` return zeros.
 DSB_DEV __amdgpu_buffer_rsrc_t make_brsrc(const void* base, int bytes) {

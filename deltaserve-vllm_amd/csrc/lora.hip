@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   // ranks j0 .. j0 + Rg - 1 of this block (groups of 64 on grid.y)
   const int j0 = blockIdx.y * 64, Rg = min(a.R - j0, 64);
   const bf16* Bg = a.B + (long)j0 * a.ldb;
-  // Chunk loads (the tile256_dma layout), set up once per block: one
+  // Chunk loads (the tile layout of tile256.h), set up once per block: one
   // descriptor per operand over its rows, the lane's offsets; per chunk only
   // the column advance, the lane's column test (past K: zeros) and, for a
   // load with no valid row or column, the zero page (so every load touches
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(256, 1) void lora_dual_kernel(DualBatch b) {
   // [c0, c0 + 512) ∩ [0, C) (rows past tb fall outside it and load zeros),
   // the lanes' byte offsets of the 8 tile loads (load 2q + i: sub-tile q,
   // tile rows 4·(4i + w) + lane/16, chunk (lane%16) ^ f(row), as in
-  // tile256_dma) and of the P load. A load with no valid row or column reads
+  // tile256.h) and of the P load. A load with no valid row or column reads
   // the zero page instead, so every load touches memory and the ring's loads
   // complete in issue order. (Computing all of this per chunk made the issue
   // of a chunk's loads take longer than streaming it.)

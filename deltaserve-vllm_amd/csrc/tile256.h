@@ -67,29 +67,12 @@ DSB_DEV bf16x8 tr_frag(const char* t, const FragOffs& fo, int base, int df) {
 
 DSB_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }  // v_exp_f32; x <= 8 here
 
-// Direct-to-LDS load of a ROWS × 128 bf16 tile: rows r < rows_valid of `base`
-// (row stride ld elements), columns < cols_valid (a multiple of 8); the rest
-// of the tile is zero-filled. 256 threads issue ROWS/16 loads each: load i of
-// wave w covers tile rows 4·(4i + w) .. +3 and lane l fills slot l%16 of row
-// l/16 with chunk (l%16) ^ f(row). A load with no valid row (or no valid
-// column) reads the zero page, so every load touches memory and the loads of
-// a ring complete in issue order.
-template <int ROWS>
-DSB_DEV void tile256_dma(const bf16* base, long ld, int rows_valid, int cols_valid, bf16* tile,
-                         int wave, int lane) {
-  static_assert(ROWS % 16 == 0, "4 waves x 4 rows per load");
-  const int bytes =
-      rows_valid > 0 && cols_valid > 0 ? (int)(((long)(rows_valid - 1) * ld + cols_valid) * 2) : 0;
-  const u32x4 rs = make_rsrc(base, bytes), zs = zero_rsrc();
-  const int rl = lane >> 4, s = lane & 15;
-#pragma unroll
-  for (int i = 0; i < ROWS / 16; ++i) {
-    const int r0 = 4 * (4 * i + wave), r = r0 + rl;  // r0: wave-uniform
-    const int c = s ^ aswz(r);
-    const bool live = r0 < rows_valid && cols_valid > 0;  // row r0 has chunk 0 in bounds
-    const int voff = c * 8 < cols_valid ? (int)(((long)r * ld + c * 8) * 2) : 0x7ff00000;
-    lds_dma16(pick_rsrc(live, rs, zs), live ? voff : lane * 16, lds_addr(tile + r0 * 128));
-  }
-}
+// Direct-to-LDS tile fills (attention.hip SeqTiles, the LoRA kernels' chunk
+// loads) write this layout with 256 threads: load i of wave w covers tile
+// rows 4·(4i + w) .. +3, lane l filling slot l%16 of row 4·(4i + w) + l/16
+// with chunk (l%16) ^ aswz(row) (aswz(r) depends only on r % 16, so all
+// loads of a lane fetch the same chunk). Descriptors and lane offsets are set
+// up once per block and only the row or column advance changes per load:
+// building them per load costs more issue time than the load itself.
 
 }  // namespace dsb
