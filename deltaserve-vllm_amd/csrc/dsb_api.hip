@@ -258,7 +258,7 @@ struct dsb_handle {
   bool finalized = false;
   std::vector<void*> allocs;
   // workspace
-  bf16 *xn1, *qkv_pre, *qk, *ctx, *resid, *xn2, *gu, *hb, *gh;
+  bf16 *xn1, *qkv_pre, *qk, *ctx, *resid, *xn2, *gu, *hb;
   float *lse, *dsum;
   bf16 *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
   bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
@@ -415,7 +415,6 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->xn2, NN * D));
   CKR(dalloc(h, &h->gu, NN * 2 * I));
   CKR(dalloc(h, &h->hb, NN * I));
-  CKR(dalloc(h, &h->gh, NN * I));
   CKR(dalloc(h, &h->Zqkv_b, NN * 3 * r));
   CKR(dalloc(h, &h->Zo_b, NN * r));
   CKR(dalloc(h, &h->Zgu_b, NN * 2 * r));
@@ -667,7 +666,7 @@ template <class Epi>
 int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hipStream_t st,
          double ob, double xrow) {
   const double K = (double)p.K1 + p.K2;
-  if constexpr (std::is_same<Epi, EpiBF16>::value) {
+  if constexpr (std::is_same<Epi, EpiBF16>::value || std::is_same<Epi, EpiSwiGLUBwd>::value) {
     // too few 256×256 tiles for the chip: split K (unless a tile is forced)
     const int ksplit = h->gemm_cfg >= 0 ? 1 : gemm_split_count(p.M, p.N, p.K1 + p.K2);
     if (ksplit > 1 && (long)ksplit * p.M * p.N <= h->part_elems) {
@@ -1005,15 +1004,13 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
     if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
     {
-      // gh = g·W_down (+ gZ_d·A_d): grad wrt h = silu(gate)·up
+      // gh = g·W_down (+ gZ_d·A_d), the gradient wrt h = silu(gate)·up; the
+      // epilogue turns it into d_gate ‖ d_up (reads gate ‖ up, writes Ggu),
+      // so gh itself is never stored
       GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
                     hd ? ls.AdT : nullptr, (long)r, N, I, D, hd ? r : 0, nd};
-      EpiBF16 e{h->gh, (long)I, I, nullptr, 0};
-      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
-    }
-    {
-      KScope ks(h, st, "swiglu_bwd", 0, 0, 0, 10.0 * I, 0, 0);
-      LK(swiglu_bwd(h->gh, I, gu, ldgu, h->Ggu, 2L * I, N, nd, I, st));
+      EpiSwiGLUBwd e{gu, ldgu, h->Ggu, 2L * I, I};
+      CKR(gemm(h, "dswiglu", p, e, st, 8.0, 0.0));
     }
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];

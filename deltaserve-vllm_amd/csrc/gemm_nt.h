@@ -231,10 +231,13 @@ DSB_DEV int lds_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 // through a dependent type so the kernel template can use it before then.
 struct EpiF32;
 struct EpiBF16;
+struct EpiSwiGLUBwd;
 template <class E>
 struct SplitPart {
   using type = EpiF32;
-  static constexpr bool enabled = std::is_same<E, EpiBF16>::value || std::is_same<E, EpiF32>::value;
+  static constexpr bool enabled = std::is_same<E, EpiBF16>::value ||
+                                  std::is_same<E, EpiF32>::value ||
+                                  std::is_same<E, EpiSwiGLUBwd>::value;
 };
 
 template <int BM, int BN, int WM, int WN, class Epi>
@@ -611,6 +614,58 @@ struct EpiGLU {
   }
 };
 
+// SwiGLU backward in the epilogue of the product whose output is the gradient
+// wrt h = silu(gate)·up (ffn.py:40-45; the GEMM's N is I): from the bf16
+// rounding of each output value and the bf16 gate and up features GU[m, f],
+// GU[m, I + f] it writes d_gate to G[m, f] and d_up to G[m, I + f] (bf16),
+// so the [n, I] gradient itself never reaches memory. The gradient is rounded
+// to bf16 first, as the reference's bf16 matmul output is. I, ldgu, ldg
+// multiples of 8 and GU, G 16-byte aligned (whole 8-feature chunks).
+struct EpiSwiGLUBwd {
+  const bf16* GU;
+  long ldgu;
+  bf16* G;
+  long ldg;
+  int I;
+  struct Chunk {
+    u32x4 g, u;
+  };
+  DSB_DEV Chunk load(int m, int n) const {
+    const bf16* p = GU + (long)m * ldgu + n;
+    return Chunk{ldg128(p), ldg128(p + I)};
+  }
+  DSB_DEV void finish(int m, int n, const float* v, const Chunk& c) const {
+    float d[8], g[8], u[8], og[8], ou[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = (float)(bf16)v[i];
+    unpack8(c.g, g);
+    unpack8(c.u, u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sg = 1.f / (1.f + __expf(-g[e]));  // σ(gate)
+      og[e] = d[e] * u[e] * (sg * (1.f + g[e] * (1.f - sg)));
+      ou[e] = d[e] * (g[e] * sg);
+    }
+    bf16* o = G + (long)m * ldg + n;
+    stg128(o, pack8(og));
+    stg128(o + I, pack8(ou));
+  }
+  // the epilogue of one 8-column chunk (split-K reduction)
+  DSB_DEV void apply8(int m, int n, float* v) const {
+    if (n < I) finish(m, n, v, load(m, n));
+  }
+  template <int FM, int FN, int WM, int WN>
+  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+                   void* smem) const {
+    for_each_row8_pf(
+        acc, mw, nw, M, lane, wave, smem,
+        [&](int m, int n) { return n < I ? load(m, n) : Chunk{}; },
+        [&](int m, int n, float* v, const Chunk& c) {
+          if (n < I) finish(m, n, v, c);
+        });
+  }
+};
+
 // C (+)= acc, fp32 out.
 struct EpiF32 {
   float* C;
@@ -754,7 +809,8 @@ hipError_t launch_gemm(const GemmProblem& p, const Epi& e, hipStream_t s, int cf
 // K split over the grid's y dimension for problems with too few 256×256
 // tiles to fill the chip: `ks` blocks per tile each store the fp32 partial
 // of a slice of K to p.part ([ks, M, N]), then one reduction launch sums them
-// and applies the epilogue. EpiBF16 and EpiF32 only; N a multiple of 8.
+// and applies the epilogue (those with apply8: EpiBF16, EpiF32, EpiSwiGLUBwd);
+// N a multiple of 8.
 // Splits so the tiles × splits blocks fit one round of the 256 CUs (a second,
 // partly filled round costs more than it spreads), at least 4 K tiles each;
 // 1 when the problem has more than 128 tiles (the fp32 partials' traffic
@@ -768,8 +824,7 @@ inline int gemm_split_count(int M, int N, int K) {
 }
 template <class Epi>
 hipError_t launch_gemm_split(const GemmProblem& p, const Epi& e, int ks, hipStream_t s) {
-  static_assert(std::is_same<Epi, EpiBF16>::value || std::is_same<Epi, EpiF32>::value,
-                "split-K epilogues");
+  static_assert(SplitPart<Epi>::enabled, "split-K epilogues");
   const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
   if (nbm == 0 || nbn == 0) return hipSuccess;
   if (!p.part || p.N % 8 != 0 || ks < 2) return hipErrorInvalidValue;

@@ -26,8 +26,6 @@ hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* c
                     const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s);
 hipError_t swiglu_h(const bf16* gu, long ldgu, bf16* h, long ldh, int n, const int* n_dev,
                     int I, hipStream_t s);
-hipError_t swiglu_bwd(const bf16* gh, long ldgh, const bf16* gu, long ldgu, bf16* G, long ldg,
-                      int n, const int* n_dev, int I, hipStream_t s);
 
 // ---- attention.hip
 // Packed varlen causal GQA attention, head_dim 128. `tiles` holds one int4

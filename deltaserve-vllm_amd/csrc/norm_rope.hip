@@ -345,33 +345,6 @@ __global__ __launch_bounds__(256) void swiglu_h_kernel(const bf16* __restrict__ 
   stg128(h + (long)m * ldh + c * 8, pack8(o));
 }
 
-// SwiGLU backward (ffn.py:29-48): gh = grad wrt h = silu(gate)·up,
-//   G[m, n] = gh·up·silu'(gate), G[m, I + n] = gh·silu(gate),
-//   silu'(g) = σ(g)·(1 + g·(1 − σ(g))).
-__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const bf16* __restrict__ gh, long ldgh,
-                                                         const bf16* __restrict__ gu, long ldgu,
-                                                         bf16* __restrict__ G, long ldg, int n,
-                                                         const int* n_dev, int I) {
-  int N = n;
-  if (n_dev) N = min(N, *n_dev);
-  const int cpr = I >> 3;
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)N * cpr) return;
-  const int m = (int)(idx / cpr), c = (int)(idx % cpr);
-  float d[8], g[8], u[8], og[8], ou[8];
-  unpack8(ldg128(gh + (long)m * ldgh + c * 8), d);
-  unpack8(ldg128(gu + (long)m * ldgu + c * 8), g);
-  unpack8(ldg128(gu + (long)m * ldgu + I + c * 8), u);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float sg = 1.f / (1.f + __expf(-g[e]));
-    og[e] = d[e] * u[e] * (sg * (1.f + g[e] * (1.f - sg)));
-    ou[e] = d[e] * (g[e] * sg);
-  }
-  stg128(G + (long)m * ldg + c * 8, pack8(og));
-  stg128(G + (long)m * ldg + I + c * 8, pack8(ou));
-}
-
 // ------------------------------------------------------------------ launchers
 
 hipError_t rmsnorm_fwd(const bf16* x, long ldx, const bf16* w, bf16* y, long ldy, int rows,
@@ -439,15 +412,6 @@ hipError_t swiglu_h(const bf16* gu, long ldgu, bf16* h, long ldh, int n, const i
   if (tot <= 0) return hipSuccess;
   hipLaunchKernelGGL(swiglu_h_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, gu,
                      ldgu, h, ldh, n, n_dev, I);
-  return hipGetLastError();
-}
-
-hipError_t swiglu_bwd(const bf16* gh, long ldgh, const bf16* gu, long ldgu, bf16* G, long ldg,
-                      int n, const int* n_dev, int I, hipStream_t s) {
-  const long tot = (long)n * (I >> 3);
-  if (tot <= 0) return hipSuccess;
-  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, gh,
-                     ldgh, gu, ldgu, G, ldg, n, n_dev, I);
   return hipGetLastError();
 }
 
