@@ -646,9 +646,10 @@ struct EpiSwiGLUBwd {
       og[e] = d[e] * u[e] * (sg * (1.f + g[e] * (1.f - sg)));
       ou[e] = d[e] * (g[e] * sg);
     }
+    // streamed past the caches, as store8_bf16 does
     bf16* o = G + (long)m * ldg + n;
-    stg128(o, pack8(og));
-    stg128(o + I, pack8(ou));
+    __builtin_nontemporal_store(pack8(og), reinterpret_cast<u32x4*>(o));
+    __builtin_nontemporal_store(pack8(ou), reinterpret_cast<u32x4*>(o + I));
   }
   // the epilogue of one 8-column chunk (split-K reduction)
   DSB_DEV void apply8(int m, int n, float* v) const {
