@@ -278,6 +278,7 @@ struct dsb_handle {
   long tn_work_elems;
   float* part = nullptr;  // split-K partials of the products with too few 256×256 tiles
   long part_elems = 0;
+  int ncu = 0;  // compute units of the device (wave-quantisation tails)
   std::vector<TnArgs> tn_pending;  // TN passes of the current layer (see tn_flush)
   float *cosb, *sinb, *inv_freq;
   int* labels;
@@ -446,13 +447,20 @@ int finalize(dsb_handle* h) {
   h->tn_work_elems = 32L << 20;
   CKR(dalloc(h, &h->tn_work, h->tn_work_elems));
   {
+    int dev = 0;
+    CK(hipGetDevice(&dev));
+    CK(hipDeviceGetAttribute(&h->ncu, hipDeviceAttributeMultiprocessorCount, dev));
     // split-K partials: the largest ks·M·N over the cycle's bf16/fp32 products
-    // (output width, reduction depth) that gemm_split_count splits
+    // (output width, reduction depth) that gemm_split_count splits, and the
+    // largest ks·tail tile partials of those gemm_tail_split splits
     const int shapes[][2] = {{W3, D}, {D, q}, {I, D}, {D, 2 * I}, {q, D}, {D, W3}, {D, h->vchunk}};
     long need = 0;
     for (const auto& sh : shapes) {
       const int ks = gemm_split_count(N, sh[0], sh[1]);
       if (ks > 1) need = std::max(need, (long)ks * N * sh[0]);
+      int tail = 0;
+      const int kt = gemm_tail_split(N, sh[0], sh[1], h->ncu, &tail);
+      if (ks == 1 && kt > 1) need = std::max(need, (long)kt * tail * 65536);
     }
     h->part_elems = need;
     if (need > 0) CKR(dalloc(h, &h->part, need));
@@ -675,6 +683,17 @@ int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hip
       GemmProblem q = p;
       q.part = h->part;
       LK(launch_gemm_split(q, e, ksplit, st));
+      return 0;
+    }
+    // a partly filled last round of tiles: split K over the tail tiles
+    int tail = 0;
+    const int kt = h->gemm_cfg >= 0 || ksplit > 1
+                       ? 1
+                       : gemm_tail_split(p.M, p.N, p.K1 + p.K2, h->ncu, &tail);
+    if (kt > 1 && (long)kt * tail * 65536 <= h->part_elems) {
+      KScope ks(h, st, std::string("gemm256t_") + epi, 2.0 * p.N * K, 0, 0,
+                2.0 * K + ob * p.N + xrow, 0, 2.0 * p.N * K);
+      LK(launch_gemm_tail(p, e, kt, tail, h->part, st));
       return 0;
     }
   }
@@ -1760,7 +1779,27 @@ int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const vo
   GemmProblem p{(const bf16*)A, lda, (const bf16*)B, ldb, (const bf16*)A2, lda2,
                 (const bf16*)B2, ldb2, M, N, K1, K2, nullptr};
   // cfg -2: split K as the cycle does for problems with too few 256-wide
-  // tiles (partials in a buffer allocated for the call); by shape otherwise
+  // tiles; cfg -3: split K over the tiles of a partly filled last round, as
+  // the cycle does (partials in a buffer allocated for the call); by shape
+  // otherwise
+  if (cfg == -3) {
+    int dev = 0, ncu = 0, tail = 0;
+    OPCK(hipGetDevice(&dev));
+    OPCK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    const int kt = gemm_tail_split(M, N, K1 + K2, ncu, &tail);
+    if (kt > 1) {
+      float* tp = nullptr;
+      OPCK(hipMalloc((void**)&tp, sizeof(float) * (size_t)kt * tail * 65536));
+      hipError_t e1;
+      if (out_f32) e1 = launch_gemm_tail(p, EpiF32{(float*)C, ldc, N, accumulate}, kt, tail, tp, s);
+      else e1 = launch_gemm_tail(p, EpiBF16{(bf16*)C, ldc, N, (const bf16*)R, ldr}, kt, tail, tp, s);
+      const hipError_t e2 = e1 == hipSuccess ? hipStreamSynchronize(s) : e1;
+      (void)hipFree(tp);
+      OPCK(e2);
+      return 0;
+    }
+    cfg = -1;
+  }
   const int ks = cfg == -2 ? gemm_split_count(M, N, K1 + K2) : 1;
   if (cfg == -2) cfg = -1;
   if (ks > 1) {

@@ -68,6 +68,13 @@ struct GemmProblem {
   // partial to part + z·M·N (row stride N) instead of running the epilogue;
   // gemm_split_reduce then sums the partials in order and applies it.
   float* part = nullptr;
+  // Tail launch (launch_gemm_tail): the launch's block x takes tile
+  // tile0 + x of the problem's tile order; with tpart set, a block stores its
+  // fp32 partial as one BM × BN tile (row stride BN) at
+  // tpart + (blockIdx.y · gridDim.x + blockIdx.x) · BM · BN instead of running
+  // the epilogue.
+  int tile0 = 0;
+  float* tpart = nullptr;
 };
 
 DSB_DEV void tile_map(int bid, int nbm, int nbn, int& pm, int& pn) {
@@ -260,7 +267,7 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   if (p.M_dev) M = min(M, *p.M_dev);
   const int nbm = (p.M + BM - 1) / BM, nbn = (p.N + BN - 1) / BN;
   int pm, pn;
-  tile_map(blockIdx.x, nbm, nbn, pm, pn);
+  tile_map(blockIdx.x + p.tile0, nbm, nbn, pm, pn);
   const int m0 = pm * BM, n0 = pn * BN;
   if (m0 >= M) return;
 
@@ -492,6 +499,16 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     if (p.part) {
       const typename SplitPart<Epi>::type ep{p.part + (long)blockIdx.y * p.M * p.N, (long)p.N,
                                              p.N, 0};
+      ep.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
+                                      (void*)smem);
+      return;
+    }
+    if (p.tpart) {
+      // tile-local partial: base shifted so that global (m, n) lands at
+      // (m − m0)·BN + (n − n0) of the block's tile
+      const long blk = (long)blockIdx.y * gridDim.x + blockIdx.x;
+      const typename SplitPart<Epi>::type ep{
+          p.tpart + blk * (BM * BN) - ((long)m0 * BN + n0), (long)BN, p.N, 0};
       ep.template run<FM, FN, WM, WN>(acc, m0 + wm * TM, n0 + wn * TN, M, lane, wave,
                                       (void*)smem);
       return;
@@ -834,6 +851,75 @@ hipError_t launch_gemm_split(const GemmProblem& p, const Epi& e, int ks, hipStre
   const long n = (long)p.M * (p.N / 8);
   hipLaunchKernelGGL(gemm_split_reduce_kernel<Epi>, dim3((unsigned)((n + 255) / 256)), dim3(256),
                      0, s, p, ks, e);
+  return hipGetLastError();
+}
+
+// Sum of the tail launch's tile-local partials (launch_gemm_tail) in split
+// order through epi.apply8: 32 blocks per tail tile, one 8-column chunk of
+// the 256 × 256 tile per thread; live rows and columns only.
+template <class Epi>
+__global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(GemmProblem p, int ks, int ntail,
+                                                               Epi epi) {
+  int M = p.M;
+  if (p.M_dev) M = min(M, *p.M_dev);
+  const int t = blockIdx.x >> 5;                            // tail tile
+  const int c = ((blockIdx.x & 31) << 8) + threadIdx.x;     // chunk within the tile
+  const int row = c >> 5, col = (c & 31) << 3;
+  const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
+  int pm, pn;
+  tile_map(p.tile0 + t, nbm, nbn, pm, pn);
+  const int m = pm * 256 + row, n = pn * 256 + col;
+  if (m >= M || n >= p.N) return;
+  const float* src = p.tpart + (long)t * 65536 + row * 256 + col;
+  const long plane = (long)ntail * 65536;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < ks; ++z) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src + z * plane);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + z * plane + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] += a[i];
+      v[4 + i] += b[i];
+    }
+  }
+  epi.apply8(m, n, v);
+}
+
+// Wave-quantisation tail: a problem whose 256 × 256 tiles fill whole rounds
+// of the ncu CUs plus a partial one of `tail` ≤ ncu/2 tiles. The full rounds
+// run as one launch; the tail tiles then split K over ks blocks each
+// (ks·tail ≤ ncu, at least 16 K tiles per block: with fewer, the partial
+// stores and the reduction cost more than the idle CUs), store fp32 tile
+// partials, and a reduction applies the epilogue, so the last round takes
+// about 1/ks of a tile's time instead of a whole one. Returns ks (1: no tail
+// split) and the tail tile count.
+inline int gemm_tail_split(int M, int N, int K, int ncu, int* tail) {
+  const long tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
+  const int nk = (K + 63) / 64;
+  *tail = ncu > 0 ? (int)(tiles % ncu) : 0;
+  if (ncu <= 0 || ncu % 8 || tiles <= ncu || *tail == 0 || N % 8 != 0 || nk < 8) return 1;
+  const int ks = std::min(ncu / *tail, std::min(8, nk / 16));
+  return ks >= 2 ? ks : 1;
+}
+// tpart holds ks · tail · 65536 floats.
+template <class Epi>
+hipError_t launch_gemm_tail(const GemmProblem& p, const Epi& e, int ks, int tail, float* tpart,
+                            hipStream_t s) {
+  static_assert(SplitPart<Epi>::enabled, "tail-split epilogues");
+  const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
+  const int full = nbm * nbn - tail;
+  // full is a whole number of rounds of a CU count that is a multiple of 8,
+  // so the tail launch's block x lands on the XCD that tile_map assumes
+  if (!tpart || tail <= 0 || full <= 0 || full % 8 || ks < 2 || p.N % 8 || p.part)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(full), dim3(256), 0, s, p, e);
+  GemmProblem q = p;
+  q.tile0 = full;
+  q.tpart = tpart;
+  hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(tail, ks), dim3(256), 0, s, q,
+                     e);
+  hipLaunchKernelGGL(gemm_tail_reduce_kernel<Epi>, dim3(tail * 32), dim3(256), 0, s, q, ks, tail,
+                     e);
   return hipGetLastError();
 }
 

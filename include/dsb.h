@@ -230,7 +230,9 @@ int dsb_save_ids(const int64_t* ids, int64_t ids_len, const int64_t* src, const 
 
 /* C = A·Bᵀ (+ A2·B2ᵀ) [+ R]; out_f32 selects fp32 C (accumulate adds to C).
  * cfg: -1 tile by shape, 0/1/2 force 256/128/64-wide tiles, -2 split K over
- * the grid as the cycle does when the problem has too few 256-wide tiles. */
+ * the grid as the cycle does when the problem has too few 256-wide tiles,
+ * -3 split K over the tiles of a partly filled last round of the device's
+ * compute units, as the cycle does (plain launch when there is no such tail). */
 int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
                 int64_t lda2, const void* B2, int64_t ldb2, int M, int N, int K1, int K2,
                 void* C, int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr,

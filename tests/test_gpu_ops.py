@@ -65,6 +65,37 @@ def test_gemm_nt(cfg, M, N, K, K2):
     assert max_rel(acc, ref + A.float() @ B.float().t()) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K,K2", [(4352, 4104, 2048, 0), (4400, 3840, 2048, 64)])
+def test_gemm_nt_tail_split(M, N, K, K2):
+    """cfg -3: the tiles past the last full round of the CUs (289 tiles: 33
+    of them; 270 tiles: 14, with a ragged last row block and the LoRA K
+    segment in the second slice) split K in two and reduce their tile
+    partials, as the cycle does for products whose tiles leave a partly
+    filled last round."""
+    from deltaserve_amd import ops
+    A = _bf(_rnd(M, K, seed=11))
+    B = _bf(_rnd(N, K, seed=12))
+    A2 = _bf(_rnd(M, K2, seed=13)) if K2 else None
+    B2 = _bf(_rnd(N, K2, seed=14)) if K2 else None
+    ref = A.float() @ B.float().t()
+    if K2:
+        ref += A2.float() @ B2.float().t()
+    dA, dB = A.to(DEV), B.to(DEV)
+    dA2 = None if A2 is None else A2.to(DEV)
+    dB2 = None if B2 is None else B2.to(DEV)
+    c32 = ops.gemm_nt(dA, dB, dA2, dB2, out_dtype=torch.float32, cfg=-3)
+    assert max_rel(c32, ref) < 1e-5
+    # the plain launch gives the same product
+    c32p = ops.gemm_nt(dA, dB, dA2, dB2, out_dtype=torch.float32, cfg=0)
+    assert max_rel(c32, c32p.cpu()) < 1e-5
+    R = _bf(_rnd(M, N, seed=15))
+    c16 = ops.gemm_nt(dA, dB, dA2, dB2, R=R.to(DEV), cfg=-3)
+    assert max_rel(c16, ref + R.float()) < 8e-3
+    acc = c32.clone()
+    ops.gemm_nt(dA, dB, out_dtype=torch.float32, out=acc, accumulate=True, cfg=-3)
+    assert max_rel(acc, ref + A.float() @ B.float().t()) < 1e-5
+
+
 def test_gemm_strided_views():
     """Row strides and column offsets (the fused qkv / gate_up slices)."""
     from deltaserve_amd import ops
