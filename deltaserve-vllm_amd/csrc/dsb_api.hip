@@ -837,7 +837,7 @@ HeadArgs head_args(dsb_handle* h) {
   ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
   ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
   ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH; ha.gemm_cfg = h->gemm_cfg;
-  ha.part = h->part; ha.part_elems = h->part_elems;
+  ha.part = h->part; ha.part_elems = h->part_elems; ha.ncu = h->ncu;
   return ha;
 }
 
@@ -905,8 +905,11 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     {
       const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(N, D);
       const bool split = head_dh_split(ha, c0) > 1;
-      KScope ks(h, st, std::string(split ? "gemm256sk" : cfg_name(cfg)) + "_f32", 2.0 * Vc * D, 0,
-                0, 2.0 * Vc + 8.0 * D, 0, 2.0 * Vc * D);
+      int tail = 0;
+      const bool tsplit = head_dh_tail(ha, c0, &tail) > 1;
+      KScope ks(h, st,
+                std::string(split ? "gemm256sk" : tsplit ? "gemm256t" : cfg_name(cfg)) + "_f32",
+                2.0 * Vc * D, 0, 0, 2.0 * Vc + 8.0 * D, 0, 2.0 * Vc * D);
       LK(head_chunk_dh(ha, c0, st));
     }
     if (c == C - 1) {

@@ -225,6 +225,14 @@ int head_dh_split(const HeadArgs& a, int c0) {
   return ks > 1 && (long)ks * a.n * a.D <= a.part_elems ? ks : 1;
 }
 
+int head_dh_tail(const HeadArgs& a, int c0, int* tail) {
+  *tail = 0;
+  if (a.gemm_cfg >= 0 || !a.part || head_dh_split(a, c0) > 1) return 1;
+  const int Nc8 = (min(a.vchunk, a.V - c0) + 7) / 8 * 8;
+  const int kt = gemm_tail_split(a.n, a.D, Nc8, a.ncu, tail);
+  return kt > 1 && (long)kt * *tail * 65536 <= a.part_elems ? kt : 1;
+}
+
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
   const int Nc8 = (min(a.vchunk, a.V - c0) + 7) / 8 * 8;
   GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, a.ldwt, nullptr, 0, nullptr, 0,
@@ -235,6 +243,9 @@ hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
     q.part = a.part;
     return launch_gemm_split(q, ef, ks, s);
   }
+  int tail = 0;
+  const int kt = head_dh_tail(a, c0, &tail);
+  if (kt > 1) return launch_gemm_tail(q, ef, kt, tail, a.part, s);
   return launch_gemm(q, ef, s, a.gemm_cfg);
 }
 

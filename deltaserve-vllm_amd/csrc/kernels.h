@@ -155,6 +155,7 @@ struct HeadArgs {
   int gemm_cfg;                   // tile of the dH product (-1: by shape)
   float* part = nullptr;          // split-K partials for the dH product (null: no split)
   long part_elems = 0;
+  int ncu = 0;                    // compute units (tail split of the dH product; 0: none)
 };
 // Chunk c0 (a multiple of vchunk) of pass 1 / pass 2; head_reduce between the passes.
 int head_num_chunks(const HeadArgs& a);
@@ -163,8 +164,10 @@ hipError_t head_stats(const HeadArgs& a, int c0, hipStream_t s);
 hipError_t head_reduce(const HeadArgs& a, hipStream_t s);
 hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s);
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s);
-// K splits head_chunk_dh uses for chunk c0 (1: none)
+// K splits head_chunk_dh uses for chunk c0 (1: none), over the whole product
+// or (head_dh_tail) over the tiles of its partly filled last round
 int head_dh_split(const HeadArgs& a, int c0);
+int head_dh_tail(const HeadArgs& a, int c0, int* tail);
 
 // ---- optim.hip
 struct OptTensor {
