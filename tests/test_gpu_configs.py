@@ -64,6 +64,20 @@ def test_config_layer_and_head(name):
     assert worst["graph"]
 
 
+def test_c4_spare_capacity_tail_split():
+    """C4 widths with s_max = 9900 > n = 8192: the products' grids are sized
+    for 39 row blocks, so qkv (1092 tiles) and o, gctx, gxn1, gxn2 and the
+    head's dH (780 tiles each) leave partly filled last rounds that split K,
+    while row blocks past the live rows exit early and the tail reduction
+    skips them."""
+    meta, lens = config_meta("c4", L=1, s_max=None)
+    meta["max_saved_finetuning_tokens"] = 9900
+    worst = cycle_parity(meta, lens, w_std=0.02, b_std=0.01, norm_jitter=0.0,
+                         ref_device="cuda")
+    _report("c4 spare capacity", worst)
+    assert_north_star(worst, direct_masters=False)
+
+
 def test_c3_saved_gate_up():
     """C3 widths with the mlp_gate_up save point bound: the cycle takes gate
     and up from the store instead of recomputing them (llama3.py:63-72)."""
