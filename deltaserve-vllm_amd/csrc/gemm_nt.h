@@ -804,6 +804,11 @@ inline GemmCfg pick_gemm_cfg(int M, int N) {
   if (N <= 64) return GEMM_SKINNY;
   const long big_tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
   if (big_tiles >= 192) return GEMM_BIG;
+  // One 256-row block (a serving-size cycle): the product streams its
+  // weights, and 128-wide tiles only fetch each weight panel twice (once per
+  // 128-row half); from 64 tiles up the 256-wide tile streams faster (M = 256,
+  // K = 5120: N = 17408 97 µs against 120, N = 34816 140 against 227).
+  if (M <= 256 && big_tiles >= 64) return GEMM_BIG;
   return GEMM_MID;
 }
 

@@ -25,6 +25,11 @@ CONFIGS = {
     "c4": dict(name="qwen3-14b", family="qwen3", L=40, D=5120, Hq=40, Hkv=8, I=17408,
                V=151936, r=32, alpha=64, theta=1e6, eps=1e-6, nseq=8, lo=512, hi=2048, total=8192,
                tie=False, rope_scaling=None),
+    # the reference's Qwen3-14B serving preset: 256 fine-tuning tokens per
+    # backward cycle (max_saved_finetuning_tokens), LoRA rank 16
+    "c4s": dict(name="qwen3-14b-serving", family="qwen3", L=40, D=5120, Hq=40, Hkv=8, I=17408,
+                V=151936, r=16, alpha=32, theta=1e6, eps=1e-6, nseq=2, lo=64, hi=192, total=256,
+                tie=False, rope_scaling=None),
     "c5": dict(name="llama3-8b-long", family="llama3", L=32, D=4096, Hq=32, Hkv=8, I=14336,
                V=128256, r=64, alpha=128, theta=5e5, eps=1e-5, nseq=2, lo=8192, hi=8192,
                total=16384, tie=False,
