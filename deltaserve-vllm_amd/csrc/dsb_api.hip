@@ -1053,10 +1053,18 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
            grad_b(h, ls, DSB_PROJ_GATE), h->s, 1},
           {h->Ggu + I, 2L * I, I, h->Zgu_b + r, 2L * r, ls.BTu, h->gZgu_b + r, 2L * r,
            grad_b(h, ls, DSB_PROJ_UP), h->s, 1}};
-      // two launches: 2 × 28 column blocks at C3 would leave a 256-CU grid
-      // with 224 blocks (one split fewer per pass), one pass keeps 28 × 9
-      dual_g = dual(h, &d[0], 1, r, st);
-      dual_u = dual(h, &d[1], 1, r, st);
+      // Two launches when each fills more of the CUs than one launch of
+      // both would (C3: one pass gives 28 column blocks × 9 token splits,
+      // both together 56 × 4); one launch when the token count caps the
+      // splits anyway (256-token cycles: 34 × 4 per pass, 68 × 3 together)
+      const int Cg[2] = {I, I};
+      const int ns1 = dual_splits(h, Cg, 1, r), ns2 = dual_splits(h, Cg, 2, r);
+      if (ns1 > 0 && ns2 > 0 && 2 * ns2 >= ns1) {
+        dual_g = dual_u = dual(h, d, 2, r, st);
+      } else {
+        dual_g = dual(h, &d[0], 1, r, st);
+        dual_u = dual(h, &d[1], 1, r, st);
+      }
       if (dual_g < 0 || dual_u < 0) return -1;
       if (dual_g) CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
       if (dual_u) CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
