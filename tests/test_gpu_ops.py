@@ -107,10 +107,13 @@ def test_gemm_strided_views():
 
 
 @pytest.mark.parametrize("M,I,K,K2", [(700, 512, 256, 16), (8192, 1536, 512, 32),
-                                      (333, 192, 128, 0), (64, 128, 1024, 48)])
+                                      (333, 192, 128, 0), (64, 128, 1024, 48),
+                                      (200, 8192, 256, 16)])
 def test_gemm_glu(M, I, K, K2):
-    """Gate‖up with the SwiGLU forward in the epilogue (256- and 128-wide tiles):
-    GU against an fp32 product, H exactly silu(gate)·up of the returned halves."""
+    """Gate‖up with the SwiGLU forward in the epilogue (256- and 128-wide tiles;
+    the last shape is one row block with 64 column tiles, which takes the
+    256-wide tile as serving-size cycles do): GU against an fp32 product, H
+    exactly silu(gate)·up of the returned halves."""
     from deltaserve_amd import ops
     A = _bf(_rnd(M, K, seed=21))
     B = _bf(_rnd(2 * I, K, seed=22))
