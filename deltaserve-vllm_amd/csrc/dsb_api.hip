@@ -708,6 +708,10 @@ int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hip
 int skinny(dsb_handle* h, const bf16* X, long ldx, const bf16* B, int R, int K, bf16* Z,
            long ldz, hipStream_t s) {
   SkinnyArgs a{X, ldx, B, (long)K, R, K, Z, ldz, h->N, &h->d_hdr->n};
+  // K-split partials (short token ranges) in the TN workspace, which holds
+  // nothing between the launches that use it
+  a.part = h->tn_work;
+  a.part_elems = h->tn_work_elems;
   KScope ks(h, s, "lora_skinny", 2.0 * R * K, 0, 0, 2.0 * K + 2.0 * R, 0, 2.0 * R * K);
   LK(lora_skinny(a, s));
   return 0;
@@ -2069,6 +2073,14 @@ int dsb_op_lora_skinny(const void* X, int64_t ldx, const void* B, int64_t ldb, i
   if (K % 8 || ldx % 8 || ldb % 8) return fail(nullptr, "dsb_op_lora_skinny: K, ldx, ldb must be multiples of 8");
   hipStream_t s = (hipStream_t)stream;
   SkinnyArgs a{(const bf16*)X, ldx, (const bf16*)B, ldb, R, K, (bf16*)Z, ldz, n, nullptr};
+  // the K split the cycle takes for short token ranges, partials in a buffer
+  // allocated for the call
+  TmpDev tmp;
+  a.part_elems = 8L * n * R;
+  if (lora_skinny_split(a) > 1) {
+    a.part = tmp.alloc<float>((size_t)a.part_elems);
+    if (!a.part) return fail(nullptr, "dsb_op_lora_skinny: hipMalloc failed");
+  }
   OPCK(lora_skinny(a, s));
   OPCK(hipStreamSynchronize(s));
   return 0;

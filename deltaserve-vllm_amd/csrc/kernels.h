@@ -80,7 +80,14 @@ struct SkinnyArgs {
   int R, K;
   bf16* Z; long ldz;
   int n; const int* n_dev;
+  // fp32 workspace of part_elems floats for a K split (null: no split)
+  float* part = nullptr;
+  long part_elems = 0;
 };
+// K slices for a (1: none): short token ranges whose blocks would leave most
+// CUs idle split K when part_elems holds slices · n · R partials; lora_skinny
+// takes the split when a.part is set
+int lora_skinny_split(const SkinnyArgs& a);
 hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s);
 // out[j, c] (or out[c, j] when transposed) = scale · sum_t P[t, j] * X[t, c],
 // t < n. Output rows j are split into groups of `rg` written to outs[j / rg].

@@ -54,7 +54,9 @@ hipError_t lora_cast(const CastJob* jobs_dev, const int2* chunks_dev, int nchunk
 // stream through a direct-to-LDS ring of up to 96 KB (up to 8 stages; one
 // barrier per chunk); wave w multiplies columns 32w .. 32w+31 of each chunk
 // with 16×16×32 MFMAs (TT token tiles × RB rank tiles) and the four waves'
-// partial sums are added through LDS at the end.
+// partial sums are added through LDS at the end. With a K split (grid.z > 1)
+// block z takes the z-th run of 128-column chunks and stores its fp32 sums
+// to a.part[z][t][j]; lora_skinny_reduce_kernel adds the slices in order.
 template <int TT, int RB>
 __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   constexpr int TR = 16 * TT;  // tokens per block
@@ -69,6 +71,10 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   const int rows = min(N - t0, TR);
   const bf16* X0 = a.X + (long)t0 * a.ldx;
   const int nc = (a.K + 127) / 128;
+  // this block's chunks [cb, ce) (all of them unless K is split over grid.z)
+  const int nz = (int)gridDim.z;
+  const int cpk = nz == 1 ? nc : (nc + nz - 1) / nz;
+  const int cb = min(nc, (int)blockIdx.z * cpk), ce = min(nc, cb + cpk);
   // ranks j0 .. j0 + Rg - 1 of this block (groups of 64 on grid.y)
   const int j0 = blockIdx.y * 64, Rg = min(a.R - j0, 64);
   const bf16* Bg = a.B + (long)j0 * a.ldb;
@@ -86,7 +92,7 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   const unsigned lds0 = lds_addr(smem);
   auto issue = [&](int c, int slot) {
     const int k0 = c * 128;
-    const bool kin = k0 < a.K;          // uniform
+    const bool kin = c < ce;            // uniform (ce <= nc: the chunk starts inside K)
     const bool cin = k0 + lcol < a.K;   // the lane's chunk
     const unsigned d = lds0 + (unsigned)(slot * SE * 2);
 #pragma unroll
@@ -114,12 +120,13 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
   const int off = toff(fr, fc) * 2;  // tiles start at multiples of 16 rows: f(r) = f(l%16)
 
 #pragma unroll
-  for (int c = 0; c < NS - 1; ++c) issue(c, c);
-  for (int c = 0; c < nc; ++c) {
+  for (int c = 0; c < NS - 1; ++c) issue(cb + c, c);
+  for (int c = cb; c < ce; ++c) {
+    const int i = c - cb;        // ring position
     wait_vm<(NS - 2) * LPS>();  // own loads of chunk c landed (c+1 .. c+NS-2 may fly)
     lds_barrier();               // chunk c visible; the slot of chunk c-1 is free
-    issue(c + NS - 1, (c + NS - 1) % NS);
-    const char* st = reinterpret_cast<const char*>(smem + (c % NS) * SE);
+    issue(c + NS - 1, (i + NS - 1) % NS);
+    const char* st = reinterpret_cast<const char*>(smem + (i % NS) * SE);
     bf16x8 xf[TT], bfr[RB];
 #pragma unroll
     for (int i = 0; i < TT; ++i) xf[i] = *reinterpret_cast<const bf16x8*>(st + off + i * 16 * 256);
@@ -148,13 +155,29 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(SkinnyArgs a) {
     if (tt >= rows || jj >= Rg) continue;
     const float v = red[tt * RP + jj] + red[(TR + tt) * RP + jj] + red[(2 * TR + tt) * RP + jj] +
                     red[(3 * TR + tt) * RP + jj];
-    a.Z[(long)(t0 + tt) * a.ldz + j0 + jj] = (bf16)v;
+    if (a.part)
+      a.part[((long)blockIdx.z * a.n + t0 + tt) * a.R + j0 + jj] = v;
+    else
+      a.Z[(long)(t0 + tt) * a.ldz + j0 + jj] = (bf16)v;
   }
 }
 
+// Z[t, j] = bf16(sum over the K slices z, in order, of part[z][t][j]), live rows.
+__global__ __launch_bounds__(256) void lora_skinny_reduce_kernel(SkinnyArgs a, int ks) {
+  int N = a.n;
+  if (a.n_dev) N = min(N, *a.n_dev);
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)N * a.R) return;
+  const int t = (int)(idx / a.R), j = (int)(idx % a.R);
+  const long plane = (long)a.n * a.R;
+  float v = 0.f;
+  for (int z = 0; z < ks; ++z) v += a.part[z * plane + idx];
+  a.Z[(long)t * a.ldz + j] = (bf16)v;
+}
+
 template <int TT>
-static hipError_t launch_skinny(const SkinnyArgs& a, hipStream_t s) {
-  const dim3 grid((a.n + 16 * TT - 1) / (16 * TT), (a.R + 63) / 64);
+static hipError_t launch_skinny(const SkinnyArgs& a, int ks, hipStream_t s) {
+  const dim3 grid((a.n + 16 * TT - 1) / (16 * TT), (a.R + 63) / 64, ks);
   switch ((std::min(a.R, 64) + 15) / 16) {
     case 1: hipLaunchKernelGGL((lora_skinny_kernel<TT, 1>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((lora_skinny_kernel<TT, 2>), grid, dim3(256), 0, s, a); break;
@@ -165,12 +188,36 @@ static hipError_t launch_skinny(const SkinnyArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+static int skinny_tt(const SkinnyArgs& a) { return a.K <= 8192 && a.R <= 16 ? 1 : 2; }
+
+int lora_skinny_split(const SkinnyArgs& a) {
+  if (a.part_elems <= 0 || a.R <= 0 || a.n <= 0) return 1;
+  const int tr = 16 * skinny_tt(a);
+  const long blocks = (long)((a.n + tr - 1) / tr) * ((a.R + 63) / 64);
+  const int nc = (a.K + 127) / 128;
+  // only long rows gain: with fewer than 32 chunks (4096 columns) per block
+  // the second launch costs more than the slices save (C1: 2.5 → 3.3 ms per
+  // cycle); then about one round of the 256 CUs, at least 8 chunks per slice
+  if (blocks >= 128 || nc < 32) return 1;
+  int ks = std::min((int)(256 / blocks), std::min(8, nc / 8));
+  while (ks > 1 && (long)ks * a.n * a.R > a.part_elems) --ks;
+  return ks >= 2 ? ks : 1;
+}
+
 hipError_t lora_skinny(const SkinnyArgs& a, hipStream_t s) {
   if (a.R <= 0 || a.n <= 0) return hipSuccess;
   // short rows at one rank group of 16: 16-token blocks (twice the blocks, two
   // per CU); wider rank groups keep 32 tokens so the B chunk is shared by two
   // token tiles
-  return a.K <= 8192 && a.R <= 16 ? launch_skinny<1>(a, s) : launch_skinny<2>(a, s);
+  const int ks = a.part ? lora_skinny_split(a) : 1;
+  SkinnyArgs b = a;
+  if (ks == 1) b.part = nullptr;
+  hipError_t e = skinny_tt(a) == 1 ? launch_skinny<1>(b, ks, s) : launch_skinny<2>(b, ks, s);
+  if (e != hipSuccess || ks == 1) return e;
+  const long tot = (long)a.n * a.R;
+  hipLaunchKernelGGL(lora_skinny_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256),
+                     0, s, b, ks);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ TN

@@ -276,8 +276,12 @@ def test_lora_tn(n, R, C):
     assert max_rel(outT, 2.0 * ref.t()) < 1e-5
 
 
-@pytest.mark.parametrize("n,R,K", [(333, 24, 520), (8192, 48, 4096), (100, 16, 14336), (5, 64, 64)])
+@pytest.mark.parametrize("n,R,K", [(333, 24, 520), (8192, 48, 4096), (100, 16, 14336), (5, 64, 64),
+                                   (256, 48, 5120), (504, 16, 4096), (77, 32, 4200)])
 def test_lora_skinny(n, R, K):
+    """Z = X·Bᵀ; short token ranges over long rows (100, 256, 504 and 77 rows)
+    split K into 8, 5, 4 and 4 slices (the last with a partial 128-column
+    chunk) and add the fp32 slices in a second launch, as the cycle does."""
     from deltaserve_amd import ops
     X = _bf(_rnd(n, K, seed=53)).to(DEV)
     B = _bf(_rnd(R, K, seed=54)).to(DEV)
