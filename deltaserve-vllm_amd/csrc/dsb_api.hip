@@ -237,7 +237,7 @@ struct GraphSet {  // the cycle's graphs for one attention grid capacity
 
 struct dsb_handle {
   dsb_desc d{};
-  int D, Hq, Hkv, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk, nvc;
+  int D, Hq, Hkv, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk, nvc, ce_bn;
   int gemm_cfg = -1;  // forced dense-product tile (GEMM_*), -1 by shape
   int tile_cap = 0;   // attention grid capacity of the current cycle
   float s;
@@ -837,7 +837,7 @@ HeadArgs head_args(dsb_handle* h) {
   ha.normed = h->normed; ha.ldh = h->D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.ldwt = h->ldwt;
   ha.labels = h->labels;
   ha.n = h->N; ha.n_dev = &h->d_hdr->n; ha.D = h->D; ha.V = h->V; ha.stats = h->stats;
-  ha.ntn = h->ntn;
+  ha.ntn = h->ntn; ha.ce_bn = h->ce_bn;
   ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
   ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
   ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH; ha.gemm_cfg = h->gemm_cfg;
@@ -889,7 +889,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     if (seg < C) {
       {
         // 2·n·Vc·D of the head's algorithmic 4·M·D·V (the logits product)
-        KScope ks(h, st, "gemm256_ce_stats", 2.0 * Vc * D, 0, 0, 2.0 * D + 8.0 * Vc / 256.0, 0,
+        KScope ks(h, st, h->ce_bn == 128 ? "gemm256x128_ce_stats" : "gemm256_ce_stats",
+                  2.0 * Vc * D, 0, 0, 2.0 * D + 8.0 * Vc / h->ce_bn, 0,
                   2.0 * Vc * D);
         LK(head_stats(ha, c0, st));
       }
@@ -902,7 +903,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     {
       // the logits of the chunk again (not algorithmic work: the price of
       // not keeping them), with the dlogits in the epilogue
-      KScope ks(h, st, "gemm256_ce_grad", 2.0 * Vc * D, 0, 0, 2.0 * D + 2.0 * Vc, 0,
+      KScope ks(h, st, h->ce_bn == 128 ? "gemm256x128_ce_grad" : "gemm256_ce_grad",
+                2.0 * Vc * D, 0, 0, 2.0 * D + 2.0 * Vc, 0,
                 2.0 * Vc * D);
       LK(head_chunk_grad(ha, c0, st));
     }
@@ -1407,11 +1409,15 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
   h->I = d->intermediate; h->V = d->vocab; h->r = d->lora_rank; h->L = d->n_layers;
   h->N = d->s_max; h->s = d->lora_scaling; h->qwen = d->family == DSB_FAMILY_QWEN3;
   h->max_tiles = max_tiles_for(d->s_max, std::min(d->max_seqs, d->s_max));
-  h->ntn = (h->V + 255) / 256;
   // LM-head vocab chunk: one pause point per chunk in each pass, and the
   // width of the bf16 dlogits tile (16384 columns: 268 MB at 8192 rows)
   h->vchunk = d->vocab_chunk > 0 ? d->vocab_chunk : 16384;
   h->vchunk = (int)std::min<long>(h->vchunk, ((long)h->V + 255) / 256 * 256);
+  // CE passes: 128-wide vocab tiles when 256-wide ones would leave a chunk's
+  // launch with under 192 tiles (short cycles: 256 tokens give 64), so the
+  // launch streams the head's weights over twice the CUs
+  h->ce_bn = (long)((h->N + 255) / 256) * (h->vchunk / 256) < 192 ? 128 : 256;
+  h->ntn = (h->V + h->ce_bn - 1) / h->ce_bn;
   h->nvc = (h->V + h->vchunk - 1) / h->vchunk;
   h->gemm_cfg = d->gemm_tile == 256 ? GEMM_BIG
               : d->gemm_tile == 128 ? GEMM_MID

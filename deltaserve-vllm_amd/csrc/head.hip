@@ -197,6 +197,7 @@ hipError_t head_stats(const HeadArgs& a, int c0, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const int Vc = min(a.vchunk, a.V - c0);
   EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, c0, Vc};
+  if (a.ce_bn == 128) return launch_gemm_cfg<256, 128, 2, 2>(chunk_logits_problem(a, c0), epi, s);
   return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
 
@@ -215,6 +216,7 @@ hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const int Vc = min(a.vchunk, a.V - c0), Nc8 = (Vc + 7) / 8 * 8;
   EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Vc, Nc8};
+  if (a.ce_bn == 128) return launch_gemm_cfg<256, 128, 2, 2>(chunk_logits_problem(a, c0), epi, s);
   return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
 

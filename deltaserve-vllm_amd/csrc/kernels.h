@@ -150,7 +150,8 @@ struct HeadArgs {
   int n; const int* n_dev;
   int D, V;
   float2* stats;                  // [n_cap, ntn]
-  int ntn;                        // ceil(V / 256)
+  int ntn;                        // ceil(V / ce_bn)
+  int ce_bn = 256;                // vocab tile width of the CE passes (256 or 128)
   float* tgt_logit;               // [n_cap]
   float* lse;                     // [n_cap]
   float* loss_row;                // [n_cap]
