@@ -534,16 +534,20 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   const float sl2 = kScale * kLog2e;
   const FragOffs fo(lane);
 
-  // (head, q tile) pairs flattened into one pipelined sequence
+  // (head, q tile) pairs flattened into one pipelined sequence; with a head
+  // split (grid.z > 1) this block takes q-heads h_lo .. h_lo + hc - 1 of the
+  // group and stores fp32 partial sums (dkdv_head_sum_kernel adds them)
+  const int hs = (int)gridDim.z, gph = (G + hs - 1) / hs;
+  const int h_lo = min(G, (int)blockIdx.z * gph), hc = min(G, h_lo + gph) - h_lo;
   const int qt0 = k0 / TR;                 // first q tile that can see these keys
   const int nq = (L + TR - 1) / TR - qt0;  // q tiles per head
-  const int nit = G * nq;
+  const int nit = hc * nq;
   // lse/dsum rows of pair `it` (threads < 64): loaded into registers one pair
   // ahead and stored to LDS at the end of the previous pair, so the compiler's
   // wait on these loads never drains the tile loads issued before them.
   float nl = 0.f, nd = 0.f;
   auto load_ld = [&](int it) {
-    const int hq = kvh * G + it / nq;
+    const int hq = kvh * G + h_lo + it / nq;
     const int q0 = (qt0 + it % nq) * TR;
     const bool ok = tid < TR && q0 + tid < L;
     nl = ok ? a.lse[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
@@ -552,7 +556,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   const SeqTiles tq(a.q, a.ldq, st, L, w, lane), to(a.dout, a.lddo, st, L, w, lane);
   const unsigned lds0 = lds_addr(smem);
   auto stage = [&](int it, int sidx) {
-    const int hq = kvh * G + it / nq;
+    const int hq = kvh * G + h_lo + it / nq;
     const int q0 = (qt0 + it % nq) * TR;
     const unsigned d = lds0 + (unsigned)(sidx * 2 * TILE * 2);
     tq.load(q0, hq * HD, d, w);
@@ -738,6 +742,25 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   // the last accumulating MFMAs (inline asm, unseen by the compiler's hazard
   // checks) complete before their AGPRs are read
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  if (hs > 1) {
+    // fp32 partials: kv_part[z][row][m·KV + kvh·128 + dim], m = 0 dK, 1 dV;
+    // the lane holds key row `key`, dims d4·32 + 8g + 4·lh .. +3
+    if (kok) {
+      const long KV = (long)a.Hkv * HD;
+      float* pr = a.kv_part + ((long)blockIdx.z * a.n + st + key) * 2 * KV + kvh * HD + 4 * lh;
+#pragma unroll
+      for (int d4 = 0; d4 < 4; ++d4)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 k4 = {dk[d4][4 * g] * kScale, dk[d4][4 * g + 1] * kScale,
+                            dk[d4][4 * g + 2] * kScale, dk[d4][4 * g + 3] * kScale};
+          const f32x4 v4 = {dv[d4][4 * g], dv[d4][4 * g + 1], dv[d4][4 * g + 2], dv[d4][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(pr + d4 * 32 + 8 * g) = k4;
+          *reinterpret_cast<f32x4*>(pr + KV + d4 * 32 + 8 * g) = v4;
+        }
+    }
+    return;
+  }
   // dK and dV as whole rows through the stages, which every wave is done
   // reading
   __syncthreads();
@@ -749,6 +772,26 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   }
 }
 
+// dK, dV = bf16(sum over the head split's slices z, in order, of the fp32
+// partials), four columns per thread, live rows only.
+__global__ __launch_bounds__(256) void dkdv_head_sum_kernel(AttnArgs a, int hs) {
+  int N = a.n;
+  if (a.n_dev) N = min(N, *a.n_dev);
+  const long KV = (long)a.Hkv * HD, c4 = 2 * KV / 4;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)N * c4) return;
+  const long row = idx / c4, col = (idx % c4) * 4;
+  const float* src = a.kv_part + row * 2 * KV + col;
+  const long plane = (long)a.n * 2 * KV;
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < hs; ++z) v += *reinterpret_cast<const f32x4*>(src + z * plane);
+  bf16x4 b;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = (bf16)v[i];
+  bf16* dst = col < KV ? a.dk + row * a.lddk + col : a.dv + row * a.lddv + (col - KV);
+  *reinterpret_cast<bf16x4*>(dst) = b;
+}
+
 hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
   if (a.max_tiles <= 0) return hipSuccess;
   hipLaunchKernelGGL(attn_fwd_kernel, dim3(a.max_tiles * (a.Hq / a.Hkv), a.Hkv), dim3(256), 0, s,
@@ -756,9 +799,23 @@ hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+int attn_dkdv_head_split(const AttnArgs& a) {
+  const int G = a.Hkv > 0 ? a.Hq / a.Hkv : 1;
+  if (G < 2 || a.n <= 0 || a.n > 1024) return 1;
+  return (long)G * a.n * 2 * a.Hkv * HD <= a.kv_part_elems ? G : 1;
+}
+
 hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
   if (a.max_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_dkdv_kernel, dim3(a.max_tiles, a.Hkv), dim3(256), 0, s, a);
+  // Short cycles (at most 1024 tokens) give the pass a block per key tile
+  // and kv head, far fewer than the CUs; each block then takes one q-head
+  // of its group and a second launch adds the heads' fp32 partials in order.
+  const int hs = a.kv_part ? attn_dkdv_head_split(a) : 1;
+  hipLaunchKernelGGL(attn_dkdv_kernel, dim3(a.max_tiles, a.Hkv, hs), dim3(256), 0, s, a);
+  if (hs == 1) return hipGetLastError();
+  const long tot = (long)a.n * (2L * a.Hkv * HD / 4);
+  hipLaunchKernelGGL(dkdv_head_sum_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
+                     a, hs);
   return hipGetLastError();
 }
 

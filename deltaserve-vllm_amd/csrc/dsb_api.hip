@@ -947,6 +947,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     at.tiles = h->d_tiles; at.tiles_k = h->d_tiles_k; at.ntiles_dev = &h->d_hdr->ntiles;
     at.max_tiles = h->tile_cap;
     at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
+    // dK/dV head-split partials (short cycles) in the TN workspace, which
+    // holds nothing while the attention passes run
+    at.kv_part = h->tn_work; at.kv_part_elems = h->tn_work_elems;
     // one causal attention matmul = Hq·Hd·S flops (S = sum L(L+1), unmasked pairs ×2)
     const double au = Hq * 128.0;
     const double arow = 2.0 * (q + 2.0 * kv);
@@ -2001,6 +2004,13 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
   a.lse = (float*)lse; a.dsum = dsum; a.ld_stat = n; a.dout = (const bf16*)dout; a.lddo = lddo;
   a.dq = (bf16*)dq; a.lddq = lddq; a.dk = (bf16*)dk; a.lddk = lddk; a.dv = (bf16*)dv;
   a.lddv = lddv; a.Hq = Hq; a.Hkv = Hkv;
+  // the dK/dV head split the cycle takes for short token counts, partials in
+  // a buffer allocated for the call
+  a.kv_part_elems = (long)(Hq / Hkv) * n * 2 * Hkv * 128;
+  if (attn_dkdv_head_split(a) > 1) {
+    a.kv_part = tmp.alloc<float>((size_t)a.kv_part_elems);
+    if (!a.kv_part) return fail(nullptr, "attn: hipMalloc failed");
+  }
   OPCK(attn_bwd(a, s));
   OPCK(hipStreamSynchronize(s));
   return 0;

@@ -53,12 +53,19 @@ struct AttnArgs {
   const int* ntiles_dev;
   int max_tiles;
   int Hq, Hkv;
-  const int* n_dev;  // live token count (unused by the attention kernels)
+  const int* n_dev;  // live token count (the dK/dV head-split sum reads it)
   int n;
+  // fp32 workspace for the dK/dV pass's head split (null: none), at least
+  // (Hq / Hkv) · n · 2 · Hkv·128 floats when the split applies
+  float* kv_part = nullptr;
+  long kv_part_elems = 0;
 };
 hipError_t attn_fwd(const AttnArgs& a, hipStream_t s);
 hipError_t attn_bwd(const AttnArgs& a, hipStream_t s);
 hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s);
+// q-head slices the dK/dV pass splits into (1: none) when kv_part_elems
+// holds the partials; attn_bwd_dkdv takes the split when kv_part is set
+int attn_dkdv_head_split(const AttnArgs& a);
 hipError_t attn_bwd_dq(const AttnArgs& a, hipStream_t s);
 
 // ---- lora.hip
