@@ -678,7 +678,8 @@ int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hip
     // too few 256×256 tiles for the chip: split K (unless a tile is forced)
     const int ksplit = h->gemm_cfg >= 0 ? 1 : gemm_split_count(p.M, p.N, p.K1 + p.K2);
     if (ksplit > 1 && (long)ksplit * p.M * p.N <= h->part_elems) {
-      KScope ks(h, st, std::string("gemm256sk_") + epi, 2.0 * p.N * K, 0, 0,
+      const bool t128 = gemm_split_tile(p.M, p.N, p.K1 + p.K2) == 128;
+      KScope ks(h, st, std::string(t128 ? "gemm128sk_" : "gemm256sk_") + epi, 2.0 * p.N * K, 0, 0,
                 2.0 * K + ob * p.N + xrow, 0, 2.0 * p.N * K);
       GemmProblem q = p;
       q.part = h->part;

@@ -838,8 +838,17 @@ hipError_t launch_gemm(const GemmProblem& p, const Epi& e, hipStream_t s, int cf
 // partly filled round costs more than it spreads), at least 4 K tiles each;
 // 1 when the problem has more than 128 tiles (the fp32 partials' traffic
 // would buy no more parallelism).
+// The split's tile: 128 × 128 for one 256-row block over K ≤ 8192 when those
+// tiles stay within 128 (a serving-size cycle's K = 5120–7168 products: the
+// smaller tiles need fewer K slices to fill the CUs, so less partial traffic;
+// M = 256, N = 5120, K = 5120: 32 µs against 37), else 256 × 256.
+inline int gemm_split_tile(int M, int N, int K) {
+  const long mid = (long)((M + 127) / 128) * ((N + 127) / 128);
+  return M <= 256 && K <= 8192 && mid <= 128 ? 128 : 256;
+}
 inline int gemm_split_count(int M, int N, int K) {
-  const long tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
+  const int t = gemm_split_tile(M, N, K);
+  const long tiles = (long)((M + t - 1) / t) * ((N + t - 1) / t);
   const int nk = (K + 63) / 64;
   if (tiles > 128 || N % 8 != 0 || nk < 8) return 1;
   const int ks = std::min((int)(256 / tiles), std::min(8, nk / 4));
@@ -848,11 +857,17 @@ inline int gemm_split_count(int M, int N, int K) {
 template <class Epi>
 hipError_t launch_gemm_split(const GemmProblem& p, const Epi& e, int ks, hipStream_t s) {
   static_assert(SplitPart<Epi>::enabled, "split-K epilogues");
-  const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
-  if (nbm == 0 || nbn == 0) return hipSuccess;
+  if (p.M <= 0 || p.N <= 0) return hipSuccess;
   if (!p.part || p.N % 8 != 0 || ks < 2) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(nbm * nbn, ks), dim3(256), 0, s,
-                     p, e);
+  if (gemm_split_tile(p.M, p.N, p.K1 + p.K2) == 128) {
+    const int mbm = (p.M + 127) / 128, mbn = (p.N + 127) / 128;
+    hipLaunchKernelGGL((gemm_nt_kernel<128, 128, 2, 2, Epi>), dim3(mbm * mbn, ks), dim3(256), 0,
+                       s, p, e);
+  } else {
+    const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
+    hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(nbm * nbn, ks), dim3(256), 0,
+                       s, p, e);
+  }
   const long n = (long)p.M * (p.N / 8);
   hipLaunchKernelGGL(gemm_split_reduce_kernel<Epi>, dim3((unsigned)((n + 255) / 256)), dim3(256),
                      0, s, p, ks, e);
