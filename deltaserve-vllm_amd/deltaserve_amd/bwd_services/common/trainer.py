@@ -338,6 +338,40 @@ class LoraSftTrainerService(BackwardService):
         rc_end = lib.dsb_step_end(self._h, stream, byref(loss), byref(nv), byref(info))
         return rc if rc != 0 else rc_end
 
+    # ------------------------------------------------------------ capture checks
+    VERIFY_TOL = 5e-2  # relative; bf16 round trips of the capture path stay well inside
+
+    def verify_activations(self, activations: dict, n: int) -> list[tuple[str, float, bool]]:
+        """Debug-gated capture checks (trainer.py:806-826; on with the
+        ``print_hash`` of ``share_activations``): the first layer's saved
+        input must be the embedding rows of the saved ids, and the final
+        norm of ``final_in`` must be the saved ``final_hidden``. Logs each
+        check and returns ``(name, relative error, ok)``."""
+        meta = self.shared.get("meta") or {}
+        base = {k.replace(".base_layer.", "."): v for k, v in (self.shared.get("base") or {}).items()}
+        out = []
+
+        def judge(name, got, want):
+            err = float((got.float() - want.float()).abs().max())
+            rel = err / (float(want.float().abs().max()) + 1e-6)
+            ok = rel < self.VERIFY_TOL
+            dprint(f"[verify] {name}: max|d|={err:.3e} rel={rel:.3e} {'OK' if ok else 'FAIL'}")
+            out.append((name, rel, ok))
+
+        ids = activations["concat_input_ids"][:n].long()
+        layer_in = activations.get("layer_in") or []
+        embed = base.get(meta.get("embed_weight_key") or "model.embed_tokens.weight")
+        if layer_in and embed is not None:
+            judge("layer_in[0] vs embed[ids]", layer_in[0][:n], embed[ids])
+        final_in, final_hidden = activations.get("final_in"), activations.get("final_hidden")
+        norm_w = base.get(meta.get("norm_weight_key") or "model.norm.weight")
+        if final_in is not None and final_hidden is not None and norm_w is not None and n > 0:
+            from deltaserve_amd import ops
+
+            normed = ops.rmsnorm(final_in[:n], norm_w, float(meta.get("rms_norm_eps", 1e-5)))
+            judge("RMSNorm(final_in) vs final_hidden", normed, final_hidden[:n])
+        return out
+
     # ------------------------------------------------------------ checkpoints
     def masters(self):
         """(PEFT key, fp32 master) pairs of the adapter being trained."""
@@ -423,9 +457,7 @@ class LoraSftTrainerService(BackwardService):
             L.check(L.load().dsb_reset_optimizer(self._h, self.weight_decay), self._h,
                     "dsb_reset_optimizer")
         self.current_epoch = 0
-        self._cur_epoch_seen = 0
-        self._epoch_processed_tokens = 0
-        self._total_tokens_per_epoch = int(hparams.get("total_tokens_per_epoch", 0))
+        self.ledger.restart(int(hparams.get("total_tokens_per_epoch", 0)))
         self._publish_to_served()
         dprint(f"[backward] switched to a new adapter: {len(matched)} LoRA tensors, "
                f"lr={self.lr}, wd={self.weight_decay}, gamma={self.gamma}")
