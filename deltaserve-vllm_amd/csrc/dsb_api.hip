@@ -263,7 +263,11 @@ struct dsb_handle {
   bf16 *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
   bf16 *gZd_b, *gZgu_b, *gZo_b, *gZqkv_b;
   bf16 *g0, *g1, *Ggu, *grm, *gctx, *gqkv;
-  bf16 *gxn2, *gxn1;  // the FFN / attention input gradients, bf16 as the reference's cdt
+  // the FFN / attention input gradients, fp32 GEMM outputs: each layer's
+  // increment of the fp32 residual-stream gradient keeps its accumulator
+  // precision into the RMSNorm backward (bf16 here cost 0.5 % per layer of
+  // LoRA-gradient error at 32 layers)
+  float *gxn2, *gxn1;
   // the residual-stream gradient in fp32 (g32[2] alternate by layer like g0 /
   // g1, which hold its bf16 copies for the MFMA and LoRA operands; grm32 the
   // post-attention residual's): rounding it to bf16 at every layer would
@@ -674,7 +678,8 @@ template <class Epi>
 int gemm(dsb_handle* h, const char* epi, const GemmProblem& p, const Epi& e, hipStream_t st,
          double ob, double xrow) {
   const double K = (double)p.K1 + p.K2;
-  if constexpr (std::is_same<Epi, EpiBF16>::value || std::is_same<Epi, EpiSwiGLUBwd>::value) {
+  if constexpr (std::is_same<Epi, EpiBF16>::value || std::is_same<Epi, EpiSwiGLUBwd>::value ||
+                std::is_same<Epi, EpiF32>::value) {
     // too few 256×256 tiles for the chip: split K (unless a tile is forced)
     const int ksplit = h->gemm_cfg >= 0 ? 1 : gemm_split_count(p.M, p.N, p.K1 + p.K2);
     if (ksplit > 1 && (long)ksplit * p.M * p.N <= h->part_elems) {
@@ -1082,8 +1087,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     {
       GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
                     hg ? ls.AguT : nullptr, 2L * r, N, D, 2 * I, hg ? 2 * r : 0, nd};
-      EpiBF16 e{h->gxn2, (long)D, D, nullptr, 0};
-      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
+      EpiF32 e{h->gxn2, (long)D, D, 0};
+      CKR(gemm(h, "dx32", p, e, st, 4.0, 0.0));
     }
     if (hg) {
       float* gAg = grad_a(h, ls, DSB_PROJ_GATE);
@@ -1097,8 +1102,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
                nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 16.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(h->resid, D, h->gxn2, false, D, (const bf16*)ls.w.post_ln, nullptr, D,
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 18.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(h->resid, D, h->gxn2, true, D, (const bf16*)ls.w.post_ln, nullptr, D,
                      h->grm, D, N, nd, D, eps, st, g32, h->grm32));
     }
     int dual_o = 1;
@@ -1152,8 +1157,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     {
       GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
                     hq ? ls.AqkvT : nullptr, 3L * r, N, D, W3, hq ? 3 * r : 0, nd};
-      EpiBF16 e{h->gxn1, (long)D, D, nullptr, 0};
-      CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
+      EpiF32 e{h->gxn1, (long)D, D, 0};
+      CKR(gemm(h, "dx32", p, e, st, 4.0, 0.0));
     }
     if (hq) {
       CKR(tn(h, h->gZqkv_b, 3 * r, h->xn1, D, 3 * r, D, grad_a(h, ls, DSB_PROJ_Q),
@@ -1169,8 +1174,8 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
                nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 16.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(x, ldx, h->gxn1, false, D, (const bf16*)ls.w.in_ln, nullptr, D, gnext, D,
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 18.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(x, ldx, h->gxn1, true, D, (const bf16*)ls.w.in_ln, nullptr, D, gnext, D,
                      N, nd, D, eps, st, h->grm32, gnext32));
     }
     CKR(tn_flush(h, st));

@@ -15,9 +15,9 @@ tests/test_oracle_pins.py cover the same functions.
 
 Bars: loss 1e-3 relative; LoRA grads 2e-2
 max-relative with cosine >= 0.999; n_valid exact; updated masters equal to
-the reference AdamW step of the cycle's own gradients (the direct comparison
-of masters with the fp32 run is reported, see harness.assert_north_star for
-why it is no bar at these widths).
+the reference AdamW step of the cycle's own gradients, and every master
+element further than 2e-2 from the fp32 run's explained by a reference
+gradient within the measured error of zero (harness.unexplained_master_misses).
 """
 
 import pytest
@@ -37,7 +37,9 @@ def _dev():
 def _report(name, worst):
     print(f"[configs] {name}: loss rel {worst['loss']:.2e}  grad max-rel {worst['grad']:.2e}  "
           f"cos {worst['cos']:.6f}  master max-rel {worst['w']:.2e} (vs own-grad AdamW "
-          f"{worst['w_own']:.1e})  worst at {worst.get('where')}", flush=True)
+          f"{worst['w_own']:.1e}; {worst['w_off']} of {worst['w_numel']} elements off the "
+          f"2e-2 bar, {worst['w_unexplained']} not sign-ambiguous)  worst at "
+          f"{worst.get('where')}", flush=True)
 
 
 def test_c1_full_model():
@@ -49,11 +51,15 @@ def test_c1_full_model():
     assert_north_star(worst, direct_masters=False)
 
 
-@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5"])
+@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5", "c4s"])
 def test_config_layer_and_head(name):
     """One decoder layer + the full LM head at the config's widths and packing.
     C2 keeps spare capacity (s_max > n, as the serving store does); C3-C5 run
-    with s_max = n like bench.py."""
+    with s_max = n like bench.py. C4s is the reference's 256-token Qwen3-14B
+    serving size: its products take the paths chosen for a single 256-row
+    block (128x128 split-K tiles, 256-wide tiles at small M, the skinny LoRA
+    pass split over K = 5120, the dK/dV q-head split with 5 q-heads per kv
+    head, 128-wide LM-head tiles)."""
     meta, lens = config_meta(name, L=1, s_max=None)
     if name == "c2":
         meta["max_saved_finetuning_tokens"] = sum(lens) + 333
