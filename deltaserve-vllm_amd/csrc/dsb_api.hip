@@ -277,7 +277,6 @@ struct dsb_handle {
   bf16 *normed, *dlog;
   float2* stats;
   float *tgt_logit, *lse_h, *loss_row, *dH;
-  float* sink = nullptr;  // gradient outputs of unbound projections of a LoRA group
   float* tn_work;
   long tn_work_elems;
   float* part = nullptr;  // split-K partials of the products with too few 256×256 tiles
@@ -389,12 +388,16 @@ bool has_qkv(const LayerState& ls) {
 bool has_gu(const LayerState& ls) { return ls.has[DSB_PROJ_GATE] || ls.has[DSB_PROJ_UP]; }
 
 // Gradient outputs of projection p of layer i: its torch-owned buffers, or
-// the shared sink when p is an unbound member of a bound group.
-float* grad_a(dsb_handle* h, const LayerState& ls, int p) {
-  return ls.has[p] ? ls.lora[p].gA : h->sink;
+// null when p is an untrained member of a trained q/k/v or gate/up group.
+// Such a member has zero factor slices: its rank-r passes are skipped (its
+// grad_Z columns keep the zeros they were allocated with, so the group's dX
+// product adds nothing for it), and the grouped grad_A pass, which computes
+// all of the group's rows in one tile, stores no result for it.
+float* grad_a(dsb_handle*, const LayerState& ls, int p) {
+  return ls.has[p] ? ls.lora[p].gA : nullptr;
 }
-float* grad_b(dsb_handle* h, const LayerState& ls, int p) {
-  return ls.has[p] ? ls.lora[p].gB : h->sink;
+float* grad_b(dsb_handle*, const LayerState& ls, int p) {
+  return ls.has[p] ? ls.lora[p].gB : nullptr;
 }
 
 int finalize(dsb_handle* h) {
@@ -425,9 +428,9 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->Zgu_b, NN * 2 * r));
   CKR(dalloc(h, &h->Zd_b, NN * r));
   CKR(dalloc(h, &h->gZd_b, NN * r));
-  CKR(dalloc(h, &h->gZgu_b, NN * 2 * r));
+  CKR(dalloc_zero(h, &h->gZgu_b, NN * 2 * r));
   CKR(dalloc(h, &h->gZo_b, NN * r));
-  CKR(dalloc(h, &h->gZqkv_b, NN * 3 * r));
+  CKR(dalloc_zero(h, &h->gZqkv_b, NN * 3 * r));
   CKR(dalloc(h, &h->g0, NN * D));
   CKR(dalloc(h, &h->g1, NN * D));
   CKR(dalloc(h, &h->Ggu, NN * 2 * I));
@@ -447,7 +450,6 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->loss_row, NN));
   CKR(dalloc(h, &h->dlog, NN * h->vchunk));
   CKR(dalloc(h, &h->dH, NN * D));
-  CKR(dalloc(h, &h->sink, (size_t)r * std::max(std::max(D, q), I)));
   h->tn_work_elems = 32L << 20;
   CKR(dalloc(h, &h->tn_work, h->tn_work_elems));
   {
@@ -455,16 +457,23 @@ int finalize(dsb_handle* h) {
     CK(hipGetDevice(&dev));
     CK(hipDeviceGetAttribute(&h->ncu, hipDeviceAttributeMultiprocessorCount, dev));
     // split-K partials: the largest ks·M·N over the cycle's bf16/fp32 products
-    // (output width, reduction depth) that gemm_split_count splits, and the
-    // largest ks·tail tile partials of those gemm_tail_split splits
-    const int shapes[][2] = {{W3, D}, {D, q}, {I, D}, {D, 2 * I}, {q, D}, {D, W3}, {D, h->vchunk}};
+    // that gemm_split_count splits, and the largest ks·tail tile partials of
+    // those gemm_tail_split splits. Each product is (output width, base
+    // reduction depth, LoRA segment): qkv and o recompute, gh, gxn2, gctx,
+    // gxn1, the head's dH. A layer with the projection's LoRA reduces over
+    // base + segment, one without over the base alone; both are sized, so the
+    // split a product takes at run time always fits.
+    const int shapes[][3] = {{W3, D, 3 * r}, {D, q, r},  {I, D, r},         {D, 2 * I, 2 * r},
+                             {q, D, r},      {D, W3, 3 * r}, {D, h->vchunk, 0}};
     long need = 0;
     for (const auto& sh : shapes) {
-      const int ks = gemm_split_count(N, sh[0], sh[1]);
-      if (ks > 1) need = std::max(need, (long)ks * N * sh[0]);
-      int tail = 0;
-      const int kt = gemm_tail_split(N, sh[0], sh[1], h->ncu, &tail);
-      if (ks == 1 && kt > 1) need = std::max(need, (long)kt * tail * 65536);
+      for (const int K : {sh[1], sh[1] + sh[2]}) {
+        const int ks = gemm_split_count(N, sh[0], K);
+        if (ks > 1) need = std::max(need, (long)ks * N * sh[0]);
+        int tail = 0;
+        const int kt = gemm_tail_split(N, sh[0], K, h->ncu, &tail);
+        if (ks == 1 && kt > 1) need = std::max(need, (long)kt * tail * 65536);
+      }
     }
     h->part_elems = need;
     if (need > 0) CKR(dalloc(h, &h->part, need));
@@ -1061,8 +1070,10 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       }
       CKR(tn(h, h->Zd_b, r, g, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
-    int dual_g = 1, dual_u = 1;
+    // 1: the member's grad_Z / grad_B still need the separate kernels
+    int rest_g = 0, rest_u = 0;
     if (hg) {
+      const bool tg = ls.has[DSB_PROJ_GATE], tu = ls.has[DSB_PROJ_UP];
       const DualSpec d[2] = {
           {h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, h->gZgu_b, 2L * r,
            grad_b(h, ls, DSB_PROJ_GATE), h->s, 1},
@@ -1074,15 +1085,15 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       // splits anyway (256-token cycles: 34 × 4 per pass, 68 × 3 together)
       const int Cg[2] = {I, I};
       const int ns1 = dual_splits(h, Cg, 1, r), ns2 = dual_splits(h, Cg, 2, r);
-      if (ns1 > 0 && ns2 > 0 && 2 * ns2 >= ns1) {
-        dual_g = dual_u = dual(h, d, 2, r, st);
+      if (tg && tu && ns1 > 0 && ns2 > 0 && 2 * ns2 >= ns1) {
+        rest_g = rest_u = dual(h, d, 2, r, st);
       } else {
-        dual_g = dual(h, &d[0], 1, r, st);
-        dual_u = dual(h, &d[1], 1, r, st);
+        if (tg) rest_g = dual(h, &d[0], 1, r, st);
+        if (tu) rest_u = dual(h, &d[1], 1, r, st);
       }
-      if (dual_g < 0 || dual_u < 0) return -1;
-      if (dual_g) CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
-      if (dual_u) CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
+      if (rest_g < 0 || rest_u < 0) return -1;
+      if (rest_g) CKR(skinny(h, h->Ggu, 2L * I, ls.BTg, r, I, h->gZgu_b, 2 * r, st));
+      if (rest_u) CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
     }
     {
       GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
@@ -1094,10 +1105,10 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       float* gAg = grad_a(h, ls, DSB_PROJ_GATE);
       float* gAu = grad_a(h, ls, DSB_PROJ_UP);
       CKR(tn(h, h->gZgu_b, 2 * r, h->xn2, D, 2 * r, D, gAg, gAu, nullptr, r, 0, 1.f, st));
-      if (dual_g)
+      if (rest_g)
         CKR(tn(h, h->Zgu_b, 2 * r, h->Ggu, 2L * I, r, I, grad_b(h, ls, DSB_PROJ_GATE), nullptr,
                nullptr, r, 1, h->s, st));
-      if (dual_u)
+      if (rest_u)
         CKR(tn(h, h->Zgu_b + r, 2 * r, h->Ggu + I, 2L * I, r, I, grad_b(h, ls, DSB_PROJ_UP),
                nullptr, nullptr, r, 1, h->s, st));
     }
@@ -1139,20 +1150,27 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
                   h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
-    int dual_q = 1, dual_k = 1, dual_v = 1;
+    int rest_qkv[3] = {0, 0, 0};
     if (hq) {
-      const DualSpec d[3] = {
+      const DualSpec all[3] = {
           {h->gqkv, W3, q, h->Zqkv_b, 3L * r, ls.BTq, h->gZqkv_b, 3L * r,
            grad_b(h, ls, DSB_PROJ_Q), h->s, 1},
           {h->gqkv + q, W3, kv, h->Zqkv_b + r, 3L * r, ls.BTk, h->gZqkv_b + r, 3L * r,
            grad_b(h, ls, DSB_PROJ_K), h->s, 1},
           {h->gqkv + q + kv, W3, kv, h->Zqkv_b + 2 * r, 3L * r, ls.BTv, h->gZqkv_b + 2 * r, 3L * r,
            grad_b(h, ls, DSB_PROJ_V), h->s, 1}};
-      dual_q = dual_k = dual_v = dual(h, d, 3, r, st);
-      if (dual_q < 0) return -1;
-      if (dual_q) CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
-      if (dual_k) CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_b + r, 3 * r, st));
-      if (dual_v) CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_b + 2 * r, 3 * r, st));
+      // the trained members in one launch
+      DualSpec d[3];
+      int member[3], cnt = 0;
+      for (int p = 0; p < 3; ++p)
+        if (ls.has[p]) { d[cnt] = all[p]; member[cnt++] = p; }
+      const int rest = dual(h, d, cnt, r, st);
+      if (rest < 0) return -1;
+      for (int i = 0; i < cnt; ++i) rest_qkv[member[i]] = rest;
+      if (rest_qkv[0]) CKR(skinny(h, h->gqkv, W3, ls.BTq, r, q, h->gZqkv_b, 3 * r, st));
+      if (rest_qkv[1]) CKR(skinny(h, h->gqkv + q, W3, ls.BTk, r, kv, h->gZqkv_b + r, 3 * r, st));
+      if (rest_qkv[2])
+        CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_b + 2 * r, 3 * r, st));
     }
     {
       GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
@@ -1163,13 +1181,13 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     if (hq) {
       CKR(tn(h, h->gZqkv_b, 3 * r, h->xn1, D, 3 * r, D, grad_a(h, ls, DSB_PROJ_Q),
              grad_a(h, ls, DSB_PROJ_K), grad_a(h, ls, DSB_PROJ_V), r, 0, 1.f, st));
-      if (dual_q)
+      if (rest_qkv[0])
         CKR(tn(h, h->Zqkv_b, 3 * r, h->gqkv, W3, r, q, grad_b(h, ls, DSB_PROJ_Q), nullptr, nullptr,
                r, 1, h->s, st));
-      if (dual_k)
+      if (rest_qkv[1])
         CKR(tn(h, h->Zqkv_b + r, 3 * r, h->gqkv + q, W3, r, kv, grad_b(h, ls, DSB_PROJ_K), nullptr,
                nullptr, r, 1, h->s, st));
-      if (dual_v)
+      if (rest_qkv[2])
         CKR(tn(h, h->Zqkv_b + 2 * r, 3 * r, h->gqkv + q + kv, W3, r, kv, grad_b(h, ls, DSB_PROJ_V),
                nullptr, nullptr, r, 1, h->s, st));
     }
@@ -2179,7 +2197,13 @@ float* scratch_for_current_device() {
   std::lock_guard<std::mutex> lk(scratch_mu);
   if (!scratch_dev[dev]) {
     void* p = nullptr;
+    // The first call on a device may come while a stream of this thread is
+    // being captured into a graph: the lookup is not a stream operation, and
+    // relaxed mode lets it run under any capture mode.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || !p) {
       set_error("dsb_op_lora_dual_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
                 dev, hipGetErrorString(e));

@@ -370,6 +370,7 @@ __global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnBatch b) {
   s *= a.scale;
   const int grp = j / a.rg, jj = j % a.rg;
   float* o = a.outs[grp];
+  if (o == nullptr) return;  // an untrained member of a LoRA group
   if (a.transpose_out)
     o[(long)c * a.rg + jj] = s;
   else
