@@ -252,6 +252,9 @@ struct dsb_handle {
   std::vector<const bf16*> layer_in;
   std::vector<const bf16*> gate_up_in;  // saved gate‖up per layer (empty: recompute)
   long ld_gate_up = 0;
+  // the other optional save points per layer (empty: recomputed)
+  std::vector<const bf16*> q_in, k_in, v_in, ctx_in, rm_in;
+  long ld_q_in = 0, ld_k_in = 0, ld_v_in = 0, ld_ctx_in = 0, ld_rm_in = 0;
   const bf16* final_in = nullptr;
   const int64_t* ids = nullptr;
   long act_ld = 0;
@@ -983,6 +986,24 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     const bf16* wgu = (const bf16*)ls.w.gate_up;
     const bf16* qnw = (const bf16*)ls.w.q_norm;
     const bf16* knw = (const bf16*)ls.w.k_norm;
+    // The optional save points (trainer.py:532-552). Saved q/k/v: Llama-3's
+    // q/k are post-RoPE, attended in place; Qwen3's are pre-norm and go
+    // through the q/k-norm + RoPE pass into qk. v is attended in place.
+    const bool sqkv = !h->q_in.empty(), sctx = !h->ctx_in.empty(), srm = !h->rm_in.empty();
+    if (sqkv) {
+      if (!h->qwen) {
+        at.q = h->q_in[li]; at.ldq = h->ld_q_in;
+        at.k = h->k_in[li]; at.ldk = h->ld_k_in;
+      }
+      at.v = h->v_in[li]; at.ldv = h->ld_v_in;
+    }
+    // the O projection's input: the saved context, else the recomputed one
+    // (the recomputed ctx and its residual still feed rowsum(dO∘O))
+    const bf16* cx = sctx ? h->ctx_in[li] : h->ctx;
+    const long ldcx = sctx ? h->ld_ctx_in : (long)q;
+    // the post-attention residual: saved, or recomputed by the O projection
+    const bf16* rs = srm ? h->rm_in[li] : h->resid;
+    const long ldrs = srm ? h->ld_rm_in : (long)D;
 
     // ================= forward recompute (llama3.py:62-146, qwen3.py:68-130)
     {
@@ -990,31 +1011,35 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       LK(rmsnorm_fwd(x, ldx, (const bf16*)ls.w.in_ln, h->xn1, D, N, nd, D, eps, st));
     }
     if (hq) CKR(skinny(h, h->xn1, D, ls.Aqkv, 3 * r, D, h->Zqkv_b, 3 * r, st));
-    {
+    if (!sqkv) {
       GemmProblem p{h->xn1, (long)D, wqkv, (long)D, hq ? h->Zqkv_b : nullptr, 3L * r,
                     hq ? ls.B2qkv : nullptr, 3L * r, N, W3, D, hq ? 3 * r : 0, nd};
       EpiBF16 e{h->qkv_pre, (long)W3, W3, nullptr, 0};
       CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
-    {
+    if (!sqkv || h->qwen) {
       KScope ks(h, st, "rope_fwd", 0, 0, 0, 2.0 * (q + kv) * 2 + 512.0, 0, 0);
-      LK(rope_fwd(h->qkv_pre, W3, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
-                  h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+      if (sqkv)
+        LK(rope_fwd(h->q_in[li], h->ld_q_in, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq,
+                    h->Hkv, qnw, knw, eps, st, h->k_in[li], h->ld_k_in));
+      else
+        LK(rope_fwd(h->qkv_pre, W3, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
+                    h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     {
       KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 4.0 * q + 4.0 * Hq, 0, 0);
       LK(attn_fwd(at, st));
     }
-    if (ho) CKR(skinny(h, h->ctx, q, ls.Ao, r, q, h->Zo_b, r, st));
-    {
-      GemmProblem p{h->ctx, (long)q, wo, (long)q, ho ? h->Zo_b : nullptr, (long)r,
+    if (ho) CKR(skinny(h, cx, ldcx, ls.Ao, r, q, h->Zo_b, r, st));
+    if (!srm) {
+      GemmProblem p{cx, ldcx, wo, (long)q, ho ? h->Zo_b : nullptr, (long)r,
                     ho ? ls.Bo : nullptr, (long)r, N, D, q, ho ? r : 0, nd};
       EpiBF16 e{h->resid, (long)D, D, x, ldx};
       CKR(gemm(h, "bf16", p, e, st, 2.0, 2.0 * D));
     }
     {
       KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_fwd(h->resid, D, (const bf16*)ls.w.post_ln, h->xn2, D, N, nd, D, eps, st));
+      LK(rmsnorm_fwd(rs, ldrs, (const bf16*)ls.w.post_ln, h->xn2, D, N, nd, D, eps, st));
     }
     if (hg) CKR(skinny(h, h->xn2, D, ls.Agu, 2 * r, D, h->Zgu_b, 2 * r, st));
     if (saved_gu) {
@@ -1114,7 +1139,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     {
       KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 18.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(h->resid, D, h->gxn2, true, D, (const bf16*)ls.w.post_ln, nullptr, D,
+      LK(rmsnorm_bwd(rs, ldrs, h->gxn2, true, D, (const bf16*)ls.w.post_ln, nullptr, D,
                      h->grm, D, N, nd, D, eps, st, g32, h->grm32));
     }
     int dual_o = 1;
@@ -1133,7 +1158,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     if (ho) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
-      CKR(tn(h, h->gZo_b, r, h->ctx, q, r, q, t.gA, nullptr, nullptr, r, 0, 1.f, st));
+      CKR(tn(h, h->gZo_b, r, cx, ldcx, r, q, t.gA, nullptr, nullptr, r, 0, 1.f, st));
       if (dual_o) CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
@@ -1147,8 +1172,13 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     {
       KScope ks(h, st, "rope_bwd", 0, 0, 0, 4.0 * (q + kv) + 512.0, 0, 0);
-      LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
-                  h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+      // the q/k-norm backward (Qwen3) reads the pre-norm q/k: saved or recomputed
+      if (sqkv && h->qwen)
+        LK(rope_bwd(h->gqkv, W3, h->q_in[li], h->ld_q_in, h->cosb, h->sinb, N, nd, h->Hq,
+                    h->Hkv, qnw, knw, eps, st, h->k_in[li], h->ld_k_in));
+      else
+        LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
+                    h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     int rest_qkv[3] = {0, 0, 0};
     if (hq) {
@@ -1571,6 +1601,37 @@ int dsb_bind_activations(dsb_handle* h, const dsb_activations* a) {
       gu.push_back((const bf16*)a->mlp_gate_up[i]);
     }
   }
+  // the optional save points: per-layer bf16 rows of at least `width`
+  // columns, 16-byte aligned with a stride that is a multiple of 8
+  auto saved = [&](const void* const* ptrs, int64_t ld, int width, const char* what,
+                   std::vector<const bf16*>& out) -> int {
+    out.clear();
+    if (!ptrs) return 0;
+    if (ld < width || ld % 8) {
+      set_error("dsb_bind_activations: %s row stride must be a multiple of 8 and >= %d", what,
+                width);
+      h->err = get_error();
+      return -1;
+    }
+    for (int i = 0; i < h->L; ++i) {
+      if (!ptrs[i] || ((uintptr_t)ptrs[i] & 15)) {
+        set_error("dsb_bind_activations: %s pointers must be non-null, 16-byte aligned", what);
+        h->err = get_error();
+        return -1;
+      }
+      out.push_back((const bf16*)ptrs[i]);
+    }
+    return 0;
+  };
+  if ((a->attn_q != nullptr) != (a->attn_k != nullptr) ||
+      (a->attn_q != nullptr) != (a->attn_v != nullptr))
+    return fail(h, "dsb_bind_activations: attn_q, attn_k and attn_v are bound together");
+  std::vector<const bf16*> qv, kv_, vv, cv, rv;
+  CKR(saved(a->attn_q, a->ld_q, h->q, "attn_q", qv));
+  CKR(saved(a->attn_k, a->ld_k, h->kv, "attn_k", kv_));
+  CKR(saved(a->attn_v, a->ld_v, h->kv, "attn_v", vv));
+  CKR(saved(a->attn_ctx, a->ld_ctx, h->q, "attn_ctx", cv));
+  CKR(saved(a->resid_mid, a->ld_resid_mid, h->D, "resid_mid", rv));
   h->layer_in.assign(h->L, nullptr);
   for (int i = 0; i < h->L; ++i) {
     if (!a->layer_in[i]) return fail(h, "dsb_bind_activations: null layer_in");
@@ -1578,6 +1639,9 @@ int dsb_bind_activations(dsb_handle* h, const dsb_activations* a) {
   }
   h->gate_up_in = gu;
   h->ld_gate_up = a->mlp_gate_up ? (long)a->ld_gate_up : 0;
+  h->q_in = qv; h->k_in = kv_; h->v_in = vv; h->ctx_in = cv; h->rm_in = rv;
+  h->ld_q_in = a->ld_q; h->ld_k_in = a->ld_k; h->ld_v_in = a->ld_v;
+  h->ld_ctx_in = a->ld_ctx; h->ld_rm_in = a->ld_resid_mid;
   h->final_in = (const bf16*)a->final_in;
   h->ids = a->input_ids;
   h->act_ld = a->ld;

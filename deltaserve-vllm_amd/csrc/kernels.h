@@ -18,12 +18,16 @@ hipError_t rmsnorm_bwd(const bf16* x, long ldx, const void* g, bool g_f32, long 
                        const float* resid32 = nullptr, float* out32 = nullptr);
 hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_freq,
                       int half, float* cosb, float* sinb, hipStream_t s);
+// q heads of a row at in / pre (row stride ldin / ldp); k heads at ink / prek
+// (stride ldk / ldpk), by default right after the q heads of the same row.
 hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
                     const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
-                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s);
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
+                    const bf16* ink = nullptr, long ldk = 0);
 hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* cosb,
                     const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
-                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s);
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
+                    const bf16* prek = nullptr, long ldpk = 0);
 hipError_t swiglu_h(const bf16* gu, long ldgu, bf16* h, long ldh, int n, const int* n_dev,
                     int I, hipStream_t s);
 

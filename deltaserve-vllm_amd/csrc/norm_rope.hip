@@ -203,7 +203,9 @@ __global__ void rope_table_kernel(const int* __restrict__ pos, int n, const int*
 // rotate-half pairs (8i + e, 64 + 8i + e), e = 0..7, moved as 16-byte
 // vectors; one wave covers 8 heads of one token (q heads, then k heads), and
 // per-head sums reduce over the group's 8 lanes.
-//   in : qkv_pre row [q | k | v] (pre-norm, pre-RoPE projection output)
+//   in : the q heads of a row at in (stride ldin) and its k heads at ink
+//        (stride ldk): pre-norm, pre-RoPE projection outputs, either the
+//        [q | k | v] rows of the recompute or separate saved q / k buffers
 //   out: qk row [q | k] after (optional per-head RMSNorm, rounded to bf16) + RoPE
 DSB_DEV float group8_sum(float v) {
   v += __shfl_xor(v, 1, 64);
@@ -213,7 +215,8 @@ DSB_DEV float group8_sum(float v) {
 }
 
 __global__ __launch_bounds__(256) void rope_fwd_kernel(
-    const bf16* __restrict__ in, long ldin, bf16* __restrict__ out, long ldout,
+    const bf16* __restrict__ in, long ldin, const bf16* __restrict__ ink, long ldk,
+    bf16* __restrict__ out, long ldout,
     const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
     const int* n_dev, int Hq, int Hkv, const bf16* __restrict__ qn_w,
     const bf16* __restrict__ kn_w, float eps) {
@@ -226,7 +229,8 @@ __global__ __launch_bounds__(256) void rope_fwd_kernel(
   const int hh = (int)(item % HG) * 8 + (l >> 3);
   const bool live = hh < H;
   const int h = live ? hh : H - 1;
-  const bf16* src = in + (long)t * ldin + h * 128 + 8 * i;
+  const bf16* src = h < Hq ? in + (long)t * ldin + h * 128 + 8 * i
+                            : ink + (long)t * ldk + (h - Hq) * 128 + 8 * i;
   float x1[8], x2[8];
   unpack8(ldg128(src), x1);
   unpack8(ldg128(src + 64), x2);
@@ -268,6 +272,7 @@ __global__ __launch_bounds__(256) void rope_fwd_kernel(
 // same lane layout as the forward.
 __global__ __launch_bounds__(256) void rope_bwd_kernel(
     bf16* __restrict__ g, long ldg, const bf16* __restrict__ pre, long ldp,
+    const bf16* __restrict__ prek, long ldpk,
     const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
     const int* n_dev, int Hq, int Hkv, const bf16* __restrict__ qn_w,
     const bf16* __restrict__ kn_w, float eps) {
@@ -297,7 +302,8 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(
   }
   const bf16* nw = h < Hq ? qn_w : kn_w;
   if (nw) {
-    const bf16* xp = pre + (long)t * ldp + h * 128 + 8 * i;
+    const bf16* xp = h < Hq ? pre + (long)t * ldp + h * 128 + 8 * i
+                            : prek + (long)t * ldpk + (h - Hq) * 128 + 8 * i;
     float x1[8], x2[8], w1[8], w2[8];
     unpack8(ldg128(xp), x1);
     unpack8(ldg128(xp + 64), x2);
@@ -388,21 +394,31 @@ hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_
 
 hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
                     const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
-                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s) {
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
+                    const bf16* ink, long ldk) {
   const long items = (long)n * ((Hq + Hkv + 7) / 8);
   if (items <= 0) return hipSuccess;
+  if (!ink) {
+    ink = in + (long)Hq * 128;
+    ldk = ldin;
+  }
   hipLaunchKernelGGL(rope_fwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, in,
-                     ldin, out, ldout, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+                     ldin, ink, ldk, out, ldout, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
   return hipGetLastError();
 }
 
 hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* cosb,
                     const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
-                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s) {
+                    const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
+                    const bf16* prek, long ldpk) {
   const long items = (long)n * ((Hq + Hkv + 7) / 8);
   if (items <= 0) return hipSuccess;
+  if (!prek) {
+    prek = pre + (long)Hq * 128;
+    ldpk = ldp;
+  }
   hipLaunchKernelGGL(rope_bwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, g,
-                     ldg, pre, ldp, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+                     ldg, pre, ldp, prek, ldpk, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
   return hipGetLastError();
 }
 

@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 # timing); the in-tree build is the default.
 LIB_PATH = os.environ.get("DSB_LIB") or os.path.join(LIB_DIR, "libdsb.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
 ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
@@ -57,7 +57,11 @@ class DsbLoraTensors(Structure):
 class DsbActivations(Structure):
     _fields_ = [("layer_in", POINTER(c_void_p)), ("final_in", c_void_p),
                 ("input_ids", c_void_p), ("ld", c_int64),
-                ("mlp_gate_up", POINTER(c_void_p)), ("ld_gate_up", c_int64)]
+                ("mlp_gate_up", POINTER(c_void_p)), ("ld_gate_up", c_int64),
+                ("attn_q", POINTER(c_void_p)), ("attn_k", POINTER(c_void_p)),
+                ("attn_v", POINTER(c_void_p)), ("ld_q", c_int64), ("ld_k", c_int64),
+                ("ld_v", c_int64), ("attn_ctx", POINTER(c_void_p)), ("ld_ctx", c_int64),
+                ("resid_mid", POINTER(c_void_p)), ("ld_resid_mid", c_int64)]
 
 
 class DsbDualPass(Structure):

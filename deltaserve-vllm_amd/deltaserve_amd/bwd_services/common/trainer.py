@@ -222,11 +222,39 @@ class LoraSftTrainerService(BackwardService):
                                  self._grads[(layer, proj, "B")].data_ptr())
             L.check(lib.dsb_bind_lora(h, layer, L.PROJ_INDEX[proj], byref(t)), h, "dsb_bind_lora")
 
+    def _saved_points(self, activations) -> dict:
+        """The optional save points the cycle consumes, gated as the reference
+        trainer gates them (trainer.py:160-177, :532-552): ``mlp_gate_up``
+        and ``attn_ctx`` whenever the store carries them, q/k/v only with the
+        worker's ``save_attn_qkv`` (all three buffers), ``resid_mid`` only
+        with ``save_resid_mid``. Returns name -> (per-layer list, width)."""
+        meta = self.shared.get("meta") or {}
+        want = {"mlp_gate_up": 2 * self.inter, "attn_ctx": self.q_size}
+        if meta.get("save_attn_qkv") and self.family.supports_saved_qkv and all(
+                activations.get(k) is not None for k in ("attn_qh", "attn_kh", "attn_vh")):
+            want.update(attn_qh=self.q_size, attn_kh=self.kv_size, attn_vh=self.kv_size)
+        if meta.get("save_resid_mid"):
+            want["resid_mid"] = self.D
+        out = {}
+        for name, width in want.items():
+            bufs = activations.get(name)
+            if bufs is None or (isinstance(bufs, (list, tuple)) and not bufs):
+                continue
+            if len(bufs) != self.L:
+                raise ValueError(f"{name} carries {len(bufs)} layers, the model has {self.L}")
+            ld = bufs[0].stride(0)
+            for t in bufs:
+                if (t.dtype != torch.bfloat16 or not t.is_cuda or t.stride(0) != ld
+                        or t.stride(1) != 1 or t.shape[1] != width):
+                    raise TypeError(f"{name} buffers must be bf16 CUDA [rows, {width}] with one "
+                                    "row stride")
+            out[name] = (bufs, ld)
+        return out
+
     def _bind_activations(self, activations) -> None:
         li = activations["layer_in"]
         fi = activations["final_in"]
         ids = activations["concat_input_ids"]
-        gu = activations.get("mlp_gate_up")
         if len(li) != self.L:
             raise ValueError(f"activations carry {len(li)} layer inputs, the model has {self.L}")
         ld = fi.stride(0)
@@ -235,34 +263,32 @@ class LoraSftTrainerService(BackwardService):
                 raise TypeError("activation buffers must be bf16 CUDA [rows, D] with one row stride")
         if ids.dtype != torch.int64 or not ids.is_cuda:
             raise TypeError("concat_input_ids must be an int64 CUDA tensor")
-        ld_gu = 0
-        if gu is not None:
-            # the gate||up save point (accumulate.py:174, :210-212): used in place
-            # of the gate_up recompute (llama3.py:63-72, ffn.py:18-26)
-            if len(gu) != self.L:
-                raise ValueError(f"mlp_gate_up carries {len(gu)} layers, the model has {self.L}")
-            ld_gu = gu[0].stride(0)
-            for t in gu:
-                if (t.dtype != torch.bfloat16 or not t.is_cuda or t.stride(0) != ld_gu
-                        or t.stride(1) != 1 or t.shape[1] != 2 * self.inter):
-                    raise TypeError("mlp_gate_up buffers must be bf16 CUDA [rows, 2*intermediate] "
-                                    "with one row stride")
+        saved = self._saved_points(activations)
         key = (tuple(t.data_ptr() for t in li), fi.data_ptr(), ids.data_ptr(), ld,
-               None if gu is None else tuple(t.data_ptr() for t in gu), ld_gu)
+               tuple((name, tuple(t.data_ptr() for t in bufs), sld)
+                     for name, (bufs, sld) in sorted(saved.items())))
         if key == self._act_key:
             return
-        ptrs = (c_void_p * self.L)(*[t.data_ptr() for t in li])
-        self._act_ptrs = ptrs
-        gptrs = None
-        if gu is not None:
-            gptrs = (c_void_p * self.L)(*[t.data_ptr() for t in gu])
-        self._gu_ptrs = gptrs
-        a = L.DsbActivations(ctypes.cast(ptrs, ctypes.POINTER(c_void_p)), fi.data_ptr(),
-                             ids.data_ptr(), ld,
-                             None if gptrs is None else ctypes.cast(gptrs, ctypes.POINTER(c_void_p)),
-                             ld_gu)
+        keep = []  # the pointer arrays must outlive the bind call
+
+        def ptrs(bufs):
+            arr = (c_void_p * self.L)(*[t.data_ptr() for t in bufs])
+            keep.append(arr)
+            return ctypes.cast(arr, ctypes.POINTER(c_void_p))
+
+        a = L.DsbActivations()
+        a.layer_in, a.final_in, a.input_ids, a.ld = ptrs(li), fi.data_ptr(), ids.data_ptr(), ld
+        fields = {"mlp_gate_up": ("mlp_gate_up", "ld_gate_up"), "attn_qh": ("attn_q", "ld_q"),
+                  "attn_kh": ("attn_k", "ld_k"), "attn_vh": ("attn_v", "ld_v"),
+                  "attn_ctx": ("attn_ctx", "ld_ctx"), "resid_mid": ("resid_mid", "ld_resid_mid")}
+        for name, (bufs, sld) in saved.items():
+            f_ptr, f_ld = fields[name]
+            setattr(a, f_ptr, ptrs(bufs))
+            setattr(a, f_ld, sld)
         L.check(L.load().dsb_bind_activations(self._h, byref(a)), self._h, "dsb_bind_activations")
+        self._act_ptrs = keep
         self._act_key = key
+        self.saved_points = sorted(saved)
 
     # ------------------------------------------------------------ the cycle
     def process_backward(self, activations, sample_lens, n, epoch):

@@ -159,19 +159,32 @@ class ActivationStore:
     ``[max_saved]``. With ``intermediate_size`` > 0 (the reference saves it
     whenever the MLP's gate_up modules exist, accumulate.py:174, :210-212)
     ``mlp_gate_up[i]`` is bf16 ``[max_saved + 1, 2·intermediate]``, the gate‖up
-    projection output the backward then reads instead of recomputing it. The
-    slot table has the reference's 7 slots per layer plus the final norm's;
-    slots of activations that the backward recomputes (residual mid-point,
-    q/k/v, attention context) hold no buffer, so their save calls are no-ops,
-    as in the reference when those saves are switched off.
+    projection output the backward then reads instead of recomputing it.
+
+    The opt-in save points (accumulate.py:213-235), each per layer:
+    ``save_attn_qkv`` → ``attn_qh`` / ``attn_kh`` / ``attn_vh`` bf16
+    ``[max_saved + 1, q_size | kv_size]`` (the attention call's q, k, v; for a
+    family whose backward needs the pre-transform q/k, the q/k-norm inputs),
+    ``save_attn_ctx`` → ``attn_ctx`` ``[max_saved + 1, q_size]`` (the attention
+    output), ``save_resid_mid`` → ``resid_mid`` ``[max_saved + 1, hidden]``
+    (the post-attention residual), and ``save_final_hidden`` →
+    ``final_hidden`` (the final norm's output, for the debug capture check).
+    The slot table has the reference's 7 slots per layer plus the final
+    norm's; the slots of save points that are off hold no buffer, so their
+    save calls are no-ops, as in the reference.
     """
 
     STAGES = 4  # pinned staging slots for the index refresh (accumulate.py:262)
 
     def __init__(self, num_layers: int, hidden_size: int, max_saved: int, device="cuda",
-                 intermediate_size: int = 0):
+                 intermediate_size: int = 0, q_size: int = 0, kv_size: int = 0,
+                 save_attn_qkv: bool = False, save_attn_ctx: bool = False,
+                 save_resid_mid: bool = False, save_final_hidden: bool = False):
         if max_saved <= 0 or num_layers <= 0 or hidden_size <= 0 or intermediate_size < 0:
             raise ValueError("ActivationStore: sizes must be positive")
+        if (save_attn_qkv and (q_size <= 0 or kv_size <= 0)) or (save_attn_ctx and q_size <= 0):
+            raise ValueError("ActivationStore: the q/k/v and context save points need "
+                             "q_size (and kv_size)")
         self.num_layers, self.hidden_size, self.max_saved = num_layers, hidden_size, max_saved
         self.intermediate_size = intermediate_size
         self.device = torch.device(device)
@@ -182,6 +195,13 @@ class ActivationStore:
         self.layer_in = [buf() for _ in range(num_layers)]
         self.mlp_gate_up = ([buf(2 * intermediate_size) for _ in range(num_layers)]
                             if intermediate_size > 0 else [])
+        per_layer = lambda on, width: [buf(width) for _ in range(num_layers)] if on else []  # noqa: E731
+        self.attn_qh = per_layer(save_attn_qkv, q_size)
+        self.attn_kh = per_layer(save_attn_qkv, kv_size)
+        self.attn_vh = per_layer(save_attn_qkv, kv_size)
+        self.attn_ctx = per_layer(save_attn_ctx, q_size)
+        self.resid_mid = per_layer(save_resid_mid, hidden_size)
+        self.final_hidden = buf() if save_final_hidden else None
         self.final_in = buf()
         self.concat_input_ids = torch.zeros(max_saved, dtype=torch.int64, device=self.device)
         self.ft_src = torch.zeros(max_saved, dtype=torch.int64, device=self.device)
@@ -192,9 +212,12 @@ class ActivationStore:
         self._idx_pin_pos = 0
         bufs: list = [None] * (SLOTS_PER_LAYER * num_layers + 1)
         for i in range(num_layers):
-            bufs[SLOTS_PER_LAYER * i + SLOT_LAYER_IN] = self.layer_in[i]
-            if self.mlp_gate_up:
-                bufs[SLOTS_PER_LAYER * i + SLOT_GATE_UP] = self.mlp_gate_up[i]
+            for kind, per in ((SLOT_LAYER_IN, self.layer_in), (SLOT_GATE_UP, self.mlp_gate_up),
+                              (SLOT_RESID_MID, self.resid_mid), (SLOT_QH, self.attn_qh),
+                              (SLOT_KH, self.attn_kh), (SLOT_VH, self.attn_vh),
+                              (SLOT_CTX, self.attn_ctx)):
+                if per:
+                    bufs[SLOTS_PER_LAYER * i + kind] = per[i]
         bufs[SLOTS_PER_LAYER * num_layers] = self.final_in
         self.op_bufs = bufs
         self.marker = torch.zeros(1, dtype=torch.int32, device=self.device)
@@ -275,11 +298,15 @@ class ActivationStore:
     def end_step(self) -> None:
         self._eager = None
 
-    def accumulate_final(self, input_ids_flat: torch.Tensor) -> None:
-        """The ids of the armed eager step's FT rows (accumulate.py:598-622)."""
+    def accumulate_final(self, input_ids_flat: torch.Tensor,
+                         hidden_states: Optional[torch.Tensor] = None) -> None:
+        """The ids of the armed eager step's FT rows, and with a
+        ``final_hidden`` buffer the model output's rows (accumulate.py:598-622)."""
         fs = self._eager
         if fs is not None:
             save_ids(input_ids_flat, fs.src, fs.dst, self.concat_input_ids)
+            if self.final_hidden is not None and hidden_states is not None:
+                save_rows(hidden_states, None, self.final_hidden, fs.src, fs.dst)
 
     def zero_offset_range(self, off: int, n: int) -> None:
         """Zero rows ``[off, off + n)`` of every buffer after an aborted forward
@@ -289,7 +316,7 @@ class ActivationStore:
         n = min(n, self.max_saved - off)
         if n <= 0:
             return
-        for b in self.layer_in + self.mlp_gate_up + [self.final_in]:
+        for b in self._all_buffers():
             b[off:off + n].zero_()
         self.concat_input_ids[off:off + n].zero_()
 
@@ -300,13 +327,21 @@ class ActivationStore:
         fs = state or self.capture_state()
         save_ids(input_ids_flat, fs.src, fs.dst, self.concat_input_ids)
 
+    def _all_buffers(self) -> list:
+        out = (self.layer_in + self.mlp_gate_up + self.attn_qh + self.attn_kh + self.attn_vh
+               + self.attn_ctx + self.resid_mid + [self.final_in])
+        return out + ([self.final_hidden] if self.final_hidden is not None else [])
+
     def activations(self) -> dict:
         """The activation dict a backward cycle takes (the ``buffers`` of the
-        share_activations message, base.py:460-470)."""
+        share_activations message, accumulate.py:236-252)."""
         out = {"layer_in": self.layer_in, "final_in": self.final_in,
                "concat_input_ids": self.concat_input_ids}
-        if self.mlp_gate_up:
-            out["mlp_gate_up"] = self.mlp_gate_up
+        for name in ("mlp_gate_up", "attn_qh", "attn_kh", "attn_vh", "attn_ctx", "resid_mid"):
+            if getattr(self, name):
+                out[name] = getattr(self, name)
+        if self.final_hidden is not None:
+            out["final_hidden"] = self.final_hidden
         return out
 
 

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DSB_ABI_VERSION 2
+#define DSB_ABI_VERSION 3
 
 enum { DSB_FAMILY_LLAMA3 = 0, DSB_FAMILY_QWEN3 = 1 };
 enum { DSB_ROPE_DEFAULT = 0, DSB_ROPE_LINEAR = 1, DSB_ROPE_LLAMA3 = 2 };
@@ -97,6 +97,28 @@ typedef struct dsb_activations {
   int64_t ld;
   const void* const* mlp_gate_up;  /* n_layers pointers, or NULL */
   int64_t ld_gate_up;
+  /* The optional q/k/v save point (all three or none; accumulate.py:213-226):
+   * bf16 [s_max + 1, q | kv | kv] per layer, row strides ld_q / ld_k / ld_v.
+   * Llama-3 saves q and k after RoPE, Qwen3 before its q/k-norm
+   * (family.py:75-84). When bound, the Q/K/V projection is not recomputed
+   * (llama3.py:118-126, qwen3.py:90-96): Llama-3 attends the saved rows
+   * directly, Qwen3 re-applies the q/k-norm and RoPE to them. The callers
+   * pass them only when the worker's save_attn_qkv is on (trainer.py:539-544). */
+  const void* const* attn_q;
+  const void* const* attn_k;
+  const void* const* attn_v;
+  int64_t ld_q, ld_k, ld_v;
+  /* The optional attention-context save point, bf16 [s_max + 1, q]: the O
+   * projection's input (llama3.py:128-132). The attention forward still
+   * runs, since the backward takes its softmax statistics and rowsum(dO∘O)
+   * from it. */
+  const void* const* attn_ctx;
+  int64_t ld_ctx;
+  /* The optional post-attention residual save point, bf16 [s_max + 1, D]:
+   * used in place of the O projection and the residual add
+   * (llama3.py:134-141; passed when save_resid_mid is on, trainer.py:552). */
+  const void* const* resid_mid;
+  int64_t ld_resid_mid;
 } dsb_activations;
 
 /* Per-cycle device timing (ms), filled by dsb_step when requested. */

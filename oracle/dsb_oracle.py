@@ -235,25 +235,44 @@ def _lora(lw, p):
 
 
 def layer_forward(x, lw, s, cos, sin, seq_lens, b_start, dims, eps, qk_norm=False,
-                  saved_gate_up=None):
+                  saved_gate_up=None, saved_qkv=None, saved_ctx=None, saved_resid_mid=None):
     """llama3.py:62-146 / qwen3.py:68-130 with ffn.py:18-26 (gate/up LoRA added).
     ``saved_gate_up`` [n, 2I] (gate first): the captured pre-activations,
-    used instead of the gate/up recompute (ffn.py:21-24, llama3.py:142)."""
+    used instead of the gate/up recompute (ffn.py:21-24, llama3.py:142).
+    ``saved_qkv`` = (q, k, v) flat [n, q|kv]: skips the Q/K/V projections;
+    Llama-3 takes q/k as saved after RoPE (llama3.py:120-126), Qwen3 before
+    its q/k-norm, re-applying norm and RoPE (qwen3.py:90-96).
+    ``saved_ctx`` [n, q]: the attention context, used instead of the attention
+    forward (llama3.py:128-132). ``saved_resid_mid`` [n, D]: the
+    post-attention residual, used instead of the O projection and residual
+    add (llama3.py:134-141)."""
     Hq, Hkv, Hd = dims
     n = x.shape[0]
     xn1 = rmsnorm(x, lw["in_ln"], eps)
-    q = proj(xn1, lw["q"], *_lora(lw, "q"), s)
-    k = proj(xn1, lw["k"], *_lora(lw, "k"), s)
-    v = proj(xn1, lw["v"], *_lora(lw, "v"), s)
-    q_pre, k_pre = q.view(n, Hq, Hd), k.view(n, Hkv, Hd)
+    if saved_qkv is not None:
+        q, k, v = saved_qkv
+    else:
+        q = proj(xn1, lw["q"], *_lora(lw, "q"), s)
+        k = proj(xn1, lw["k"], *_lora(lw, "k"), s)
+        v = proj(xn1, lw["v"], *_lora(lw, "v"), s)
+    q_pre, k_pre = q.reshape(n, Hq, Hd), k.reshape(n, Hkv, Hd)
     if qk_norm:
         qh = apply_rope(rmsnorm(q_pre, lw["q_norm"], eps), cos, sin)
         kh = apply_rope(rmsnorm(k_pre, lw["k_norm"], eps), cos, sin)
+    elif saved_qkv is not None:
+        qh, kh = q_pre, k_pre  # Llama-3 saves them after RoPE
+        q_pre = k_pre = None
     else:
         qh, kh = apply_rope(q_pre, cos, sin), apply_rope(k_pre, cos, sin)
-    vh = v.view(n, Hkv, Hd)
-    ctx = attn_forward(qh, kh, vh, seq_lens, b_start, Hq, Hkv)
-    resid_mid = x + proj(ctx, lw["o"], *_lora(lw, "o"), s)
+    vh = v.reshape(n, Hkv, Hd)
+    if saved_ctx is not None:
+        ctx = saved_ctx.reshape(n, Hq * Hd)
+    else:
+        ctx = attn_forward(qh, kh, vh, seq_lens, b_start, Hq, Hkv)
+    if saved_resid_mid is not None:
+        resid_mid = saved_resid_mid
+    else:
+        resid_mid = x + proj(ctx, lw["o"], *_lora(lw, "o"), s)
     xn2 = rmsnorm(resid_mid, lw["post_ln"], eps)
     if saved_gate_up is not None:
         inter = saved_gate_up.shape[-1] // 2
@@ -388,11 +407,16 @@ class Model:
         return self.meta.get("family", "llama3") == "qwen3"
 
 
-def forward_capture(model: Model, ids, seq_lens, save_gate_up=False):
+def forward_capture(model: Model, ids, seq_lens, save_gate_up=False, save_attn_qkv=False,
+                    save_attn_ctx=False, save_resid_mid=False):
     """Full forward → the activation dict process_backward consumes
     (tests/bwd_harness.py:242-258): layer_in[i], final_in, concat_input_ids,
     and with ``save_gate_up`` the per-layer gate‖up projection outputs of the
-    ``mlp_gate_up`` save point (accumulate.py:134-135, :174)."""
+    ``mlp_gate_up`` save point (accumulate.py:134-135, :174). The other save
+    points (accumulate.py:213-235): ``attn_qh/kh/vh`` flat [n, q|kv] — q/k
+    after RoPE for Llama-3 (the attention call's inputs), before the q/k-norm
+    for Qwen3 (``Family.saved_qkv_pre_transform``, family.py:75-84) —,
+    ``attn_ctx`` [n, q] and ``resid_mid`` [n, D]."""
     m = model.meta
     b_start, positions, *_ = pack(seq_lens)
     dev = model.embed.device
@@ -400,16 +424,25 @@ def forward_capture(model: Model, ids, seq_lens, save_gate_up=False):
                             device=dev)
     s, eps = m["lora_scaling"], m["rms_norm_eps"]
     x = model.embed[ids.to(dev).long()]
-    layer_in, gate_up = [], []
+    n = x.shape[0]
+    saved = {k: [] for k in ("mlp_gate_up", "attn_qh", "attn_kh", "attn_vh", "attn_ctx",
+                             "resid_mid")}
+    layer_in = []
     for lw in model.layers:
         layer_in.append(x)
         c = layer_forward(x, lw, s, cos, sin, seq_lens, b_start, model.dims, eps, model.qk_norm)
-        if save_gate_up:
-            gate_up.append(torch.cat([c["gate"], c["up"]], dim=1))
+        saved["mlp_gate_up"].append(torch.cat([c["gate"], c["up"]], dim=1))
+        q, k = (c["q_pre"], c["k_pre"]) if model.qk_norm else (c["qh"], c["kh"])
+        saved["attn_qh"].append(q.reshape(n, -1))
+        saved["attn_kh"].append(k.reshape(n, -1))
+        saved["attn_vh"].append(c["vh"].reshape(n, -1))
+        saved["attn_ctx"].append(c["ctx"])
+        saved["resid_mid"].append(c["resid_mid"])
         x = layer_output(c, lw, s)
     out = {"layer_in": layer_in, "final_in": x, "concat_input_ids": ids}
-    if save_gate_up:
-        out["mlp_gate_up"] = gate_up
+    keep = {"mlp_gate_up": save_gate_up, "attn_qh": save_attn_qkv, "attn_kh": save_attn_qkv,
+            "attn_vh": save_attn_qkv, "attn_ctx": save_attn_ctx, "resid_mid": save_resid_mid}
+    out.update({k: v for k, v in saved.items() if keep[k]})
     return out
 
 
@@ -429,6 +462,13 @@ def process_backward(model: Model, activations, seq_lens, n, lr, step, clip=True
     s, eps = m["lora_scaling"], m["rms_norm_eps"]
     ids = activations["concat_input_ids"][:n]
     saved_gu = activations.get("mlp_gate_up")
+    # the optional save points, gated as the trainer gates them
+    # (trainer.py:160-177, :532-552): q/k/v and resid_mid only when the meta
+    # says the worker saves them, the context whenever it is there
+    qkv_on = bool(m.get("save_attn_qkv")) and all(
+        activations.get(k) is not None for k in ("attn_qh", "attn_kh", "attn_vh"))
+    ctx_all = activations.get("attn_ctx")
+    rm_all = activations.get("resid_mid") if m.get("save_resid_mid") else None
     loss, n_valid, g = head_backward(activations["final_in"][:n].float(), model.lm_w,
                                      model.norm_w, eps, ids, seq_lens)
     grads = [None] * len(model.layers)
@@ -436,8 +476,13 @@ def process_backward(model: Model, activations, seq_lens, n, lr, step, clip=True
         lw = model.layers[i]
         x = activations["layer_in"][i][:n].float()
         gu = None if saved_gu is None else saved_gu[i][:n].float()
+        sq = None
+        if qkv_on:
+            sq = tuple(activations[k][i][:n].float() for k in ("attn_qh", "attn_kh", "attn_vh"))
         c = layer_forward(x, lw, s, cos, sin, seq_lens, b_start, model.dims, eps, model.qk_norm,
-                          saved_gate_up=gu)
+                          saved_gate_up=gu, saved_qkv=sq,
+                          saved_ctx=None if ctx_all is None else ctx_all[i][:n].float(),
+                          saved_resid_mid=None if rm_all is None else rm_all[i][:n].float())
         g, gr = layer_backward(g, c, lw, s, cos, sin, seq_lens, b_start, model.dims, eps,
                                model.qk_norm)
         if clip and gr:

@@ -103,13 +103,20 @@ def gpu_activations(acts, s_max, device="cuda"):
     ids[:n] = acts["concat_input_ids"].to(device)
     out = {"layer_in": [buf(t) for t in acts["layer_in"]], "final_in": buf(acts["final_in"]),
            "concat_input_ids": ids}
-    if "mlp_gate_up" in acts:
-        def gbuf(t):
-            b = torch.zeros(s_max + 1, t.shape[1], dtype=torch.bfloat16, device=device)
-            b[:n] = t.to(device=device, dtype=torch.bfloat16)
-            return b
-        out["mlp_gate_up"] = [gbuf(t) for t in acts["mlp_gate_up"]]
+
+    def wbuf(t):
+        b = torch.zeros(s_max + 1, t.shape[1], dtype=torch.bfloat16, device=device)
+        b[:n] = t.to(device=device, dtype=torch.bfloat16)
+        return b
+
+    for key in SAVE_POINTS:
+        if key in acts:
+            out[key] = [wbuf(t) for t in acts[key]]
     return out
+
+
+# the optional per-layer save points of the activation store (accumulate.py:208-235)
+SAVE_POINTS = ("mlp_gate_up", "attn_qh", "attn_kh", "attn_vh", "attn_ctx", "resid_mid")
 
 
 def bf16_round_acts(acts):
@@ -117,8 +124,9 @@ def bf16_round_acts(acts):
     out = {"layer_in": [t.to(torch.bfloat16).float() for t in acts["layer_in"]],
            "final_in": acts["final_in"].to(torch.bfloat16).float(),
            "concat_input_ids": acts["concat_input_ids"]}
-    if "mlp_gate_up" in acts:
-        out["mlp_gate_up"] = [t.to(torch.bfloat16).float() for t in acts["mlp_gate_up"]]
+    for key in SAVE_POINTS:
+        if key in acts:
+            out[key] = [t.to(torch.bfloat16).float() for t in acts[key]]
     return out
 
 
@@ -191,7 +199,7 @@ def unexplained_master_misses(w_got, w_ref, steps, bar=2e-2):
 
 
 def cycle_parity(meta, seq_lens, projs=O.PROJS, steps=2, seed=0, w_std=0.05, b_std=0.02,
-                 norm_jitter=0.2, ref_device="cpu", save_gate_up=False):
+                 norm_jitter=0.2, ref_device="cpu", save_gate_up=False, saves=()):
     """Runs ``steps`` cycles of LoraSftTrainerService.process_backward (libdsb,
     one hipGraph) and of the oracle's process_backward on the same seeded
     model and activations; returns the worst gradient / master max-relative
@@ -200,12 +208,17 @@ def cycle_parity(meta, seq_lens, projs=O.PROJS, steps=2, seed=0, w_std=0.05, b_s
     BASELINE-width slices)."""
     if ref_device != "cpu":
         fp32_reference_mode()
+    # ``saves``: the other save points ("attn_qkv", "attn_ctx", "resid_mid"),
+    # with the meta keys the worker sets when it captures them
+    meta = dict(meta, **{"save_" + name: True for name in saves
+                         if name in ("attn_qkv", "resid_mid")})
     model = O.make_model(meta, seed=seed, projs=projs, w_std=w_std, b_std=b_std,
                          norm_jitter=norm_jitter, device=ref_device)
     n = sum(seq_lens)
     ids = torch.randint(0, meta["vocab_size"], (n,), generator=torch.Generator().manual_seed(seed + 1))
-    acts = bf16_round_acts(O.forward_capture(model, ids.to(ref_device), seq_lens,
-                                             save_gate_up=save_gate_up))
+    acts = bf16_round_acts(O.forward_capture(
+        model, ids.to(ref_device), seq_lens, save_gate_up=save_gate_up,
+        **{"save_" + name: True for name in saves}))
     svc = build_service(model, meta["family"])
     gacts = gpu_activations(acts, meta["max_saved_finetuning_tokens"])
     ref = clone_model(model)

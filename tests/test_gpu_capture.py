@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from harness import O, build_service, gpu_activations, tiny_meta
+from harness import O, bf16_round_acts, build_service, gpu_activations, tiny_meta
 
 pytestmark = pytest.mark.gpu
 
@@ -300,3 +300,65 @@ def test_gate_up_slot_feeds_the_saved_path():
         one.close()
         two.close()
         three.close()
+
+
+@pytest.mark.parametrize("family", ["llama3", "qwen3"])
+def test_every_save_point_filled_by_the_op_feeds_the_cycle(family):
+    """A store with every opt-in save point (accumulate.py:213-235): the
+    op writes q/k/v (Llama-3 after RoPE, Qwen3 before the q/k-norm), the
+    attention context, the post-attention residual and the final hidden
+    state into their slots bit-exact; ``activations()`` hands them over;
+    with the worker's save_attn_qkv / save_resid_mid meta keys the cycle on
+    the store equals the same buffers handed over directly, and the capture
+    check (verify_activations, trainer.py:806-826) passes on it."""
+    C = _capture()
+    meta = tiny_meta(family=family, L=2)
+    model = O.make_model(meta, seed=21, w_std=0.05, b_std=0.02, norm_jitter=0.2)
+    S, D, Lyr = meta["max_saved_finetuning_tokens"], meta["hidden_size"], 2
+    q_size = meta["num_attention_heads"] * 128
+    kv_size = meta["num_key_value_heads"] * 128
+    n = sum(SEQ)
+    ids = torch.randint(0, meta["vocab_size"], (n,), generator=torch.Generator().manual_seed(21))
+    acts = O.forward_capture(model, ids, SEQ, save_gate_up=True, save_attn_qkv=True,
+                             save_attn_ctx=True, save_resid_mid=True)
+    final_hidden = O.rmsnorm(acts["final_in"], model.norm_w, meta["rms_norm_eps"])
+    store = C.ActivationStore(Lyr, D, S, intermediate_size=meta["intermediate_size"],
+                              q_size=q_size, kv_size=kv_size, save_attn_qkv=True,
+                              save_attn_ctx=True, save_resid_mid=True, save_final_hidden=True)
+    slots = {"layer_in": C.SLOT_LAYER_IN, "mlp_gate_up": C.SLOT_GATE_UP,
+             "resid_mid": C.SLOT_RESID_MID, "attn_qh": C.SLOT_QH, "attn_kh": C.SLOT_KH,
+             "attn_vh": C.SLOT_VH, "attn_ctx": C.SLOT_CTX}
+    st = store.begin_step(None, n, 0, start=0, contiguous=True)
+    for i in range(Lyr):
+        for name, kind in slots.items():
+            store.save(store.slot(i, kind), acts[name][i].to(torch.bfloat16).cuda())
+    store.save(store.final_slot, acts["final_in"].to(torch.bfloat16).cuda())
+    store.accumulate_final(ids.cuda(), final_hidden.to(torch.bfloat16).cuda())
+    store.end_step()
+    torch.cuda.synchronize()
+    got = store.activations()
+    for name in slots:
+        for i in range(Lyr):
+            assert torch.equal(got[name][i][:n].cpu(), acts[name][i].to(torch.bfloat16)), (name, i)
+    assert torch.equal(got["final_hidden"][:n].cpu(), final_hidden.to(torch.bfloat16))
+    assert st.src.shape[0] == S
+
+    direct = gpu_activations(bf16_round_acts(acts), S)
+    svcs = [build_service(model, family) for _ in range(2)]
+    try:
+        for svc in svcs:
+            svc.shared["meta"].update(save_attn_qkv=True, save_resid_mid=True)
+        checks = svcs[0].verify_activations(got, n)
+        assert checks and all(ok for _, _, ok in checks), checks
+        l1, n1 = svcs[0].process_backward(got, SEQ, n, epoch=0)
+        l2, n2 = svcs[1].process_backward(direct, SEQ, n, epoch=0)
+        assert svcs[0].saved_points == ["attn_ctx", "attn_kh", "attn_qh", "attn_vh",
+                                        "mlp_gate_up", "resid_mid"]
+        assert n1 == n2 and l1 == l2, (l1, l2)
+        for i, d in svcs[0].lora.items():
+            for p, dd in d.items():
+                for ab, t in dd.items():
+                    assert torch.equal(t.grad, svcs[1].lora[i][p][ab].grad), (i, p, ab)
+    finally:
+        for svc in svcs:
+            svc.close()

@@ -92,3 +92,17 @@ def test_c3_saved_gate_up():
                          ref_device="cuda", save_gate_up=True)
     _report("c3 saved gate_up", worst)
     assert_north_star(worst, direct_masters=False)
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_all_save_points(name):
+    """Every save point of the store bound at the config's widths: gate‖up,
+    q/k/v (Llama-3 post-RoPE, Qwen3 pre-norm), the attention context and the
+    post-attention residual, so the layer recompute is the input RMSNorm,
+    the LoRA Z passes and the attention forward (trainer.py:532-552)."""
+    meta, lens = config_meta(name, L=1)
+    worst = cycle_parity(meta, lens, w_std=0.02, b_std=0.01, norm_jitter=0.0,
+                         ref_device="cuda", save_gate_up=True,
+                         saves=("attn_qkv", "attn_ctx", "resid_mid"))
+    _report(f"{name} all save points", worst)
+    assert_north_star(worst, direct_masters=False)

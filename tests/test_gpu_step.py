@@ -130,6 +130,62 @@ def test_saved_gate_up_matches_recompute():
         b.close()
 
 
+SAVE_CASES = [("attn_qkv",), ("attn_ctx",), ("resid_mid",), ("attn_qkv", "attn_ctx", "resid_mid")]
+
+
+@pytest.mark.parametrize("family", ["llama3", "qwen3"])
+@pytest.mark.parametrize("saves", SAVE_CASES, ids=["+".join(c) for c in SAVE_CASES])
+def test_cycle_parity_saved_points(family, saves):
+    """The optional save points (trainer.py:532-552; llama3.py:62-142,
+    qwen3.py:68-130): saved q/k/v skip the Q/K/V projection (and Llama-3's
+    RoPE), the saved post-attention residual skips the O projection, the
+    saved context feeds the O projection. Against the oracle fed the same
+    saved values, at the north-star bars, with the 256-wide tiles and batched
+    LoRA passes of the production shapes."""
+    meta = tiny_meta(family=family, L=2, D=512, Hq=4, Hkv=2, I=768, r=16, s_max=700)
+    worst = _run(meta, [37, 128, 1, 200, 64], saves=saves, save_gate_up=True)
+    assert_north_star(worst)
+
+
+@pytest.mark.parametrize("family", ["llama3", "qwen3"])
+def test_saved_points_match_recompute(family):
+    """Saved-shortcut == recompute (test_llama3_backward_graph.py:271-311):
+    with the store holding the forward's own q/k/v, context and residual
+    mid-point, a cycle gives the recompute cycle's gradients up to the bf16
+    rounding of the stored values; without the worker's save_attn_qkv /
+    save_resid_mid meta keys those buffers are not read at all (the cycle is
+    bit-identical to the recompute cycle)."""
+    meta = tiny_meta(family=family, L=2, r=16)
+    model = O.make_model(meta, seed=4, w_std=0.05, b_std=0.02, norm_jitter=0.2)
+    seq = [37, 128, 1, 200, 64]
+    n = sum(seq)
+    ids = torch.randint(0, meta["vocab_size"], (n,), generator=torch.Generator().manual_seed(9))
+    acts = bf16_round_acts(O.forward_capture(model, ids, seq, save_attn_qkv=True,
+                                             save_resid_mid=True))
+    plain = {k: v for k, v in acts.items() if k in ("layer_in", "final_in", "concat_input_ids")}
+    a = build_service(model, "llama3" if family == "llama3" else "qwen3")
+    b = build_service(model, "llama3" if family == "llama3" else "qwen3")
+    c = build_service(model, "llama3" if family == "llama3" else "qwen3")
+    b.shared["meta"].update(save_attn_qkv=True, save_resid_mid=True)
+    try:
+        la, na = a.process_backward(gpu_activations(plain, 512), seq, n, epoch=0)
+        lb, nb = b.process_backward(gpu_activations(acts, 512), seq, n, epoch=0)
+        lc, nc = c.process_backward(gpu_activations(acts, 512), seq, n, epoch=0)
+        assert b.saved_points == ["attn_kh", "attn_qh", "attn_vh", "resid_mid"]
+        assert c.saved_points == []
+        assert na == nb == nc and abs(la - lb) / la < 1e-3 and la == lc
+        for i, d in a.lora.items():
+            for p, dd in d.items():
+                for ab in "AB":
+                    ga, gb, gc = dd[ab].grad, b.lora[i][p][ab].grad, c.lora[i][p][ab].grad
+                    assert max_rel(gb, ga) < 2e-2 and cosine(gb, ga) > 0.999, (i, p, ab)
+                    assert torch.equal(gc, ga), (i, p, ab)
+    finally:
+        a.close()
+        b.close()
+        c.close()
+
+
 def test_cycle_many_short_sequences():
     """A packing of many short samples (more than the attention grid of the
     first capture holds): the cycle captures a graph for the larger tile

@@ -571,6 +571,78 @@ def test_saved_gate_up_equals_recompute():
     check_saved_gate_up()
 
 
+def check_saved_points(family, capture=O.forward_capture):
+    """The other save points (trainer.py:532-552, llama3.py:62-142,
+    qwen3.py:68-130): the cycle fed the forward's own q/k/v (Llama-3 after
+    RoPE, Qwen3 before its q/k-norm), attention context and post-attention
+    residual — each alone and all together — gives the recompute cycle's loss
+    and gradients. The meta keys gate q/k/v and resid_mid as the trainer
+    does: without them the buffers are ignored."""
+    meta = tiny_meta(family=family, L=2, D=128, Hq=2, Hkv=1, I=160, V=97, r=4)
+    model = O.make_model(meta, seed=13, w_std=0.08, b_std=0.05, norm_jitter=0.2)
+    seq_lens = [6, 11]
+    ids = torch.randint(0, 97, (17,), generator=torch.Generator().manual_seed(4))
+    acts = capture(model, ids, seq_lens, save_attn_qkv=True, save_attn_ctx=True,
+                   save_resid_mid=True)
+    base_keys = ("layer_in", "final_in", "concat_input_ids")
+    plain = {k: acts[k] for k in base_keys}
+    l1, n1, g1 = O.process_backward(model, plain, seq_lens, 17, lr=0.0, step=1, update=False)
+    cases = [(("attn_qh", "attn_kh", "attn_vh"), {"save_attn_qkv": True}),
+             (("attn_ctx",), {}), (("resid_mid",), {"save_resid_mid": True}),
+             (("attn_qh", "attn_kh", "attn_vh", "attn_ctx", "resid_mid"),
+              {"save_attn_qkv": True, "save_resid_mid": True})]
+    for keys, flags in cases:
+        model.meta.update(flags)
+        try:
+            a = dict(plain, **{k: acts[k] for k in keys})
+            l2, n2, g2 = O.process_backward(model, a, seq_lens, 17, lr=0.0, step=1, update=False)
+        finally:
+            for f in flags:
+                model.meta.pop(f)
+        assert n1 == n2 and abs(l1 - l2) < 1e-6 * abs(l1), keys
+        for x, y in zip(g1, g2):
+            for k in x:
+                assert _rel(y[k], x[k]) < 1e-5, (keys, k)
+
+
+@pytest.mark.parametrize("family", ["llama3", "qwen3"])
+def test_saved_points_equal_recompute(family):
+    check_saved_points(family)
+
+
+def test_saved_qkv_ignored_without_the_meta_flag():
+    """trainer.py:539-544: q/k/v buffers are read only with save_attn_qkv on;
+    corrupted buffers then change nothing."""
+    meta = tiny_meta(L=1, D=128, Hq=2, Hkv=1, I=160, V=97, r=4)
+    model = O.make_model(meta, seed=14, w_std=0.08, b_std=0.05)
+    seq_lens = [9]
+    ids = torch.randint(0, 97, (9,), generator=torch.Generator().manual_seed(5))
+    acts = O.forward_capture(model, ids, seq_lens, save_attn_qkv=True, save_resid_mid=True)
+    junk = dict(acts, attn_qh=[t * 0 + 3 for t in acts["attn_qh"]],
+                resid_mid=[t * 0 - 1 for t in acts["resid_mid"]])
+    la, _, ga = O.process_backward(model, acts, seq_lens, 9, lr=0.0, step=1, update=False)
+    lb, _, gb = O.process_backward(model, junk, seq_lens, 9, lr=0.0, step=1, update=False)
+    assert la == lb and all(torch.equal(x[k], y[k]) for x, y in zip(ga, gb) for k in x)
+
+
+def _bad_capture_qk_before_rope(model, ids, seq_lens, **kw):  # Llama-3 q/k saved pre-RoPE
+    acts = O.forward_capture(model, ids, seq_lens, **kw)
+    m = model.meta
+    _, positions, *_ = O.pack(seq_lens)
+    cos, sin = O.rope_cos_sin(positions, m["head_dim"], m["rope_theta"])
+    n = len(positions)
+    for key, H in (("attn_qh", m["num_attention_heads"]), ("attn_kh", m["num_key_value_heads"])):
+        acts[key] = [O.rope_backward(t.reshape(n, H, -1), cos, sin).reshape(n, -1)
+                     for t in acts[key]]
+    return acts
+
+
+def _bad_capture_resid(model, ids, seq_lens, **kw):  # resid_mid without the residual x
+    acts = O.forward_capture(model, ids, seq_lens, **kw)
+    acts["resid_mid"] = [r - x for r, x in zip(acts["resid_mid"], acts["layer_in"])]
+    return acts
+
+
 def _bad_capture_gate_up(model, ids, seq_lens, save_gate_up=False):  # halves stored up‖gate
     acts = O.forward_capture(model, ids, seq_lens, save_gate_up=save_gate_up)
     I = acts["mlp_gate_up"][0].shape[1] // 2
@@ -763,6 +835,8 @@ PLANTED = {
     "adamw_bias_correction": lambda: check_adamw(_bad_adamw),
     "cycle_lora_scale": lambda: check_cycle(_bad_cycle, "llama3", projs=("q", "v")),
     "saved_gate_up_order": lambda: check_saved_gate_up(_bad_capture_gate_up),
+    "saved_qk_rope_side": lambda: check_saved_points("llama3", _bad_capture_qk_before_rope),
+    "saved_resid_mid_residual": lambda: check_saved_points("qwen3", _bad_capture_resid),
 }
 
 
