@@ -11,27 +11,25 @@
 // fetched by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds; 8 lanes
 // cover one row, so every request is a whole 128-byte line) into one of two
 // LDS stages. Each wave owns a (BM/WM)×(BN/WN) sub-tile of
-// v_mfma_f32_32x32x16_bf16 accumulators. Per K step (four 16-deep slices,
-// slice 0 already in registers): MFMAs of slice s, with the fragment reads
-// of slice s+1 issued one after each of the first MFMAs and the stage loads
-// one after each of the later ones; before the last slice: wait for the own
-// loads and reads → barrier → MFMAs of slice 3 with the reads of slice 0 of
-// stage kt+1 and the first half of stage kt+2's loads (the second half goes
-// with slice 0 of the next step). A wave issues at most one instruction every
-// few cycles, so anything issued in bursts between MFMAs idles the matrix
-// pipe; one or two instructions between MFMAs issue in the shadow of the
-// previous MFMA.
-// The one barrier per step publishes stage kt+1 (every wave's loads landed)
-// and retires stage kt (every wave's reads of it returned), so the loads
-// after it can fill that slot. Past the end of K the loads zero-fill the slot
-// without touching memory, so the waits are constants.
+// v_mfma_f32_16x16x32_bf16 accumulators, tied to their AGPRs by inline-asm
+// MFMAs (with the builtin the compiler gave each MFMA's result registers
+// other than its accumulator's and moved every accumulator back at the end
+// of each iteration: 400 moves per K step). A K step is two 32-deep slices:
+// the first half of slice 0's MFMAs carries the fragment reads of slice 1
+// (one after each MFMA); then every wave's reads of stage kt have returned
+// and its loads of stage kt+1 have landed, so one barrier publishes stage
+// kt+1 and frees stage kt's slot; the rest of the step's MFMAs carry the
+// loads of stage kt+2 into that slot (one after every other MFMA) and, in
+// slice 1, the reads of slice 0 of stage kt+1. Loads get about one step of
+// latency budget. Past the end of K the loads zero-fill the slot without
+// touching memory, so the waits are constants.
 //
 // LDS layout per stage and operand: rows of 128 B (64 bf16) as eight 16-byte
 // chunks; chunk c of row r sits in slot c ^ f(r), f(r) = ((r>>1)&7) ^ ((r&1)<<2),
-// which makes the 32-row fragment reads conflict-free for both 128-byte and
-// 256-byte bank windows. The loads write LDS linearly (lane i of a load lands
-// at byte 16·i of its 1 KB segment = 8 rows), so the swizzle is applied on
-// the global side: the lane filling slot s of row r fetches chunk s ^ f(r).
+// which makes the 16-row fragment reads (one chunk of 16 consecutive rows per
+// quarter-wave) conflict-free. The loads write LDS linearly (lane i of a load
+// lands at byte 16·i of its 1 KB segment = 8 rows), so the swizzle is applied
+// on the global side: the lane filling slot s of row r fetches chunk s ^ f(r).
 // Out-of-range rows (past M or N) and chunks past K are fetched from an offset
 // outside the buffer descriptor and land as zeros.
 //
@@ -93,62 +91,71 @@ DSB_DEV void tile_map(int bid, int nbm, int nbn, int& pm, int& pn) {
   pn = r / gsz;
 }
 
-// Visit the accumulator as runs of 4 consecutive output columns of one row.
-template <int FM, int FN, class F>
-DSB_DEV void for_each_quad(const f32x16 (&acc)[FM][FN], int mw, int nw, int M,
-                           int lane, F&& f) {
-  const int lr = lane & 31, lh = lane >> 5;
+// acc += A-fragment × B-fragment with the accumulator tied to its four AGPRs.
+// Operands: lane l supplies row l%16 of its 16-row block with K-values
+// 8·(l/16) .. +7 of the slice; lane l then holds output row l%16 of the
+// A block against columns 4·(l/16) .. +3 of the B block (mfma16 with the B
+// fragment first). The compiler cannot see the MFMA's latency through the
+// asm: a kernel waits before reading the accumulators (mfma_drain).
+DSB_DEV void mfma16_acc(f32x4& acc, bf16x8 b, bf16x8 a) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(b), "v"(a));
+}
+// Wait states covering the last MFMA's result (4 passes) before the
+// accumulators are read.
+DSB_DEV void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+
+// buffer_load_dwordx4 ... lds with M0 set and not restored: the GEMM kernels
+// issue no other instruction that reads M0 (checked on their assembly), so
+// the three scalar instructions per load of a save/restore are not needed.
+DSB_DEV void lds_dma16_m0(u32x4 rsrc, int voff, unsigned lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(lds_addr)
+      : "memory", "m0");
+}
+
+// Writes 32-row block b (rows 32b .. 32b+31 of the wave tile) of the
+// accumulators, row-major at `buf` (row pitch PITCH floats): acc[2b + h][fn]
+// of lane l is row 16h + l%16, columns 16fn + 4(l/16) .. +3.
+template <int FM, int FN, int PITCH>
+DSB_DEV void stage32(const f32x4 (&acc)[FM][FN], int b, float* buf, int lane) {
+  const int l16 = lane & 15, lq = lane >> 4;
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    const int m = mw + fm * 32 + lr;
-    if (m >= M) continue;
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = nw + fn * 32 + 8 * g + 4 * lh;
-        float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1],
-                      acc[fm][fn][4 * g + 2], acc[fm][fn][4 * g + 3]};
-        f(m, n, v);
-      }
-    }
-  }
+    for (int fn = 0; fn < FN; ++fn)
+      *reinterpret_cast<f32x4*>(buf + (16 * h + l16) * PITCH + fn * 16 + 4 * lq) = acc[2 * b + h][fn];
 }
 
 // Visit the wave's accumulator tile as runs of 8 consecutive output columns
 // of one row (n a multiple of 8), staged through the wave's own LDS region
-// (32 rows × TN fp32, row pitch TN + 4 floats) one 32-row fragment row at a
-// time, so TN/8 consecutive lanes cover one row and every global access of
-// the epilogue is a 16- or 32-byte row-contiguous transfer. Needs
+// (32 rows × TN fp32, row pitch TN + 4 floats) one 32-row block at a time,
+// so TN/8 consecutive lanes cover one row and every global access of the
+// epilogue is a 16- or 32-byte row-contiguous transfer. Needs
 // 32·(TN + 4)·4 bytes of LDS per wave at `smem`; wave-local (a wave's LDS
 // accesses complete in order), so no barrier beyond the one before the
 // epilogue.
 template <int FM, int FN, class F>
-DSB_DEV void for_each_row8(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
+DSB_DEV void for_each_row8(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane,
                            int wave, void* smem, F&& f) {
-  constexpr int TN = FN * 32, PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG;
-  static_assert(64 % CG == 0, "row groups");
+  constexpr int TN = FN * 16, PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG;
+  static_assert(64 % CG == 0 && FM % 2 == 0, "row groups");
   float* buf = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
-  const int lr = lane & 31, lh = lane >> 5;
   const int rsub = lane / CG, cg = lane % CG;
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    if (mw + fm * 32 >= M) break;  // uniform: the rest of the wave tile is past M
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                         acc[fm][fn][4 * g + 3]};
-        *reinterpret_cast<f32x4*>(buf + lr * PITCH + fn * 32 + 8 * g + 4 * lh) = v;
-      }
+  for (int b = 0; b < FM / 2; ++b) {
+    if (mw + b * 32 >= M) break;  // uniform: the rest of the wave tile is past M
+    stage32<FM, FN, PITCH>(acc, b, buf, lane);
 #pragma unroll
     for (int it = 0; it < 32 / RPI; ++it) {
       const int row = it * RPI + rsub;
-      const f32x4 a = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
-      float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-      const int m = mw + fm * 32 + row;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
+      float v[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+      const int m = mw + b * 32 + row;
       if (m < M) f(m, nw + cg * 8, v);
     }
   }
@@ -162,43 +169,35 @@ DSB_DEV void for_each_row8(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, i
 // latency is spent under the epilogue's other work instead of stalling every
 // row (reading them in `f` left one global-load latency per 4 rows).
 template <int FM, int FN, class L, class F>
-DSB_DEV void for_each_row8_pf(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
+DSB_DEV void for_each_row8_pf(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane,
                               int wave, void* smem, L&& load, F&& f) {
-  constexpr int TN = FN * 32, PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG, IT = 32 / RPI;
-  static_assert(64 % CG == 0, "row groups");
+  constexpr int TN = FN * 16, PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG, IT = 32 / RPI;
+  static_assert(64 % CG == 0 && FM % 2 == 0, "row groups");
   using T = decltype(load(0, 0));
   float* buf = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
-  const int lr = lane & 31, lh = lane >> 5;
   const int rsub = lane / CG, cg = lane % CG;
   T pf[2][IT];
-  auto issue = [&](int fm, T (&dst)[IT]) {
+  auto issue = [&](int b, T (&dst)[IT]) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int m = mw + fm * 32 + it * RPI + rsub;
+      const int m = mw + b * 32 + it * RPI + rsub;
       dst[it] = m < M ? load(m, nw + cg * 8) : T{};
     }
   };
   if (mw < M) issue(0, pf[0]);
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    if (mw + fm * 32 >= M) break;  // uniform: the rest of the wave tile is past M
-    if (fm + 1 < FM && mw + (fm + 1) * 32 < M) issue(fm + 1, pf[(fm + 1) & 1]);
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                         acc[fm][fn][4 * g + 3]};
-        *reinterpret_cast<f32x4*>(buf + lr * PITCH + fn * 32 + 8 * g + 4 * lh) = v;
-      }
+  for (int b = 0; b < FM / 2; ++b) {
+    if (mw + b * 32 >= M) break;  // uniform: the rest of the wave tile is past M
+    if (b + 1 < FM / 2 && mw + (b + 1) * 32 < M) issue(b + 1, pf[(b + 1) & 1]);
+    stage32<FM, FN, PITCH>(acc, b, buf, lane);
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int row = it * RPI + rsub;
-      const f32x4 a = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
-      float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-      const int m = mw + fm * 32 + row;
-      if (m < M) f(m, nw + cg * 8, v, pf[fm & 1][it]);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
+      float v[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+      const int m = mw + b * 32 + row;
+      if (m < M) f(m, nw + cg * 8, v, pf[b & 1][it]);
     }
   }
 }
@@ -253,7 +252,7 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   constexpr int BK = 64;
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
-  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int FM = TM / 16, FN = TN / 16;
   // direct-to-LDS loads per lane per stage: one load = 64 lanes × 16 B = 8 rows
   constexpr int IA = BM / (8 * NW), IB = BN / (8 * NW), IAB = IA + IB;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be 32-aligned");
@@ -356,74 +355,65 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   };
   auto issue_one = [&](const Fill& f, int j) {
     if (j < IA)
-      lds_dma16(f.dA, f.voA + j * f.stA, f.dst + j * 8 * NW * BK * 2);
+      lds_dma16_m0(f.dA, f.voA + j * f.stA, f.dst + j * 8 * NW * BK * 2);
     else
-      lds_dma16(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]),
-                f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+      lds_dma16_m0(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]),
+                   f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
   };
 
-  f32x16 acc[FM][FN];
+  f32x4 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
 
-  const int lr = lane & 31, lh = lane >> 5;
-  // Fragment rows are 32 apart, so the swizzle depends on lr only. Slice s
-  // of the stage (K 16s .. 16s+15) is chunk 2s + lh of the lane's row.
-  const int g = lds_swz(lr);
-  const int arow = (wm * TM + lr) * BK, brow = SA + (wn * TN + lr) * BK;
+  const int l16 = lane & 15, lq = lane >> 4;
+  // Fragment rows are 16 apart, so the swizzle depends on l16 only. Slice s
+  // of the stage (K 32s .. 32s+31) is chunk 4s + lq of the lane's row.
+  const int g = lds_swz(l16);
+  const int arow = (wm * TM + l16) * BK, brow = SA + (wn * TN + l16) * BK;
   bf16x8 af[2][FM], bfr[2][FN];
-  auto read = [&](const bf16* b, int s, int buf) {
-    const int ch = ((2 * s + lh) ^ g) << 3;
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-      af[buf][fm] = *reinterpret_cast<const bf16x8*>(b + arow + ch + fm * 32 * BK);
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-      bfr[buf][fn] = *reinterpret_cast<const bf16x8*>(b + brow + ch + fn * 32 * BK);
-  };
   // Fragment i of slice s into buffer `buf`: A fragment i (i < FM), else B
   // fragment i - FM.
   auto read_one = [&](const bf16* b, int s, int buf, int i) {
-    const int ch = ((2 * s + lh) ^ g) << 3;
+    const int ch = ((4 * s + lq) ^ g) << 3;
     if (i < FM)
-      af[buf][i] = *reinterpret_cast<const bf16x8*>(b + arow + ch + i * 32 * BK);
+      af[buf][i] = *reinterpret_cast<const bf16x8*>(b + arow + ch + i * 16 * BK);
     else
-      bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(b + brow + ch + (i - FM) * 32 * BK);
+      bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(b + brow + ch + (i - FM) * 16 * BK);
   };
-  // MFMAs of the slice held in `buf`. The FM+FN fragment reads of the next
-  // slice (slice ns of the stage at nb, into buffer nbuf) go one after each
-  // of the first MFMAs, then loads j0 .. j0+nj-1 of `f` one after each of
-  // the following ones. A wave issues at most one instruction every few
-  // cycles, so bursts of reads or loads between MFMAs would leave the matrix
-  // pipe idle; one or two instructions between MFMAs issue while the
-  // previous MFMA runs.
-  auto mma = [&](int buf, const bf16* nb, int ns, int nbuf, const Fill& f, int j0, int nj) {
-    constexpr int NM = FM * FN, NR = FM + FN;
-    int r = 0, j = j0;
+  constexpr int NM = FM * FN, NR = FM + FN, H1 = IAB / 2;
+  // MFMAs t0 .. t1-1 of the slice held in `buf`, each followed by one other
+  // instruction while there are any: first the fragment reads 0 .. nr-1 of
+  // slice ns of the stage at nb (into buffer nbuf), one after each MFMA,
+  // then loads j0 .. j0+nj-1 of f, one after every other MFMA. A wave issues
+  // at most one instruction every few cycles, so a burst of other
+  // instructions between MFMAs would leave the matrix pipe idle.
+  auto mma = [&](int buf, int t0, int t1, const bf16* nb, int ns, int nbuf, int nr,
+                 const Fill& f, int j0, int nj) {
+    int r = 0, j = 0;
 #pragma unroll
-    for (int t = 0; t < NM; ++t) {
+    for (int t = t0; t < t1; ++t) {
       const int fm = t / FN, fn = t % FN;
-      acc[fm][fn] = mfma32(bfr[buf][fn], af[buf][fm], acc[fm][fn]);
-      if (r < NR) {
+      mfma16_acc(acc[fm][fn], bfr[buf][fn], af[buf][fm]);
+      if (r < nr) {
         __builtin_amdgcn_sched_barrier(0);
         read_one(nb, ns, nbuf, r++);
         __builtin_amdgcn_sched_barrier(0);
-      } else if (j < j0 + nj) {
+      } else if (j < nj && (t & 1) == 1) {
         __builtin_amdgcn_sched_barrier(0);
-        issue_one(f, j++);
+        issue_one(f, j0 + j++);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
     for (int rr = 0; rr < NR; ++rr)
-      if (rr >= r) read_one(nb, ns, nbuf, rr);
+      if (rr >= r && rr < nr) read_one(nb, ns, nbuf, rr);
 #pragma unroll
     for (int jj = 0; jj < IAB; ++jj)
-      if (jj >= j && jj < j0 + nj) issue_one(f, jj);
+      if (jj >= j && jj < nj) issue_one(f, j0 + jj);
   };
   // Loads of K tile kt (< nk1, first segment) into slot `slot`: the
   // descriptors and row offsets are the loop-invariant ones of segment 1.
@@ -441,17 +431,8 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     return f;
   };
 
-  // Two stages of BK = 64. Step kt computes on slot kt&1 while the loads of
-  // stage kt+1 fill the other slot. The step's barrier sits before its last
-  // slice: by then every wave has its own loads of stage kt+1 landed
-  // (vmcnt 0) and its fragment reads of stage kt returned (lgkmcnt 0), so the
-  // barrier both publishes stage kt+1 and frees slot kt&1. After it, the
-  // first slice of stage kt+1 is read and the loads of stage kt+2 start
-  // while the MFMAs of the last slice of stage kt run, so neither the LDS
-  // read latency nor the loads' set-up leaves the matrix pipe idle at the
-  // step boundary. The loads of a stage are split between the last slice of
-  // one step and the first slice of the next.
-  constexpr int H1 = IAB / 2;
+  // Prologue: stage kt0 loaded and published, slice 0 of it read, and the
+  // loads of stage kt0+1 in flight.
   {
     const Fill f = make_fill(kt0, 0);
 #pragma unroll
@@ -459,28 +440,29 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   }
   wait_vm<0>();
   lds_barrier();
-  read(smem, 0, 0);
-  Fill fn = make_fill(kt0 + 1, 1);
 #pragma unroll
-  for (int j = 0; j < H1; ++j) issue_one(fn, j);
+  for (int i = 0; i < NR; ++i) read_one(smem, 0, 0, i);
+  {
+    const Fill f = make_fill(kt0 + 1, 1);
+#pragma unroll
+    for (int j = 0; j < IAB; ++j) issue_one(f, j);
+  }
 
+  // Step kt computes on slot kt&1 (fragments of slice 0 already in buffer 0).
   auto step = [&](int kt, auto&& mk) {
     const int cur = (kt - kt0) & 1;
     const bf16* b = smem + cur * SE;
+    const Fill next2 = mk(kt + 2, cur);  // stage kt+2 refills this step's slot
     __builtin_amdgcn_sched_barrier(0);
-    mma(0, b, 1, 1, fn, H1, IAB - H1);
-    __builtin_amdgcn_sched_barrier(0);
-    const Fill fnn = mk(kt + 2, cur);
-    mma(1, b, 2, 0, fn, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(0, b, 3, 1, fn, 0, 0);
+    mma(0, 0, NM / 2, b, 1, 1, NR, next2, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm0();
     wait_vm<0>();
     lds_barrier();
-    fn = fnn;
     __builtin_amdgcn_sched_barrier(0);
-    mma(1, smem + (cur ^ 1) * SE, 0, 0, fn, 0, H1);
+    mma(0, NM / 2, NM, b, 1, 1, 0, next2, 0, H1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, 0, NM, smem + (cur ^ 1) * SE, 0, 0, NR, next2, H1, IAB - H1);
     __builtin_amdgcn_sched_barrier(0);
   };
   // Steps whose prefetch (tile kt+2) stays in segment 1 use the invariant
@@ -491,6 +473,7 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   int kt = kt0;
   for (; kt < nfast; ++kt) step(kt, make_fill1);
   for (; kt < kt1; ++kt) step(kt, make_fill);
+  mfma_drain();
   // the last step's loads land before the epilogue reuses the LDS
   wait_vm<0>();
   lds_barrier();
@@ -537,7 +520,7 @@ struct EpiBF16 {
     store8_bf16(C + (long)m * ldc + n, v, lim);
   }
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+  DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
     if (!R) {
       for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
@@ -581,31 +564,23 @@ struct EpiGLU {
   long ldh;
   int I;
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+  DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
-    constexpr int TN = FN * 32, HF = TN / 2, PITCH = TN + 4, CG = HF / 8, RPI = 64 / CG;
-    static_assert(FN % 2 == 0 && 64 % CG == 0, "gate/up halves of 32-column fragments");
+    constexpr int TN = FN * 16, HF = TN / 2, PITCH = TN + 4, CG = HF / 8, RPI = 64 / CG;
+    static_assert(FN % 2 == 0 && FM % 2 == 0 && 64 % CG == 0, "gate/up halves of the wave tile");
     float* buf = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
-    const int lr = lane & 31, lh = lane >> 5;
     const int rsub = lane / CG, cg = lane % CG;
     // nw = n0 + wn·TN is the tile's output column base; the features start at
     // (n0 / BN)·(BN / 2) + wn·HF, i.e. nw / 2
     const int f0 = nw / 2;
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      if (mw + fm * 32 >= M) break;
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                           acc[fm][fn][4 * g + 3]};
-          *reinterpret_cast<f32x4*>(buf + lr * PITCH + fn * 32 + 8 * g + 4 * lh) = v;
-        }
+    for (int bk = 0; bk < FM / 2; ++bk) {
+      if (mw + bk * 32 >= M) break;
+      stage32<FM, FN, PITCH>(acc, bk, buf, lane);
 #pragma unroll
       for (int it = 0; it < 32 / RPI; ++it) {
         const int row = it * RPI + rsub;
-        const int m = mw + fm * 32 + row;
+        const int m = mw + bk * 32 + row;
         const float* gp = buf + row * PITCH + cg * 8;
         const f32x4 g0 = *reinterpret_cast<const f32x4*>(gp);
         const f32x4 g1 = *reinterpret_cast<const f32x4*>(gp + 4);
@@ -673,7 +648,7 @@ struct EpiSwiGLUBwd {
     if (n < I) finish(m, n, v, load(m, n));
   }
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+  DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
     for_each_row8_pf(
         acc, mw, nw, M, lane, wave, smem,
@@ -696,7 +671,7 @@ struct EpiF32 {
     for (int i = 0; i < 8 && i < lim; ++i) c[i] = accumulate ? c[i] + v[i] : v[i];
   }
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+  DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
     auto whole = [&](int m, int n) {
       return N - n >= 8 && (((unsigned long)(C + (long)m * ldc + n)) & 15) == 0;
@@ -737,27 +712,6 @@ struct EpiF32 {
             for (int i = 0; i < 8 && i < lim; ++i) c[i] = c[i] + v[i];
           }
         });
-  }
-};
-
-// Skinny LoRA products (N = r or a few r): Zf = sf·acc (fp32), Zb = bf16(sb·acc).
-struct EpiLoraZ {
-  float* Zf;
-  long ldzf;
-  float sf;
-  bf16* Zb;
-  long ldzb;
-  float sb;
-  int N;
-  template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane,
-                   int, void*) const {
-    for_each_quad(acc, mw, nw, M, lane, [&](int m, int n, float* v) {
-      for (int i = 0; i < 4 && n + i < N; ++i) {
-        if (Zf) Zf[(long)m * ldzf + n + i] = sf * v[i];
-        if (Zb) Zb[(long)m * ldzb + n + i] = (bf16)(sb * v[i]);
-      }
-    });
   }
 };
 

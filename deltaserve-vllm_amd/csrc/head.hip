@@ -40,40 +40,44 @@ struct EpiCEStats {
   float* tgt_logit;
   int c0, Vc;
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+  DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
-    constexpr int TM = FM * 32, TN = FN * 32, BMl = WM * TM;
+    constexpr int TM = FM * 16, TN = FN * 16, BMl = WM * TM;
     static_assert(WN * BMl * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2, "reduction scratch fits");
     const int wn = wave % WN, wm = wave / WN;
     const int n0 = nw - wn * TN;
     const int pn = c0 / (WN * TN) + n0 / (WN * TN);
-    const int lr = lane & 31, lh = lane >> 5;
+    // lane l holds row l%16 of each 16-row block, columns 4(l/16) .. +3 of
+    // each 16-column block: a row's values of the wave tile sit in the four
+    // lanes l%16 + 16q, combined with two shuffles
+    const int l16 = lane & 15, lq = lane >> 4;
     float* red = reinterpret_cast<float*>(smem);  // [WN][BMl]
     float mx[FM];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      const int m = mw + fm * 32 + lr;
+      const int m = mw + fm * 16 + l16;
       const int t = (m < M) ? labels[m] - c0 : -1;
       float v = -INFINITY;
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int n = nw + fn * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          const float x = acc[fm][fn][r];
+        for (int i = 0; i < 4; ++i) {
+          const int n = nw + fn * 16 + 4 * lq + i;
+          const float x = acc[fm][fn][i];
           if (n < Vc) v = fmaxf(v, x);
           if (n == t) tgt_logit[m] = x;
         }
+      v = fmaxf(v, __shfl_xor(v, 16, 64));
       mx[fm] = fmaxf(v, __shfl_xor(v, 32, 64));
     }
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
-      if (lh == 0) red[wn * BMl + wm * TM + fm * 32 + lr] = mx[fm];
+      if (lq == 0) red[wn * BMl + wm * TM + fm * 16 + l16] = mx[fm];
     __syncthreads();
     float sm[FM];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      const int row = wm * TM + fm * 32 + lr;
+      const int row = wm * TM + fm * 16 + l16;
       float b = red[row];
 #pragma unroll
       for (int j = 1; j < WN; ++j) b = fmaxf(b, red[j * BMl + row]);
@@ -82,22 +86,23 @@ struct EpiCEStats {
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int n = nw + fn * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          if (n < Vc) s += __expf(acc[fm][fn][r] - b);
+        for (int i = 0; i < 4; ++i) {
+          const int n = nw + fn * 16 + 4 * lq + i;
+          if (n < Vc) s += __expf(acc[fm][fn][i] - b);
         }
+      s += __shfl_xor(s, 16, 64);
       sm[fm] = s + __shfl_xor(s, 32, 64);
     }
     __syncthreads();
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
-      if (lh == 0) red[wn * BMl + wm * TM + fm * 32 + lr] = sm[fm];
+      if (lq == 0) red[wn * BMl + wm * TM + fm * 16 + l16] = sm[fm];
     __syncthreads();
-    if (wn == 0 && lh == 0) {
+    if (wn == 0 && lq == 0) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
-        const int row = wm * TM + fm * 32 + lr;
-        const int m = mw + fm * 32 + lr;
+        const int row = wm * TM + fm * 16 + l16;
+        const int m = mw + fm * 16 + l16;
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < WN; ++j) s += red[j * BMl + row];
@@ -119,7 +124,7 @@ struct EpiCEGrad {
   long ldd;
   int c0, Vc, Nc8;
   template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x16 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
+  DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
     const float sc = *inv_nvalid;
     for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
