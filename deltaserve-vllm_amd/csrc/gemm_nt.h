@@ -106,7 +106,15 @@ DSB_DEV void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop
 
 // buffer_load_dwordx4 ... lds with M0 set and not restored: the GEMM kernels
 // issue no other instruction that reads M0 (checked on their assembly), so
-// the three scalar instructions per load of a save/restore are not needed.
+// the save/restore around each load is not needed. In the main loop the M0
+// write (set_m0) goes before the MFMA that precedes its load (dma16_m0), which
+// covers the wait state between them; elsewhere lds_dma16_m0 does both.
+DSB_DEV void set_m0(unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %0" ::"s"(lds_addr) : "memory", "m0");
+}
+DSB_DEV void dma16_m0(u32x4 rsrc, int voff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc) : "memory");
+}
 DSB_DEV void lds_dma16_m0(u32x4 rsrc, int voff, unsigned lds_addr) {
   asm volatile(
       "s_mov_b32 m0, %2\n\t"
@@ -360,6 +368,16 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
       lds_dma16_m0(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]),
                    f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
   };
+  // the same load split around an MFMA: M0 before it, the load after it
+  auto pre_one = [&](const Fill& f, int j) {
+    set_m0(j < IA ? f.dst + j * 8 * NW * BK * 2 : f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+  };
+  auto go_one = [&](const Fill& f, int j) {
+    if (j < IA)
+      dma16_m0(f.dA, f.voA + j * f.stA);
+    else
+      dma16_m0(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]));
+  };
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -385,26 +403,33 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
       bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(b + brow + ch + (i - FM) * 16 * BK);
   };
   constexpr int NM = FM * FN, NR = FM + FN, H1 = IAB / 2;
-  // MFMAs t0 .. t1-1 of the slice held in `buf`, each followed by one other
-  // instruction while there are any: first the fragment reads 0 .. nr-1 of
-  // slice ns of the stage at nb (into buffer nbuf), one after each MFMA,
-  // then loads j0 .. j0+nj-1 of f, one after every other MFMA. A wave issues
-  // at most one instruction every few cycles, so a burst of other
-  // instructions between MFMAs would leave the matrix pipe idle.
+  // MFMAs t0 .. t1-1 of the slice held in `buf`, with other instructions
+  // between them: first the fragment reads 0 .. nr-1 of slice ns of the
+  // stage at nb (into buffer nbuf), one after each MFMA, then loads
+  // j0 .. j0+nj-1 of f, one after every third MFMA (its M0 write before that
+  // MFMA). A wave issues at most one instruction every few cycles, so a burst
+  // of other instructions between MFMAs would leave the matrix pipe idle
+  // (loads after every MFMA, or every other one, measured slower).
   auto mma = [&](int buf, int t0, int t1, const bf16* nb, int ns, int nbuf, int nr,
                  const Fill& f, int j0, int nj) {
     int r = 0, j = 0;
 #pragma unroll
     for (int t = t0; t < t1; ++t) {
       const int fm = t / FN, fn = t % FN;
+      const bool ld = r >= nr && j < nj && t % 3 == 2;
+      if (ld) {
+        __builtin_amdgcn_sched_barrier(0);
+        pre_one(f, j0 + j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       mfma16_acc(acc[fm][fn], bfr[buf][fn], af[buf][fm]);
       if (r < nr) {
         __builtin_amdgcn_sched_barrier(0);
         read_one(nb, ns, nbuf, r++);
         __builtin_amdgcn_sched_barrier(0);
-      } else if (j < nj && (t & 1) == 1) {
+      } else if (ld) {
         __builtin_amdgcn_sched_barrier(0);
-        issue_one(f, j0 + j++);
+        go_one(f, j0 + j++);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
