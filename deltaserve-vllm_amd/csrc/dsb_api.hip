@@ -41,31 +41,6 @@ const char* get_error() { return g_err; }
 
 // ------------------------------------------------------------ small kernels
 
-__global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restrict__ in,
-                                                             long ldi, bf16* __restrict__ out,
-                                                             long ldo, int R, int C) {
-  __shared__ bf16 t[64][66];
-  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = 0; i < 16; ++i) {
-    const int r = ty + i * 4;
-    if (r0 + r < R && c0 + tx < C) t[r][tx] = in[(long)(r0 + r) * ldi + c0 + tx];
-  }
-  __syncthreads();
-  for (int i = 0; i < 16; ++i) {
-    const int c = ty + i * 4;
-    if (c0 + c < C && r0 + tx < R) out[(long)(c0 + c) * ldo + r0 + tx] = t[tx][c];
-  }
-}
-
-static hipError_t transpose_bf16(const bf16* in, long ldi, bf16* out, long ldo, int R, int C,
-                                 hipStream_t s) {
-  if (R <= 0 || C <= 0) return hipSuccess;
-  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((C + 63) / 64, (R + 63) / 64), dim3(256), 0, s,
-                     in, ldi, out, ldo, R, C);
-  return hipGetLastError();
-}
-
 // labels[t] = pred[t] ? ids[t + 1] : -1; out-of-range ids raise err bit 1.
 __global__ void labels_kernel(const int64_t* __restrict__ ids, const int* __restrict__ pred,
                               int* __restrict__ labels, int n, const int* n_dev, int V,
@@ -209,13 +184,12 @@ struct LayerState {
   bool bound = false;
   // LoRA groups: q/k/v share one K-concatenated operand slab, gate/up another;
   // a projection of a group that is not bound has zero slices (frozen).
-  bf16 *qkvT = nullptr, *oT = nullptr, *guT = nullptr, *downT = nullptr;
   dsb_lora_tensors lora[DSB_NUM_PROJ]{};
   bool has[DSB_NUM_PROJ]{};
-  bf16 *Aqkv, *AqkvT, *B2qkv, *BTq, *BTk, *BTv;
-  bf16 *Ao, *AoT, *Bo, *BTo;
-  bf16 *Agu, *AguT, *B2gu, *BTg, *BTu;
-  bf16 *Ad, *AdT, *Bd, *BTd;
+  bf16 *Aqkv, *B2qkv, *BTq, *BTk, *BTv;
+  bf16 *Ao, *Bo, *BTo;
+  bf16 *Agu, *B2gu, *BTg, *BTu;
+  bf16 *Ad, *Bd, *BTd;
 };
 
 }  // namespace
@@ -247,8 +221,6 @@ struct dsb_handle {
   std::vector<LayerState> layers;
   const bf16* lm_w = nullptr;
   const bf16* norm_w = nullptr;
-  bf16* lm_wT = nullptr;  // [D, ldwt], columns V..ldwt zero
-  long ldwt = 0;
   std::vector<const bf16*> layer_in;
   std::vector<const bf16*> gate_up_in;  // saved gate‖up per layer (empty: recompute)
   long ld_gate_up = 0;
@@ -521,7 +493,6 @@ int finalize(dsb_handle* h) {
     LayerState& ls = h->layers[i];
     if (has_qkv(ls)) {
       CKR(dalloc_zero(h, &ls.Aqkv, 3L * r * D));
-      CKR(dalloc_zero(h, &ls.AqkvT, (long)D * 3 * r));
       CKR(dalloc_zero(h, &ls.B2qkv, (long)W3 * 3 * r));
       CKR(dalloc_zero(h, &ls.BTq, (long)r * q));
       CKR(dalloc_zero(h, &ls.BTk, (long)r * kv));
@@ -532,51 +503,43 @@ int finalize(dsb_handle* h) {
         if (!ls.has[p]) continue;
         const dsb_lora_tensors& t = ls.lora[p];
         job(t.A, r, D, D, ls.Aqkv + (long)p * r * D, D, 0, 1.f);
-        job(t.A, r, D, D, ls.AqkvT + p * r, 3 * r, 1, 1.f);
         job(t.B, outs[p], r, r, ls.B2qkv + (long)rowoff[p] * 3 * r + p * r, 3 * r, 0, s);
         job(t.B, outs[p], r, r, bts[p], outs[p], 1, s);
       }
     }
     if (ls.has[DSB_PROJ_O]) {
       CKR(dalloc(h, &ls.Ao, (long)r * q));
-      CKR(dalloc(h, &ls.AoT, (long)q * r));
       CKR(dalloc(h, &ls.Bo, (long)D * r));
       CKR(dalloc(h, &ls.BTo, (long)r * D));
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
       job(t.A, r, q, q, ls.Ao, q, 0, 1.f);
-      job(t.A, r, q, q, ls.AoT, r, 1, 1.f);
       job(t.B, D, r, r, ls.Bo, r, 0, s);
       job(t.B, D, r, r, ls.BTo, D, 1, s);
     }
     if (has_gu(ls)) {
       CKR(dalloc_zero(h, &ls.Agu, 2L * r * D));
-      CKR(dalloc_zero(h, &ls.AguT, (long)D * 2 * r));
       CKR(dalloc_zero(h, &ls.B2gu, 2L * I * 2 * r));
       CKR(dalloc_zero(h, &ls.BTg, (long)r * I));
       CKR(dalloc_zero(h, &ls.BTu, (long)r * I));
       if (ls.has[DSB_PROJ_GATE]) {
         const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
         job(tg.A, r, D, D, ls.Agu, D, 0, 1.f);
-        job(tg.A, r, D, D, ls.AguT, 2 * r, 1, 1.f);
         job(tg.B, I, r, r, ls.B2gu, 2 * r, 0, s);
         job(tg.B, I, r, r, ls.BTg, I, 1, s);
       }
       if (ls.has[DSB_PROJ_UP]) {
         const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
         job(tu.A, r, D, D, ls.Agu + (long)r * D, D, 0, 1.f);
-        job(tu.A, r, D, D, ls.AguT + r, 2 * r, 1, 1.f);
         job(tu.B, I, r, r, ls.B2gu + (long)I * 2 * r + r, 2 * r, 0, s);
         job(tu.B, I, r, r, ls.BTu, I, 1, s);
       }
     }
     if (ls.has[DSB_PROJ_DOWN]) {
       CKR(dalloc(h, &ls.Ad, (long)r * I));
-      CKR(dalloc(h, &ls.AdT, (long)I * r));
       CKR(dalloc(h, &ls.Bd, (long)D * r));
       CKR(dalloc(h, &ls.BTd, (long)r * D));
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
       job(t.A, r, I, I, ls.Ad, I, 0, 1.f);
-      job(t.A, r, I, I, ls.AdT, r, 1, 1.f);
       job(t.B, D, r, r, ls.Bd, r, 0, s);
       job(t.B, D, r, r, ls.BTd, D, 1, s);
     }
@@ -852,7 +815,7 @@ int dual(dsb_handle* h, const DualSpec* sp, int count, int r, hipStream_t s) {
 
 HeadArgs head_args(dsb_handle* h) {
   HeadArgs ha{};
-  ha.normed = h->normed; ha.ldh = h->D; ha.W = h->lm_w; ha.WT = h->lm_wT; ha.ldwt = h->ldwt;
+  ha.normed = h->normed; ha.ldh = h->D; ha.W = h->lm_w;
   ha.labels = h->labels;
   ha.n = h->N; ha.n_dev = &h->d_hdr->n; ha.D = h->D; ha.V = h->V; ha.stats = h->stats;
   ha.ntn = h->ntn; ha.ce_bn = h->ce_bn;
@@ -1078,8 +1041,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       // gh = g·W_down (+ gZ_d·A_d), the gradient wrt h = silu(gate)·up; the
       // epilogue turns it into d_gate ‖ d_up (reads gate ‖ up, writes Ggu),
       // so gh itself is never stored
-      GemmProblem p{g, (long)D, ls.downT, (long)D, hd ? h->gZd_b : nullptr, (long)r,
-                    hd ? ls.AdT : nullptr, (long)r, N, I, D, hd ? r : 0, nd};
+      GemmProblem p{g, (long)D, (const bf16*)ls.w.down, (long)I, hd ? h->gZd_b : nullptr, (long)r,
+                    hd ? ls.Ad : nullptr, (long)I, N, I, D, hd ? r : 0, nd};
+      p.b_kn = 1;
       EpiSwiGLUBwd e{gu, ldgu, h->Ggu, 2L * I, I};
       CKR(gemm(h, "dswiglu", p, e, st, 8.0, 0.0));
     }
@@ -1121,8 +1085,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       if (rest_u) CKR(skinny(h, h->Ggu + I, 2L * I, ls.BTu, r, I, h->gZgu_b + r, 2 * r, st));
     }
     {
-      GemmProblem p{h->Ggu, 2L * I, ls.guT, 2L * I, hg ? h->gZgu_b : nullptr, 2L * r,
-                    hg ? ls.AguT : nullptr, 2L * r, N, D, 2 * I, hg ? 2 * r : 0, nd};
+      GemmProblem p{h->Ggu, 2L * I, wgu, (long)D, hg ? h->gZgu_b : nullptr, 2L * r,
+                    hg ? ls.Agu : nullptr, (long)D, N, D, 2 * I, hg ? 2 * r : 0, nd};
+      p.b_kn = 1;
       EpiF32 e{h->gxn2, (long)D, D, 0};
       CKR(gemm(h, "dx32", p, e, st, 4.0, 0.0));
     }
@@ -1151,8 +1116,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       if (dual_o) CKR(skinny(h, h->grm, D, ls.BTo, r, D, h->gZo_b, r, st));
     }
     {
-      GemmProblem p{h->grm, (long)D, ls.oT, (long)D, ho ? h->gZo_b : nullptr, (long)r,
-                    ho ? ls.AoT : nullptr, (long)r, N, q, D, ho ? r : 0, nd};
+      GemmProblem p{h->grm, (long)D, wo, (long)q, ho ? h->gZo_b : nullptr, (long)r,
+                    ho ? ls.Ao : nullptr, (long)q, N, q, D, ho ? r : 0, nd};
+      p.b_kn = 1;
       EpiBF16 e{h->gctx, (long)q, q, nullptr, 0};
       CKR(gemm(h, "bf16", p, e, st, 2.0, 0.0));
     }
@@ -1203,8 +1169,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
         CKR(skinny(h, h->gqkv + q + kv, W3, ls.BTv, r, kv, h->gZqkv_b + 2 * r, 3 * r, st));
     }
     {
-      GemmProblem p{h->gqkv, (long)W3, ls.qkvT, (long)W3, hq ? h->gZqkv_b : nullptr, 3L * r,
-                    hq ? ls.AqkvT : nullptr, 3L * r, N, D, W3, hq ? 3 * r : 0, nd};
+      GemmProblem p{h->gqkv, (long)W3, wqkv, (long)D, hq ? h->gZqkv_b : nullptr, 3L * r,
+                    hq ? ls.Aqkv : nullptr, (long)D, N, D, W3, hq ? 3 * r : 0, nd};
+      p.b_kn = 1;
       EpiF32 e{h->gxn1, (long)D, D, 0};
       CKR(gemm(h, "dx32", p, e, st, 4.0, 0.0));
     }
@@ -1507,13 +1474,6 @@ void dsb_destroy(dsb_handle* h) {
     (void)hipEventDestroy(r.e1);
   }
   for (void* p : h->allocs) (void)hipFree(p);
-  for (auto& ls : h->layers) {
-    if (ls.qkvT) (void)hipFree(ls.qkvT);
-    if (ls.oT) (void)hipFree(ls.oT);
-    if (ls.guT) (void)hipFree(ls.guT);
-    if (ls.downT) (void)hipFree(ls.downT);
-  }
-  if (h->lm_wT) (void)hipFree(h->lm_wT);
   if (h->h_stage) (void)hipHostFree(h->h_stage);
   if (h->ev_in) (void)hipEventDestroy(h->ev_in);
   if (h->ev_out) (void)hipEventDestroy(h->ev_out);
@@ -1533,23 +1493,12 @@ int dsb_bind_weights(dsb_handle* h, int layer, const dsb_layer_weights* w) {
   if (h->qwen && (!w->q_norm || !w->k_norm))
     return fail(h, "dsb_bind_weights: qwen3 needs q_norm and k_norm");
   LayerState& ls = h->layers[layer];
-  ls.w = *w;
-  const int D = h->D, W3 = h->W3, q = h->q, I = h->I;
-  // The borrowed weights may still be being written by work the caller
+  // The weights are read in place, in their own [out, in] layout, by every
+  // product (no copy). They may still be being written by work the caller
   // issued on its own streams (a dtype conversion, an IPC copy): finish all
   // of it before the library's stream reads them.
   CK(hipDeviceSynchronize());
-  if (!ls.qkvT) {
-    CK(hipMalloc(&ls.qkvT, (size_t)D * W3 * 2));
-    CK(hipMalloc(&ls.oT, (size_t)q * D * 2));
-    CK(hipMalloc(&ls.guT, (size_t)D * 2 * I * 2));
-    CK(hipMalloc(&ls.downT, (size_t)I * D * 2));
-  }
-  CK(transpose_bf16((const bf16*)w->qkv, D, ls.qkvT, W3, W3, D, h->hs));
-  CK(transpose_bf16((const bf16*)w->o, q, ls.oT, D, D, q, h->hs));
-  CK(transpose_bf16((const bf16*)w->gate_up, D, ls.guT, 2L * I, 2 * I, D, h->hs));
-  CK(transpose_bf16((const bf16*)w->down, I, ls.downT, D, D, I, h->hs));
-  CK(hipStreamSynchronize(h->hs));
+  ls.w = *w;
   ls.bound = true;
   return 0;
 }
@@ -1558,16 +1507,9 @@ int dsb_bind_head(dsb_handle* h, const void* lm_head, const void* final_norm) {
   if (!h || !lm_head || !final_norm) return fail(h, "dsb_bind_head: null argument");
   std::lock_guard<std::mutex> lk(h->mu);
   if (h->finalized) return fail(h, "dsb_bind_head: state already finalized");
+  CK(hipDeviceSynchronize());  // as in dsb_bind_weights: the head may still be in flight
   h->lm_w = (const bf16*)lm_head;
   h->norm_w = (const bf16*)final_norm;
-  h->ldwt = ((long)h->V + 7) / 8 * 8;
-  CK(hipDeviceSynchronize());  // as in dsb_bind_weights: the head may still be in flight
-  if (!h->lm_wT) {
-    CK(hipMalloc(&h->lm_wT, (size_t)h->ldwt * h->D * 2));
-    CK(hipMemsetAsync(h->lm_wT, 0, (size_t)h->ldwt * h->D * 2, h->hs));
-  }
-  CK(transpose_bf16(h->lm_w, h->D, h->lm_wT, h->ldwt, h->V, h->D, h->hs));
-  CK(hipStreamSynchronize(h->hs));
   return 0;
 }
 
@@ -1883,13 +1825,16 @@ int dsb_save_ids(const int64_t* ids, int64_t ids_len, const int64_t* src, const 
 
 int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
                 int64_t lda2, const void* B2, int64_t ldb2, int M, int N, int K1, int K2, void* C,
-                int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr, int cfg,
-                void* stream) {
+                int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr, int b_kn,
+                int cfg, void* stream) {
   if (K1 % 8 || K2 % 8 || lda % 8 || ldb % 8 || (K2 && (lda2 % 8 || ldb2 % 8)) || ldc % 4)
     return fail(nullptr, "dsb_op_gemm: K and leading dims must be multiples of 8 (ldc of 4)");
+  if (b_kn && N % 8)
+    return fail(nullptr, "dsb_op_gemm: a [K, N] B needs N a multiple of 8");
   hipStream_t s = (hipStream_t)stream;
   GemmProblem p{(const bf16*)A, lda, (const bf16*)B, ldb, (const bf16*)A2, lda2,
                 (const bf16*)B2, ldb2, M, N, K1, K2, nullptr};
+  p.b_kn = b_kn ? 1 : 0;
   // cfg -2: split K as the cycle does for problems with too few 256-wide
   // tiles; cfg -3: split K over the tiles of a partly filled last round, as
   // the cycle does (partials in a buffer allocated for the call); by shape
@@ -2117,8 +2062,6 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   TmpDev tmp;
   const int ntn = (V + 255) / 256;
   const int vchunk = std::min(vocab_chunk > 0 ? vocab_chunk : 16384, ((V + 255) / 256) * 256);
-  const long ldwt = ((long)V + 7) / 8 * 8;
-  bf16* WT = tmp.alloc<bf16>((size_t)ldwt * D);
   int* dpred = tmp.alloc<int>(n + 1);
   int* labels = tmp.alloc<int>(n + 1);
   float2* stats = tmp.alloc<float2>((size_t)(n + 1) * ntn);
@@ -2128,17 +2071,15 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   float* scal = tmp.alloc<float>(4);
   int* err = tmp.alloc<int>(1);
   bf16* dlog = tmp.alloc<bf16>((size_t)(n + 1) * vchunk);
-  if (!WT || !dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog)
+  if (!dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog)
     return fail(nullptr, "dsb_op_head: hipMalloc failed");
   float hsc[4] = {nv > 0 ? 1.f / nv : 0.f, 0.f, 0.f, 0.f};
   OPCK(hipMemcpy(scal, hsc, sizeof(hsc), hipMemcpyHostToDevice));
   if (n > 0) OPCK(hipMemcpy(dpred, pred.data(), n * sizeof(int32_t), hipMemcpyHostToDevice));
   OPCK(hipMemset(err, 0, sizeof(int)));
-  OPCK(hipMemsetAsync(WT, 0, (size_t)ldwt * D * 2, s));
-  OPCK(transpose_bf16((const bf16*)lm_w, D, WT, ldwt, V, D, s));
   OPCK(build_labels(ids, dpred, labels, n, nullptr, V, err, s));
   HeadArgs a{};
-  a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w; a.WT = WT; a.ldwt = ldwt;
+  a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w;
   a.labels = labels; a.n = n; a.n_dev = nullptr; a.D = D; a.V = V; a.stats = stats; a.ntn = ntn;
   a.tgt_logit = tl; a.lse = lse; a.loss_row = lr; a.loss_out = scal + 1; a.inv_nvalid = scal;
   a.dlog = dlog; a.vchunk = vchunk; a.dH = dH; a.gemm_cfg = -1;

@@ -154,6 +154,7 @@ DSB_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
 }
 
 typedef __attribute__((address_space(3))) bf16 lds_bf16;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 DSB_DEV unsigned lds_addr(bf16* p) {
   return __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)(lds_bf16*)p);
 }

@@ -73,6 +73,15 @@ struct GemmProblem {
   // the epilogue.
   int tile0 = 0;
   float* tpart = nullptr;
+  // B (and B2) stored [K, N] row-major (element (n, k) at B[k·ldb + n]): the
+  // frozen weights in their native [out, in] layout as the operand of the dX
+  // products, and the LoRA A factors [r, in] as their second segment, so no
+  // transposed copy of either is needed.
+  int b_kn = 0;
+  // rows of a [K, N] B's first segment that exist (0: K1); rows from here to
+  // K1 load as zeros (the LM head's last vocabulary chunk runs K to a
+  // multiple of 8 past the vocabulary)
+  int kb_rows = 0;
 };
 
 DSB_DEV void tile_map(int bid, int nbm, int nbn, int& pm, int& pn) {
@@ -109,6 +118,10 @@ DSB_DEV void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop
 // the save/restore around each load is not needed. In the main loop the M0
 // write (set_m0) goes before the MFMA that precedes its load (dma16_m0), which
 // covers the wait state between them; elsewhere lds_dma16_m0 does both.
+// (clang warns on every use that M0 is reserved; the warning is silenced for
+// these two helpers only.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 DSB_DEV void set_m0(unsigned lds_addr) {
   asm volatile("s_mov_b32 m0, %0" ::"s"(lds_addr) : "memory", "m0");
 }
@@ -124,6 +137,7 @@ DSB_DEV void lds_dma16_m0(u32x4 rsrc, int voff, unsigned lds_addr) {
       : "v"(voff), "s"(rsrc), "s"(lds_addr)
       : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Writes 32-row block b (rows 32b .. 32b+31 of the wave tile) of the
 // accumulators, row-major at `buf` (row pitch PITCH floats): acc[2b + h][fn]
@@ -254,7 +268,17 @@ struct SplitPart {
                                   std::is_same<E, EpiSwiGLUBwd>::value;
 };
 
-template <int BM, int BN, int WM, int WN, class Epi>
+// Swizzle of a [K, N]-layout B stage (rows of BN·2 bytes = CPR 16-byte
+// chunks): chunk c of row k sits in slot c ^ fkn(k). A transposed B fragment
+// read covers, per 16-lane group g, rows 8g + 0..3 (+4) at two adjacent
+// chunks; fkn spreads those 4 rows over 8 distinct chunk pairs and separates
+// groups 2h and 2h+1 (bit 3), so a 16- or 32-lane phase is conflict-free.
+template <int CPR>
+DSB_DEV int fkn(int k) {
+  return ((2 * (k & 3)) ^ (((k >> 3) & 1) << 3)) & (CPR - 1);
+}
+
+template <int BM, int BN, int WM, int WN, class Epi, bool KN = false>
 __global__ __launch_bounds__(WM* WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel(GemmProblem p, Epi epi) {
   constexpr int BK = 64;
@@ -308,9 +332,23 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   const long bbase = glu ? 0 : n0;
   const int brows = glu ? p.N : rowsB;
   const u32x4 dA1 = rsrc(p.A + (long)m0 * p.lda, p.lda, rowsA, p.K1);
-  const u32x4 dB1 = rsrc(p.B + bbase * p.ldb, p.ldb, brows, p.K1);
   const u32x4 dA2 = rsrc(nk2 ? p.A2 + (long)m0 * p.lda2 : p.A, p.lda2, rowsA, K2);
+  const u32x4 dB1 = rsrc(p.B + bbase * p.ldb, p.ldb, brows, p.K1);
   const u32x4 dB2 = rsrc(nk2 ? p.B2 + bbase * p.ldb2 : p.B, p.ldb2, brows, K2);
+  // [K, N] B: one descriptor per K tile, over the tile's rows that exist
+  // (k0 .. min(k0 + BK, K) - 1) × the tile's live columns. The row advance
+  // is in the descriptor's base rather than in the load's scalar offset,
+  // which the hardware's range check does not include: rows past K fall
+  // outside the descriptor by their lane offset alone. Columns past N are
+  // forced out by their (constant) lane offset.
+  const int kbr1 = p.kb_rows > 0 ? min(p.kb_rows, p.K1) : p.K1;
+  auto kn_rsrc = [&](bool s1, int k0) {
+    const int rows = min((s1 ? kbr1 : K2) - k0, BK);
+    if (rows <= 0) return make_rsrc(p.B, 0);
+    const long ld = s1 ? p.ldb : p.ldb2;
+    return make_rsrc((s1 ? p.B : p.B2) + n0 + (long)k0 * ld,
+                     (int)(((long)(rows - 1) * ld + rowsB) * 2));
+  };
   // lane byte offset of its first row; A load j adds j·8·NW rows, B load j
   // starts at row brow0(j) of the descriptor (uniform)
   const int rw = 8 * wave + lrow;
@@ -334,6 +372,21 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   }
   // OR-ed into the offset of chunks past K: beyond any descriptor, loads zero
   constexpr int OOB = 0x7ff00000;
+  // [K, N] B loads: load jb of this wave fills LDS rows RPL·(wave + jb·NW)
+  // .. +RPL-1 of the stage (rows of BN·2 bytes, CPR chunks each); lane l
+  // fills slot l % CPR of row l / CPR with chunk slot ^ fkn(row)
+  constexpr int CPR = BN / 8, RPL = 64 / CPR;
+  int vkn1[KN ? IB : 1], vkn2[KN ? IB : 1];
+  if constexpr (KN) {
+#pragma unroll
+    for (int jb = 0; jb < IB; ++jb) {
+      const int r = RPL * (wave + jb * NW) + lane / CPR;
+      const int c = (lane % CPR) ^ fkn<CPR>(r);
+      const int out = n0 + 8 * c < p.N ? 0 : OOB;
+      vkn1[jb] = (r * (int)p.ldb + 8 * c) * 2 | out;
+      vkn2[jb] = (r * (int)p.ldb2 + 8 * c) * 2 | out;
+    }
+  }
   const unsigned lds0 = lds_addr(smem);
 
   // Loads of K tile kt into stage slot `slot`, issued one at a time by
@@ -353,7 +406,10 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     const int K = s1 ? p.K1 : K2;
     const int kb = (k0 * 2) | ((k0 + lch * 8 < K) ? 0 : OOB);
     f.dA = s1 ? dA1 : dA2;
-    f.dB = s1 ? dB1 : dB2;
+    if constexpr (KN)
+      f.dB = kn_rsrc(s1, k0);
+    else
+      f.dB = s1 ? dB1 : dB2;
     f.voA = (s1 ? voA1 : voA2) + kb;
     f.voB = (s1 ? voB1 : voB2) + kb;
     f.stA = s1 ? stA1 : stA2;
@@ -362,11 +418,16 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     return f;
   };
   auto issue_one = [&](const Fill& f, int j) {
-    if (j < IA)
+    if (j < IA) {
       lds_dma16_m0(f.dA, f.voA + j * f.stA, f.dst + j * 8 * NW * BK * 2);
-    else
+    } else if constexpr (KN) {
+      set_m0(f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+      asm volatile("s_nop 0" ::: "memory");
+      dma16_m0(f.dB, f.s1 ? vkn1[j - IA] : vkn2[j - IA]);
+    } else {
       lds_dma16_m0(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]),
                    f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+    }
   };
   // the same load split around an MFMA: M0 before it, the load after it
   auto pre_one = [&](const Fill& f, int j) {
@@ -375,6 +436,8 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   auto go_one = [&](const Fill& f, int j) {
     if (j < IA)
       dma16_m0(f.dA, f.voA + j * f.stA);
+    else if constexpr (KN)
+      dma16_m0(f.dB, f.s1 ? vkn1[j - IA] : vkn2[j - IA]);
     else
       dma16_m0(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]));
   };
@@ -393,14 +456,35 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   const int g = lds_swz(l16);
   const int arow = (wm * TM + l16) * BK, brow = SA + (wn * TN + l16) * BK;
   bf16x8 af[2][FM], bfr[2][FN];
+  // [K, N] B fragment fn of slice s: two transposed 8-byte reads. Lane j of
+  // 16-lane group q points at row 32s + 8q + j/4 (then 4 rows on), columns
+  // 16fn + 4(j%4) .. +3 of the wave's tile; ds_read_b64_tr_b16 hands lane j
+  // the element j%4 of the pieces of lanes 4k + j/4, i.e. column j at the
+  // group's 4 rows, which is the MFMA's K order. fkn(row) depends on
+  // row % 16 only, the same for both reads.
+  int btr[KN ? FN : 1];
+  if constexpr (KN) {
+    const int rq = 8 * lq + l16 / 4;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int c = (wn * TN + fn * 16 + 4 * (l16 & 3)) / 8;
+      btr[fn] = (SA + rq * BN + ((c ^ fkn<CPR>(rq)) << 3) + 4 * (l16 & 1)) * 2;
+    }
+  }
   // Fragment i of slice s into buffer `buf`: A fragment i (i < FM), else B
   // fragment i - FM.
   auto read_one = [&](const bf16* b, int s, int buf, int i) {
     const int ch = ((4 * s + lq) ^ g) << 3;
-    if (i < FM)
+    if (i < FM) {
       af[buf][i] = *reinterpret_cast<const bf16x8*>(b + arow + ch + i * 16 * BK);
-    else
+    } else if constexpr (KN) {
+      const char* t = reinterpret_cast<const char*>(b) + btr[i - FM] + 32 * s * BN * 2;
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)t);
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + 4 * BN * 2));
+      bfr[buf][i - FM] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
       bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(b + brow + ch + (i - FM) * 16 * BK);
+    }
   };
   constexpr int NM = FM * FN, NR = FM + FN, H1 = IAB / 2;
   // MFMAs t0 .. t1-1 of the slice held in `buf`, with other instructions
@@ -447,7 +531,10 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     const int k0 = kt * BK;
     const int kb = (k0 * 2) | ((k0 + lch * 8 < p.K1) ? 0 : OOB);
     f.dA = dA1;
-    f.dB = dB1;
+    if constexpr (KN)
+      f.dB = kn_rsrc(true, k0);
+    else
+      f.dB = dB1;
     f.voA = voA1 + kb;
     f.voB = voB1 + kb;
     f.stA = stA1;
@@ -771,11 +858,16 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmProblem p, i
 }
 
 template <int BM, int BN, int WM, int WN, class Epi>
-hipError_t launch_gemm_cfg(const GemmProblem& p, const Epi& e, hipStream_t s) {
+hipError_t launch_gemm_cfg(const GemmProblem& p, const Epi& e, hipStream_t s, int ks = 1) {
   const int nbm = (p.M + BM - 1) / BM, nbn = (p.N + BN - 1) / BN;
   if (nbm == 0 || nbn == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WM, WN, Epi>), dim3(nbm * nbn),
-                     dim3(WM * WN * 64), 0, s, p, e);
+  const dim3 grid(nbm * nbn, ks);
+  if (p.b_kn)
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WM, WN, Epi, true>), grid, dim3(WM * WN * 64), 0,
+                       s, p, e);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WM, WN, Epi, false>), grid, dim3(WM * WN * 64),
+                       0, s, p, e);
   return hipGetLastError();
 }
 
@@ -838,15 +930,10 @@ hipError_t launch_gemm_split(const GemmProblem& p, const Epi& e, int ks, hipStre
   static_assert(SplitPart<Epi>::enabled, "split-K epilogues");
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
   if (!p.part || p.N % 8 != 0 || ks < 2) return hipErrorInvalidValue;
-  if (gemm_split_tile(p.M, p.N, p.K1 + p.K2) == 128) {
-    const int mbm = (p.M + 127) / 128, mbn = (p.N + 127) / 128;
-    hipLaunchKernelGGL((gemm_nt_kernel<128, 128, 2, 2, Epi>), dim3(mbm * mbn, ks), dim3(256), 0,
-                       s, p, e);
-  } else {
-    const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
-    hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(nbm * nbn, ks), dim3(256), 0,
-                       s, p, e);
-  }
+  const hipError_t e0 = gemm_split_tile(p.M, p.N, p.K1 + p.K2) == 128
+                           ? launch_gemm_cfg<128, 128, 2, 2>(p, e, s, ks)
+                           : launch_gemm_cfg<256, 256, 2, 2>(p, e, s, ks);
+  if (e0 != hipSuccess) return e0;
   const long n = (long)p.M * (p.N / 8);
   hipLaunchKernelGGL(gemm_split_reduce_kernel<Epi>, dim3((unsigned)((n + 255) / 256)), dim3(256),
                      0, s, p, ks, e);
@@ -911,12 +998,20 @@ hipError_t launch_gemm_tail(const GemmProblem& p, const Epi& e, int ks, int tail
   // so the tail launch's block x lands on the XCD that tile_map assumes
   if (!tpart || tail <= 0 || full <= 0 || full % 8 || ks < 2 || p.N % 8 || p.part)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(full), dim3(256), 0, s, p, e);
+  const dim3 blk(256);
+  if (p.b_kn)
+    hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi, true>), dim3(full), blk, 0, s, p, e);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi, false>), dim3(full), blk, 0, s, p, e);
   GemmProblem q = p;
   q.tile0 = full;
   q.tpart = tpart;
-  hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi>), dim3(tail, ks), dim3(256), 0, s, q,
-                     e);
+  if (p.b_kn)
+    hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi, true>), dim3(tail, ks), blk, 0, s, q,
+                       e);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<256, 256, 2, 2, Epi, false>), dim3(tail, ks), blk, 0, s,
+                       q, e);
   hipLaunchKernelGGL(gemm_tail_reduce_kernel<Epi>, dim3(tail * 32), dim3(256), 0, s, q, ks, tail,
                      e);
   return hipGetLastError();

@@ -242,8 +242,12 @@ int head_dh_tail(const HeadArgs& a, int c0, int* tail) {
 
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
   const int Nc8 = (min(a.vchunk, a.V - c0) + 7) / 8 * 8;
-  GemmProblem q{a.dlog, (long)a.vchunk, a.WT + c0, a.ldwt, nullptr, 0, nullptr, 0,
+  // dH += dlogits[:, chunk] · W[chunk, :]: the head read in place as the
+  // [K, N] operand, rows past the vocabulary loading as zeros
+  GemmProblem q{a.dlog, (long)a.vchunk, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
                 a.n, a.D, Nc8, 0, a.n_dev};
+  q.b_kn = 1;
+  q.kb_rows = min(a.vchunk, a.V - c0);
   EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
   const int ks = head_dh_split(a, c0);
   if (ks > 1) {

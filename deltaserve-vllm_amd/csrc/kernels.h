@@ -155,8 +155,6 @@ bool lora_dual_supported(int R1, int R2, int C);
 struct HeadArgs {
   const bf16* normed; long ldh;   // [n, D]
   const bf16* W;                  // [V, D]
-  const bf16* WT;                 // [D, ldwt], columns V..ldwt zero
-  long ldwt;                      // round_up(V, 8)
   const int* labels;              // [n] target id or -1
   int n; const int* n_dev;
   int D, V;

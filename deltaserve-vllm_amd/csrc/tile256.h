@@ -21,8 +21,6 @@ DSB_DEV int toff(int r, int col) {
   return r * 128 + ((((col >> 3) ^ aswz(r)) << 3) | (col & 7));
 }
 
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-
 // Per-lane byte offsets of the fragment reads inside a tile, computed once
 // per kernel (f is linear over GF(2), f(r0 + r) = f(r) for 16 | r0, and
 // f(r + 8) = f(r) ^ 8):

@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 # timing); the in-tree build is the default.
 LIB_PATH = os.environ.get("DSB_LIB") or os.path.join(LIB_DIR, "libdsb.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
 ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
@@ -111,7 +111,8 @@ _SIGS = {
                                   c_float, POINTER(c_float)]),
     "dsb_op_gemm": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                             c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p,
-                            c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p]),
+                            c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_int,
+                            c_void_p]),
     "dsb_op_gemm_glu": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                 c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int64,
                                 c_void_p, c_int64, c_void_p]),

@@ -71,11 +71,14 @@ def rope_inv_freq(head_dim, theta, rope_scaling=None):
 
 # ---------------------------------------------------------------- dense products
 
-def gemm_nt(A, B, A2=None, B2=None, out_dtype=BF16, R=None, out=None, accumulate=False, cfg=-1):
-    """C = A·Bᵀ (+ A2·B2ᵀ) (+ R) — the projection products of ops.py:103-146."""
+def gemm_nt(A, B, A2=None, B2=None, out_dtype=BF16, R=None, out=None, accumulate=False, cfg=-1,
+            b_kn=False):
+    """C = A·Bᵀ (+ A2·B2ᵀ) (+ R) — the projection products of ops.py:103-146.
+    b_kn: B [K1, N] and B2 [K2, N] (C = A·B + A2·B2, the backward's dY·W with W
+    in its own layout)."""
     _dev(A, B, A2, B2, R)
     M, K1 = A.shape
-    N = B.shape[0]
+    N = B.shape[1] if b_kn else B.shape[0]
     K2 = 0 if A2 is None else A2.shape[1]
     f32 = out_dtype == torch.float32
     if out is None:
@@ -83,7 +86,8 @@ def gemm_nt(A, B, A2=None, B2=None, out_dtype=BF16, R=None, out=None, accumulate
     L.check(L.load().dsb_op_gemm(_p(A), _ld(A), _p(B), _ld(B), _p(A2), 0 if A2 is None else _ld(A2),
                                  _p(B2), 0 if B2 is None else _ld(B2), M, N, K1, K2, _p(out),
                                  _ld(out), int(f32), int(accumulate), _p(R),
-                                 0 if R is None else _ld(R), int(cfg), _stream()),
+                                 0 if R is None else _ld(R), int(bool(b_kn)), int(cfg),
+                                 _stream()),
             what="dsb_op_gemm")
     return out
 

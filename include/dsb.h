@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DSB_ABI_VERSION 3
+#define DSB_ABI_VERSION 4
 
 enum { DSB_FAMILY_LLAMA3 = 0, DSB_FAMILY_QWEN3 = 1 };
 enum { DSB_ROPE_DEFAULT = 0, DSB_ROPE_LINEAR = 1, DSB_ROPE_LLAMA3 = 2 };
@@ -251,6 +251,8 @@ int dsb_save_ids(const int64_t* ids, int64_t ids_len, const int64_t* src, const 
 /* ---- single-op entry points (parity tests; synchronous on `stream`) ---- */
 
 /* C = A·Bᵀ (+ A2·B2ᵀ) [+ R]; out_f32 selects fp32 C (accumulate adds to C).
+ * b_kn: B and B2 are stored [K, N] (a weight in its own [out, in] layout read
+ * by the backward's C = dY·W; N a multiple of 8) instead of [N, K].
  * cfg: -1 tile by shape, 0/1/2 force 256/128/64-wide tiles, -2 split K over
  * the grid as the cycle does when the problem has too few 256-wide tiles,
  * -3 split K over the tiles of a partly filled last round of the device's
@@ -258,7 +260,7 @@ int dsb_save_ids(const int64_t* ids, int64_t ids_len, const int64_t* src, const 
 int dsb_op_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2,
                 int64_t lda2, const void* B2, int64_t ldb2, int M, int N, int K1, int K2,
                 void* C, int64_t ldc, int out_f32, int accumulate, const void* R, int64_t ldr,
-                int cfg, void* stream);
+                int b_kn, int cfg, void* stream);
 /* Gate‖up product with the SwiGLU forward in its epilogue (the recompute of
  * ffn.py:25-26, frozen gate_up_proj plus its LoRA term; silu as ffn.py:40-41): GU[m, :] = bf16(A·Bᵀ + A2·B2ᵀ)
  * with B [2I, K1] = gate rows then up rows (GU = [gate | up], ld ldgu), and,

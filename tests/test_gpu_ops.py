@@ -37,14 +37,26 @@ def _lib():
     L.load()
 
 
+def _b_operand(B, kn):
+    """B as the product reads it: [N, K], or the [K, N] layout of a weight
+    read in place by the backward (b_kn)."""
+    if B is None:
+        return None
+    return (B.t().contiguous() if kn else B).to(DEV)
+
+
+@pytest.mark.parametrize("kn", [False, True])
 @pytest.mark.parametrize("cfg", [0, 1, 2, -2])
 @pytest.mark.parametrize("M,N,K,K2", [(300, 520, 264, 24), (64, 64, 64, 0), (513, 260, 1024, 16),
                                       (1, 8, 8, 8), (513, 264, 1024, 16), (200, 1024, 4096, 64),
                                       (1, 8, 512, 8)])
-def test_gemm_nt(cfg, M, N, K, K2):
+def test_gemm_nt(cfg, M, N, K, K2, kn):
     """cfg -2 splits K (the last three shapes: 4, 8 and 2 K slices, the
-    slices crossing into the second K segment) and sums the fp32 partials."""
+    slices crossing into the second K segment) and sums the fp32 partials.
+    kn: B and B2 stored [K, N] (N a multiple of 8 there)."""
     from deltaserve_amd import ops
+    if kn and N % 8:
+        pytest.skip("a [K, N] B needs N a multiple of 8 (test_gemm_kn_refuses_ragged_n)")
     A = _bf(_rnd(M, K, seed=1))
     B = _bf(_rnd(N, K, seed=2))
     A2 = _bf(_rnd(M, K2, seed=3)) if K2 else None
@@ -52,21 +64,49 @@ def test_gemm_nt(cfg, M, N, K, K2):
     ref = A.float() @ B.float().t()
     if K2:
         ref += A2.float() @ B2.float().t()
-    c32 = ops.gemm_nt(A.to(DEV), B.to(DEV), None if A2 is None else A2.to(DEV),
-                      None if B2 is None else B2.to(DEV), out_dtype=torch.float32, cfg=cfg)
+    dA, dA2 = A.to(DEV), None if A2 is None else A2.to(DEV)
+    dB, dB2 = _b_operand(B, kn), _b_operand(B2, kn)
+    c32 = ops.gemm_nt(dA, dB, dA2, dB2, out_dtype=torch.float32, cfg=cfg, b_kn=kn)
     assert max_rel(c32, ref) < 1e-5
     R = _bf(_rnd(M, N, seed=5))
-    c16 = ops.gemm_nt(A.to(DEV), B.to(DEV), None if A2 is None else A2.to(DEV),
-                      None if B2 is None else B2.to(DEV), R=R.to(DEV), cfg=cfg)
+    c16 = ops.gemm_nt(dA, dB, dA2, dB2, R=R.to(DEV), cfg=cfg, b_kn=kn)
     assert max_rel(c16, ref + R.float()) < 8e-3
     # accumulate into an fp32 output
     acc = c32.clone()
-    ops.gemm_nt(A.to(DEV), B.to(DEV), out_dtype=torch.float32, out=acc, accumulate=True, cfg=cfg)
+    ops.gemm_nt(dA, dB, out_dtype=torch.float32, out=acc, accumulate=True, cfg=cfg, b_kn=kn)
     assert max_rel(acc, ref + A.float() @ B.float().t()) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K,K2", [(8192, 4096, 4096, 48), (8100, 1024, 4104, 16),
+                                      (300, 5000, 14336, 16)])
+def test_gemm_kn_equals_nt(M, N, K, K2):
+    """The [K, N] operand path gives the [N, K] path's product bit for bit:
+    the same MFMA fragments in the same order, only the B staging differs
+    (cycle-sized shapes: 256-wide tiles with ragged M and K, a LoRA segment,
+    N not a multiple of the tile)."""
+    from deltaserve_amd import ops
+    A = _bf(_rnd(M, K, seed=21)).to(DEV)
+    B = _bf(_rnd(N, K, seed=22))
+    A2 = _bf(_rnd(M, K2, seed=23)).to(DEV)
+    B2 = _bf(_rnd(N, K2, seed=24))
+    nt = ops.gemm_nt(A, B.to(DEV), A2, B2.to(DEV), out_dtype=torch.float32)
+    kn = ops.gemm_nt(A, _b_operand(B, True), A2, _b_operand(B2, True), out_dtype=torch.float32,
+                     b_kn=True)
+    assert torch.equal(nt, kn)
+
+
+def test_gemm_kn_refuses_ragged_n():
+    from deltaserve_amd import _lib as L
+    from deltaserve_amd import ops
+    A = torch.zeros(16, 64, dtype=torch.bfloat16, device=DEV)
+    B = torch.zeros(64, 264, dtype=torch.bfloat16, device=DEV)[:, :260]  # N = 260, ld 264
+    with pytest.raises(L.DsbError, match="multiple of 8"):
+        ops.gemm_nt(A, B, b_kn=True)
+
+
+@pytest.mark.parametrize("kn", [False, True])
 @pytest.mark.parametrize("M,N,K,K2", [(4352, 4104, 2048, 0), (4400, 3840, 2048, 64)])
-def test_gemm_nt_tail_split(M, N, K, K2):
+def test_gemm_nt_tail_split(M, N, K, K2, kn):
     """cfg -3: the tiles past the last full round of the CUs (289 tiles: 33
     of them; 270 tiles: 14, with a ragged last row block and the LoRA K
     segment in the second slice) split K in two and reduce their tile
@@ -80,19 +120,19 @@ def test_gemm_nt_tail_split(M, N, K, K2):
     ref = A.float() @ B.float().t()
     if K2:
         ref += A2.float() @ B2.float().t()
-    dA, dB = A.to(DEV), B.to(DEV)
+    dA, dB = A.to(DEV), _b_operand(B, kn)
     dA2 = None if A2 is None else A2.to(DEV)
-    dB2 = None if B2 is None else B2.to(DEV)
-    c32 = ops.gemm_nt(dA, dB, dA2, dB2, out_dtype=torch.float32, cfg=-3)
+    dB2 = _b_operand(B2, kn)
+    c32 = ops.gemm_nt(dA, dB, dA2, dB2, out_dtype=torch.float32, cfg=-3, b_kn=kn)
     assert max_rel(c32, ref) < 1e-5
     # the plain launch gives the same product
-    c32p = ops.gemm_nt(dA, dB, dA2, dB2, out_dtype=torch.float32, cfg=0)
+    c32p = ops.gemm_nt(dA, dB, dA2, dB2, out_dtype=torch.float32, cfg=0, b_kn=kn)
     assert max_rel(c32, c32p.cpu()) < 1e-5
     R = _bf(_rnd(M, N, seed=15))
-    c16 = ops.gemm_nt(dA, dB, dA2, dB2, R=R.to(DEV), cfg=-3)
+    c16 = ops.gemm_nt(dA, dB, dA2, dB2, R=R.to(DEV), cfg=-3, b_kn=kn)
     assert max_rel(c16, ref + R.float()) < 8e-3
     acc = c32.clone()
-    ops.gemm_nt(dA, dB, out_dtype=torch.float32, out=acc, accumulate=True, cfg=-3)
+    ops.gemm_nt(dA, dB, out_dtype=torch.float32, out=acc, accumulate=True, cfg=-3, b_kn=kn)
     assert max_rel(acc, ref + A.float() @ B.float().t()) < 1e-5
 
 
