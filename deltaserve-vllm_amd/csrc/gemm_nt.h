@@ -455,7 +455,9 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   // of the stage (K 32s .. 32s+31) is chunk 4s + lq of the lane's row.
   const int g = lds_swz(l16);
   const int arow = (wm * TM + l16) * BK, brow = SA + (wn * TN + l16) * BK;
-  bf16x8 af[2][FM], bfr[2][FN];
+  bf16x8 af[2][FM], bfr[2][KN ? 1 : FN];
+  // [K, N] B fragments as their two 4-deep halves, each read on its own
+  bf16x4 bkn[2][KN ? FN : 1][2];
   // [K, N] B fragment fn of slice s: two transposed 8-byte reads. Lane j of
   // 16-lane group q points at row 32s + 8q + j/4 (then 4 rows on), columns
   // 16fn + 4(j%4) .. +3 of the wave's tile; ds_read_b64_tr_b16 hands lane j
@@ -471,22 +473,29 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
       btr[fn] = (SA + rq * BN + ((c ^ fkn<CPR>(rq)) << 3) + 4 * (l16 & 1)) * 2;
     }
   }
-  // Fragment i of slice s into buffer `buf`: A fragment i (i < FM), else B
-  // fragment i - FM.
+  // Read i of slice s into buffer `buf`: A fragment i (i < FM), else B
+  // fragment i - FM, or with a [K, N] B half (i - FM) % 2 of B fragment
+  // (i - FM) / 2 (one LDS instruction per read, so a read fits between two
+  // MFMAs).
   auto read_one = [&](const bf16* b, int s, int buf, int i) {
     const int ch = ((4 * s + lq) ^ g) << 3;
     if (i < FM) {
       af[buf][i] = *reinterpret_cast<const bf16x8*>(b + arow + ch + i * 16 * BK);
     } else if constexpr (KN) {
-      const char* t = reinterpret_cast<const char*>(b) + btr[i - FM] + 32 * s * BN * 2;
-      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)t);
-      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + 4 * BN * 2));
-      bfr[buf][i - FM] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      const int fn = (i - FM) >> 1, h = (i - FM) & 1;
+      const char* t = reinterpret_cast<const char*>(b) + btr[fn] + 32 * s * BN * 2 + h * 4 * BN * 2;
+      bkn[buf][fn][h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)t);
     } else {
       bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(b + brow + ch + (i - FM) * 16 * BK);
     }
   };
-  constexpr int NM = FM * FN, NR = FM + FN, H1 = IAB / 2;
+  constexpr int NM = FM * FN, NR = FM + (KN ? 2 : 1) * FN, H1 = IAB / 2;
+  auto bfrag = [&](int buf, int fn) {
+    if constexpr (KN)
+      return __builtin_shufflevector(bkn[buf][fn][0], bkn[buf][fn][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    else
+      return bfr[buf][fn];
+  };
   // MFMAs t0 .. t1-1 of the slice held in `buf`, with other instructions
   // between them: first the fragment reads 0 .. nr-1 of slice ns of the
   // stage at nb (into buffer nbuf), one after each MFMA, then loads
@@ -506,7 +515,7 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
         pre_one(f, j0 + j);
         __builtin_amdgcn_sched_barrier(0);
       }
-      mfma16_acc(acc[fm][fn], bfr[buf][fn], af[buf][fm]);
+      mfma16_acc(acc[fm][fn], bfrag(buf, fn), af[buf][fm]);
       if (r < nr) {
         __builtin_amdgcn_sched_barrier(0);
         read_one(nb, ns, nbuf, r++);

@@ -268,6 +268,38 @@ def test_attention(seq_lens, Hq, Hkv):
         assert cosine(got, want) > 0.999
 
 
+def test_attention_two_8192_token_sequences():
+    """C5's packing (2 x 8192 tokens) at op level: every kernel's long-sequence
+    path (128 key tiles per query block, 64 q tiles per dK/dV block) against
+    the fp32 oracle run on the device (8 q-heads over 2 kv heads keep its
+    [heads, 8192, 8192] score tensors at 2 GiB each)."""
+    from deltaserve_amd import ops
+    seq_lens, Hq, Hkv = [8192, 8192], 8, 2
+    n = sum(seq_lens)
+    b_start, *_ = O.pack(seq_lens)
+    qh = _bf(_rnd(n, Hq, 128, seed=51)).to(DEV)
+    kh = _bf(_rnd(n, Hkv, 128, seed=52)).to(DEV)
+    vh = _bf(_rnd(n, Hkv, 128, seed=53)).to(DEV)
+    ctx, o32, lse = ops.attn_forward(qh.reshape(n, -1), kh.reshape(n, -1), vh.reshape(n, -1),
+                                     seq_lens, Hq, Hkv)
+    with torch.no_grad():
+        ref = O.attn_forward(qh.float(), kh.float(), vh.float(), seq_lens, b_start, Hq, Hkv)
+    assert max_rel(o32, ref) < 1e-2
+    assert cosine(o32, ref) > 0.9999
+    g = _bf(_rnd(n, Hq * 128, seed=54)).to(DEV)
+    dq, dk, dv = ops.attn_backward(qh.reshape(n, -1), kh.reshape(n, -1), vh.reshape(n, -1), o32,
+                                   lse, g, seq_lens, Hq, Hkv)
+    with torch.no_grad():
+        rq, rk, rv = O.attn_backward(qh.float(), kh.float(), vh.float(), g.float(), seq_lens,
+                                     b_start, Hq, Hkv)
+    for name, got, want in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        want = want.reshape(n, -1)
+        print(f"[attn 2x8192] {name}: max-rel {max_rel(got, want):.2e} cos "
+              f"{cosine(got, want):.6f}", flush=True)
+        assert max_rel(got, want) < 2e-2
+        assert cosine(got, want) > 0.999
+
+
 @pytest.mark.parametrize("V,vchunk", [(1000, 0), (211, 0), (1027, 0), (1027, 256), (5000, 768),
                                       (2304, 512)])
 def test_head(V, vchunk):
