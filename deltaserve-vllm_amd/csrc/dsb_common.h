@@ -68,6 +68,11 @@ DSB_DEV float block_sum(float v, float* red) {
 DSB_DEV u32x4 ldg128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 DSB_DEV void stg128(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// σ(x) = 1/(1 + e^(−x)) with the hardware reciprocal (1 ulp) in place of an
+// IEEE division (a dozen instructions per element in the SwiGLU epilogues);
+// e^(−x) = inf for x → −inf gives 0, and 0 for x → +inf gives 1.
+DSB_DEV float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+
 DSB_DEV void unpack8(u32x4 v, float f[8]) {
   const bf16x8 b = __builtin_bit_cast(bf16x8, v);
 #pragma unroll

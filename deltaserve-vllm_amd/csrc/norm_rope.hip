@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void swiglu_h_kernel(const bf16* __restrict__ 
   unpack8(ldg128(gu + (long)m * ldgu + c * 8), g);
   unpack8(ldg128(gu + (long)m * ldgu + I + c * 8), u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = g[e] / (1.f + __expf(-g[e])) * u[e];
+  for (int e = 0; e < 8; ++e) o[e] = g[e] * sigmoid(g[e]) * u[e];
   stg128(h + (long)m * ldh + c * 8, pack8(o));
 }
 
