@@ -1,4 +1,4 @@
-// Packed varlen causal GQA attention (head_dim 128) on gfx950 MFMA:
+// Packed varlen causal GQA attention on gfx950 MFMA, head_dim 128 or 64:
 // forward recompute (ctx, optional fp32 ctx copy, row log-sum-exp) and the
 // FA2-style backward split into a dQ pass (forward and dQ blocks: 4 waves of
 // 32 queries sharing one kv head, see q_block), which also forms
@@ -6,6 +6,11 @@
 // block per 128 keys of one kv head, summing its q-head group in registers, no
 // atomics). Softmax statistics, P and dS stay fp32 in registers; P and dS are
 // rounded to bf16 only as MFMA operands.
+//
+// head_dim 64 runs the head_dim-128 kernels on heads zero-padded to 128 inside
+// the loads (dims past a.hd load as zeros, so they add nothing to Q·Kᵀ, dO·Vᵀ
+// or dsum, and come out of P·V, dS·K, dSᵀ·Q and Pᵀ·dO as zeros that the
+// stores skip), scaled by a.scale = 1/sqrt(head_dim).
 //
 // Semantics: deltaserve-plugin/deltaserve/bwd_services/common/attention.py
 //   attn_forward_core   :20-45   (scale 1/sqrt(Hd), causal mask, fp32 softmax)
@@ -41,11 +46,13 @@
 namespace dsb {
 
 namespace {
-constexpr int HD = 128;
+constexpr int HD = 128;             // head width the kernels compute on
 constexpr int TR = 64;             // rows per streamed tile
 constexpr int TILE = TR * HD;      // elements per tile (16 KB)
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kScale = 0.08838834764831845f;  // 1/sqrt(128)
+// OR-ed into the lane offset of a chunk past the head width: beyond any
+// descriptor (num_records < 2^31), so it loads zeros
+constexpr unsigned kPastHead = 0x80000000u;
 
 // Direct-to-LDS loads of one sequence's 64-row × 128-column tiles of a
 // [rows, ld] operand, set up once per block: one descriptor over the
@@ -60,31 +67,34 @@ constexpr float kScale = 0.08838834764831845f;  // 1/sqrt(128)
 // descriptor word) made the loads' issue a large share of each tile step.
 struct SeqTiles {
   u32x4 rs;
-  int off0;  // bytes: row 4w + lane/16, the lane's chunk
-  int ldb;   // row stride in bytes
-  DSB_DEV SeqTiles(const bf16* mat, long ld, int st, int L, int wave, int lane) {
+  unsigned off0;  // bytes: row 4w + lane/16, the lane's chunk (| kPastHead past hd)
+  int ldb;        // row stride in bytes
+  DSB_DEV SeqTiles(const bf16* mat, long ld, int st, int L, int wave, int lane, int hd) {
     rs = make_rsrc(mat + (long)st * ld, (int)((long)max(L, 0) * ld * 2));
     const int r = 4 * wave + (lane >> 4);
-    off0 = (int)(((long)r * ld + (((lane & 15) ^ aswz(r)) << 3)) * 2);
+    const int c = (lane & 15) ^ aswz(r);
+    off0 = (unsigned)(((long)r * ld + (c << 3)) * 2) | (8 * c < hd ? 0u : kPastHead);
     ldb = (int)(ld * 2);
   }
   // tile rows t0 .. t0+63, columns col0 .. col0+127, to the tile at LDS byte
   // address `tile`
   DSB_DEV void load(int t0, int col0, unsigned tile, int wave) const {
-    const int base = t0 * ldb + col0 * 2;
+    const unsigned base = (unsigned)(t0 * ldb + col0 * 2);
 #pragma unroll
     for (int i = 0; i < TR / 16; ++i)
-      lds_dma16(rs, off0 + base + 16 * i * ldb, tile + (unsigned)((4 * (4 * i + wave)) * 256));
+      lds_dma16(rs, (int)(off0 + base + (unsigned)(16 * i * ldb)),
+                tile + (unsigned)((4 * (4 * i + wave)) * 256));
   }
 };
 
-// Row fragments of one global row (lane's row, 8 × 16 columns) straight to registers.
+// Row fragments of one global row (lane's row, 8 × 16 columns) straight to
+// registers; columns from hd on (and rows that are not ok) are zeros.
 DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool ok, int lh,
-                            bf16x8 (&f)[8]) {
+                            int hd, bf16x8 (&f)[8]) {
   const bf16* p = base + (ok ? row * ld + col0 : 0L);
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
-    f[kk] = *reinterpret_cast<const bf16x8*>(p + kk * 16 + lh * 8);
+    f[kk] = kk * 16 < hd ? *reinterpret_cast<const bf16x8*>(p + kk * 16 + lh * 8) : bf16x8{};
     if (!ok) f[kk] = bf16x8{};
   }
 }
@@ -152,11 +162,12 @@ DSB_DEV void mfma32_acc(f32x16& acc, bf16x8 a, bf16x8 b) {
 // kRowPitch elements): the lanes write their pieces there, then read back 16
 // contiguous bytes each and store whole 256-byte rows, four rows per store
 // instruction (storing the 8-byte pieces directly scatters every instruction
-// over 32 rows). Rows r >= nvalid are not stored. With `res`, the bf16
-// rounding residual bf16(x − bf16(x)) goes to res (same row stride) after.
+// over 32 rows). Rows r >= nvalid and columns from ncol on are not stored.
+// With `res`, the bf16 rounding residual bf16(x − bf16(x)) goes to res (same
+// row stride) after.
 constexpr int kRowPitch = 136;  // 272 bytes: rows 16 apart share LDS banks, at most 2-way
 DSB_DEV void store_rows32(const f32x16 (&acc)[4], float scale, bf16* buf, bf16* out, long ld,
-                          int nvalid, int lane, bf16* res = nullptr) {
+                          int nvalid, int ncol, int lane, bf16* res = nullptr) {
   const int lr = lane & 31, lh = lane >> 5;
   for (int pass = 0; pass < (res ? 2 : 1); ++pass) {
 #pragma unroll
@@ -177,7 +188,7 @@ DSB_DEV void store_rows32(const f32x16 (&acc)[4], float scale, bf16* buf, bf16* 
     for (int i = 0; i < 8; ++i) {
       const int c = lane + 64 * i, r = c >> 4, col = (c & 15) * 8;
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(buf + r * kRowPitch + col);
-      if (r < nvalid) *reinterpret_cast<bf16x8*>(dst + (long)r * ld + col) = v;
+      if (r < nvalid && col < ncol) *reinterpret_cast<bf16x8*>(dst + (long)r * ld + col) = v;
     }
   }
 }
@@ -204,8 +215,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int qpos = qb.q0 + lr;
   const bool qok = qpos < L;
 
+  const int hd = a.hd;
   bf16x8 qf[8];
-  load_row_frags(a.q, a.ldq, st + qpos, h * HD, qok, lh, qf);
+  load_row_frags(a.q, a.ldq, st + qpos, h * hd, qok, lh, hd, qf);
 
   f32x16 o[4];
 #pragma unroll
@@ -213,14 +225,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
   float m_i = -INFINITY, l_i = 0.f;
-  const float sl2 = kScale * kLog2e;
+  const float sl2 = a.scale * kLog2e;
   const int nt = qb.nt;
 
   const FragOffs fo(lane);
-  const SeqTiles tk(a.k, a.ldk, st, L, w, lane), tv(a.v, a.ldv, st, L, w, lane);
+  const SeqTiles tk(a.k, a.ldk, st, L, w, lane, hd), tv(a.v, a.ldv, st, L, w, lane, hd);
   const unsigned lds0 = lds_addr(smem);
-  tk.load(0, kvh * HD, lds0, w);
-  tv.load(0, kvh * HD, lds0 + TILE * 2, w);
+  tk.load(0, kvh * hd, lds0, w);
+  tv.load(0, kvh * hd, lds0 + TILE * 2, w);
   // The wave computes the tiles with a key at or before its last query
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
@@ -231,8 +243,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
     if (t + 1 < nt) {
       const unsigned nxt = lds0 + (unsigned)(((t + 1) & 1) * 2 * TILE * 2);
-      tk.load((t + 1) * TR, kvh * HD, nxt, w);
-      tv.load((t + 1) * TR, kvh * HD, nxt + TILE * 2, w);
+      tk.load((t + 1) * TR, kvh * hd, nxt, w);
+      tv.load((t + 1) * TR, kvh * hd, nxt + TILE * 2, w);
     }
   };
   for (int t = 0; t < nt_w; ++t) {
@@ -321,8 +333,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     // every wave is done reading
     __syncthreads();
     if (nt_w > 0) {
-      const long r0 = (long)(st + qb.q0) * a.ldc + h * HD;
-      store_rows32(o, 1.f / l_i, smem + w * 32 * kRowPitch, a.ctx + r0, a.ldc, L - qb.q0, lane,
+      const long r0 = (long)(st + qb.q0) * a.ldc + h * hd;
+      store_rows32(o, 1.f / l_i, smem + w * 32 * kRowPitch, a.ctx + r0, a.ldc, L - qb.q0, hd,
+                   lane,
                    a.ores ? a.ores + r0 : nullptr);
     }
     if (qok && lh == 0) a.lse[(long)h * a.ld_stat + st + qpos] = m_i + log2f(l_i);
@@ -336,6 +349,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int dim = df * 32 + 8 * g + 4 * lh;
+        if (dim >= hd) continue;
         bf16x4 ob;
         f32x4 of;
 #pragma unroll
@@ -343,13 +357,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
           of[t] = o[df][4 * g + t] * inv_l;
           ob[t] = (bf16)of[t];
         }
-        *reinterpret_cast<bf16x4*>(a.ctx + row * a.ldc + h * HD + dim) = ob;
-        if (a.o32) *reinterpret_cast<f32x4*>(a.o32 + row * a.ldo32 + h * HD + dim) = of;
+        *reinterpret_cast<bf16x4*>(a.ctx + row * a.ldc + h * hd + dim) = ob;
+        if (a.o32) *reinterpret_cast<f32x4*>(a.o32 + row * a.ldo32 + h * hd + dim) = of;
         if (a.ores) {
           bf16x4 rb;
 #pragma unroll
           for (int t = 0; t < 4; ++t) rb[t] = (bf16)(of[t] - (float)ob[t]);
-          *reinterpret_cast<bf16x4*>(a.ores + row * a.ldc + h * HD + dim) = rb;
+          *reinterpret_cast<bf16x4*>(a.ores + row * a.ldc + h * hd + dim) = rb;
         }
       }
     if (lh == 0) a.lse[(long)h * a.ld_stat + row] = m_i + log2f(l_i);
@@ -369,9 +383,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   const int qpos = qb.q0 + lr;
   const bool qok = qpos < L;
 
+  const int hd = a.hd;
   bf16x8 qf[8], df_[8];
-  load_row_frags(a.q, a.ldq, st + qpos, h * HD, qok, lh, qf);
-  load_row_frags(a.dout, a.lddo, st + qpos, h * HD, qok, lh, df_);
+  load_row_frags(a.q, a.ldq, st + qpos, h * hd, qok, lh, hd, qf);
+  load_row_frags(a.dout, a.lddo, st + qpos, h * hd, qok, lh, hd, df_);
   const float lse2 = qok ? a.lse[(long)h * a.ld_stat + st + qpos] : 0.f;
   // dsum = rowsum(dO∘O) of the wave's rows: the lane's 64 dims of dO (df_)
   // against the same dims of O (ctx + its rounding residual, or the fp32 copy,
@@ -383,7 +398,8 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
     const long orow = (long)(st + (qok ? qpos : 0));
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      const int d0 = h * HD + kk * 16 + lh * 8;
+      if (kk * 16 >= hd) break;
+      const int d0 = h * hd + kk * 16 + lh * 8;
       float ov[8];
       if (a.ores) {
         float rv[8];
@@ -415,14 +431,14 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
-  const float sl2 = kScale * kLog2e;
+  const float sl2 = a.scale * kLog2e;
   const int nt = qb.nt;
 
   const FragOffs fo(lane);
-  const SeqTiles tk(a.k, a.ldk, st, L, w, lane), tv(a.v, a.ldv, st, L, w, lane);
+  const SeqTiles tk(a.k, a.ldk, st, L, w, lane, hd), tv(a.v, a.ldv, st, L, w, lane, hd);
   const unsigned lds0 = lds_addr(smem);
-  tk.load(0, kvh * HD, lds0, w);
-  tv.load(0, kvh * HD, lds0 + TILE * 2, w);
+  tk.load(0, kvh * hd, lds0, w);
+  tv.load(0, kvh * hd, lds0 + TILE * 2, w);
   // The wave computes the tiles with a key at or before its last query
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
@@ -433,8 +449,8 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
     if (t + 1 < nt) {
       const unsigned nxt = lds0 + (unsigned)(((t + 1) & 1) * 2 * TILE * 2);
-      tk.load((t + 1) * TR, kvh * HD, nxt, w);
-      tv.load((t + 1) * TR, kvh * HD, nxt + TILE * 2, w);
+      tk.load((t + 1) * TR, kvh * hd, nxt, w);
+      tv.load((t + 1) * TR, kvh * hd, nxt + TILE * 2, w);
     }
   };
   for (int t = 0; t < nt_w; ++t) {
@@ -500,8 +516,8 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   // every wave is past its last tile read: the stages take the staged rows
   __syncthreads();
   if (nt_w > 0)
-    store_rows32(dq, kScale, smem + w * 32 * kRowPitch, a.dq + (long)(st + qb.q0) * a.lddq + h * HD,
-                 a.lddq, L - qb.q0, lane);
+    store_rows32(dq, a.scale, smem + w * 32 * kRowPitch, a.dq + (long)(st + qb.q0) * a.lddq + h * hd,
+                 a.lddq, L - qb.q0, hd, lane);
 }
 
 // ---------------------------------------------------------------- dK / dV
@@ -522,16 +538,17 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   const bool kok = key < L;
   const int wk_first = k0 + w * 32;  // wave-uniform
 
+  const int hd = a.hd;
   bf16x8 kf_[8], vf_[8];
-  load_row_frags(a.k, a.ldk, st + key, kvh * HD, kok, lh, kf_);
-  load_row_frags(a.v, a.ldv, st + key, kvh * HD, kok, lh, vf_);
+  load_row_frags(a.k, a.ldk, st + key, kvh * hd, kok, lh, hd, kf_);
+  load_row_frags(a.v, a.ldv, st + key, kvh * hd, kok, lh, hd, vf_);
 
   f32x16 dk[4], dv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) { dk[i][r] = 0.f; dv[i][r] = 0.f; }
-  const float sl2 = kScale * kLog2e;
+  const float sl2 = a.scale * kLog2e;
   const FragOffs fo(lane);
 
   // (head, q tile) pairs flattened into one pipelined sequence; with a head
@@ -553,14 +570,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     nl = ok ? a.lse[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
     nd = ok ? a.dsum[(long)hq * a.ld_stat + st + q0 + tid] : 0.f;
   };
-  const SeqTiles tq(a.q, a.ldq, st, L, w, lane), to(a.dout, a.lddo, st, L, w, lane);
+  const SeqTiles tq(a.q, a.ldq, st, L, w, lane, hd), to(a.dout, a.lddo, st, L, w, lane, hd);
   const unsigned lds0 = lds_addr(smem);
   auto stage = [&](int it, int sidx) {
     const int hq = kvh * G + h_lo + it / nq;
     const int q0 = (qt0 + it % nq) * TR;
     const unsigned d = lds0 + (unsigned)(sidx * 2 * TILE * 2);
-    tq.load(q0, hq * HD, d, w);
-    to.load(q0, hq * HD, d + TILE * 2, w);
+    tq.load(q0, hq * hd, d, w);
+    to.load(q0, hq * hd, d + TILE * 2, w);
   };
   if (nit > 0) {
     load_ld(0);
@@ -746,14 +763,16 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     // fp32 partials: kv_part[z][row][m·KV + kvh·128 + dim], m = 0 dK, 1 dV;
     // the lane holds key row `key`, dims d4·32 + 8g + 4·lh .. +3
     if (kok) {
-      const long KV = (long)a.Hkv * HD;
-      float* pr = a.kv_part + ((long)blockIdx.z * a.n + st + key) * 2 * KV + kvh * HD + 4 * lh;
+      const long KV = (long)a.Hkv * hd;
+      float* pr = a.kv_part + ((long)blockIdx.z * a.n + st + key) * 2 * KV + kvh * hd + 4 * lh;
+      const float ks = a.scale;
 #pragma unroll
       for (int d4 = 0; d4 < 4; ++d4)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 k4 = {dk[d4][4 * g] * kScale, dk[d4][4 * g + 1] * kScale,
-                            dk[d4][4 * g + 2] * kScale, dk[d4][4 * g + 3] * kScale};
+          if (d4 * 32 + 8 * g >= hd) continue;
+          const f32x4 k4 = {dk[d4][4 * g] * ks, dk[d4][4 * g + 1] * ks, dk[d4][4 * g + 2] * ks,
+                            dk[d4][4 * g + 3] * ks};
           const f32x4 v4 = {dv[d4][4 * g], dv[d4][4 * g + 1], dv[d4][4 * g + 2], dv[d4][4 * g + 3]};
           *reinterpret_cast<f32x4*>(pr + d4 * 32 + 8 * g) = k4;
           *reinterpret_cast<f32x4*>(pr + KV + d4 * 32 + 8 * g) = v4;
@@ -767,8 +786,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
   if (wk_first < L) {
     bf16* buf = smem + w * 32 * kRowPitch;
     const long row0 = st + wk_first;
-    store_rows32(dk, kScale, buf, a.dk + row0 * a.lddk + kvh * HD, a.lddk, L - wk_first, lane);
-    store_rows32(dv, 1.f, buf, a.dv + row0 * a.lddv + kvh * HD, a.lddv, L - wk_first, lane);
+    store_rows32(dk, a.scale, buf, a.dk + row0 * a.lddk + kvh * hd, a.lddk, L - wk_first, hd,
+                 lane);
+    store_rows32(dv, 1.f, buf, a.dv + row0 * a.lddv + kvh * hd, a.lddv, L - wk_first, hd, lane);
   }
 }
 
@@ -777,7 +797,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
 __global__ __launch_bounds__(256) void dkdv_head_sum_kernel(AttnArgs a, int hs) {
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
-  const long KV = (long)a.Hkv * HD, c4 = 2 * KV / 4;
+  const long KV = (long)a.Hkv * a.hd, c4 = 2 * KV / 4;
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long)N * c4) return;
   const long row = idx / c4, col = (idx % c4) * 4;
@@ -802,7 +822,7 @@ hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
 int attn_dkdv_head_split(const AttnArgs& a) {
   const int G = a.Hkv > 0 ? a.Hq / a.Hkv : 1;
   if (G < 2 || a.n <= 0 || a.n > 1024) return 1;
-  return (long)G * a.n * 2 * a.Hkv * HD <= a.kv_part_elems ? G : 1;
+  return (long)G * a.n * 2 * a.Hkv * a.hd <= a.kv_part_elems ? G : 1;
 }
 
 hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
@@ -813,7 +833,7 @@ hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
   const int hs = a.kv_part ? attn_dkdv_head_split(a) : 1;
   hipLaunchKernelGGL(attn_dkdv_kernel, dim3(a.max_tiles, a.Hkv, hs), dim3(256), 0, s, a);
   if (hs == 1) return hipGetLastError();
-  const long tot = (long)a.n * (2L * a.Hkv * HD / 4);
+  const long tot = (long)a.n * (2L * a.Hkv * a.hd / 4);
   hipLaunchKernelGGL(dkdv_head_sum_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
                      a, hs);
   return hipGetLastError();

@@ -211,7 +211,7 @@ struct GraphSet {  // the cycle's graphs for one attention grid capacity
 
 struct dsb_handle {
   dsb_desc d{};
-  int D, Hq, Hkv, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk, nvc, ce_bn;
+  int D, Hq, Hkv, hd, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk, nvc, ce_bn;
   int gemm_cfg = -1;  // forced dense-product tile (GEMM_*), -1 by shape
   int tile_cap = 0;   // attention grid capacity of the current cycle
   float s;
@@ -453,13 +453,13 @@ int finalize(dsb_handle* h) {
     h->part_elems = need;
     if (need > 0) CKR(dalloc(h, &h->part, need));
   }
-  CKR(dalloc(h, &h->cosb, NN * 64));
-  CKR(dalloc(h, &h->sinb, NN * 64));
+  CKR(dalloc(h, &h->cosb, NN * (h->hd / 2)));
+  CKR(dalloc(h, &h->sinb, NN * (h->hd / 2)));
   CKR(dalloc(h, &h->inv_freq, 64));
   CKR(dalloc(h, &h->labels, NN));
   {
-    float inv[64];
-    rope_inv_freq_host(128, h->d.rope_theta, h->d.rope_type, h->d.rope_factor,
+    float inv[64] = {};
+    rope_inv_freq_host(h->hd, h->d.rope_theta, h->d.rope_type, h->d.rope_factor,
                        h->d.rope_low_freq_factor, h->d.rope_high_freq_factor,
                        h->d.rope_orig_max_pos, inv);
     CK(hipMemcpy(h->inv_freq, inv, sizeof(inv), hipMemcpyHostToDevice));
@@ -850,7 +850,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       h->kpos = 0;  // kernel-timing records restart with every cycle
       {
         KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
-        LK(rope_table(h->d_pos, N, nd, h->inv_freq, 64, h->cosb, h->sinb, st));
+        LK(rope_table(h->d_pos, N, nd, h->inv_freq, h->hd / 2, h->cosb, h->sinb, st));
       }
       {
         KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
@@ -928,11 +928,12 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     at.tiles = h->d_tiles; at.tiles_k = h->d_tiles_k; at.ntiles_dev = &h->d_hdr->ntiles;
     at.max_tiles = h->tile_cap;
     at.Hq = h->Hq; at.Hkv = h->Hkv; at.n_dev = nd; at.n = N;
+    at.hd = h->hd; at.scale = 1.f / std::sqrt((float)h->hd);
     // dK/dV head-split partials (short cycles) in the TN workspace, which
     // holds nothing while the attention passes run
     at.kv_part = h->tn_work; at.kv_part_elems = h->tn_work_elems;
     // one causal attention matmul = Hq·Hd·S flops (S = sum L(L+1), unmasked pairs ×2)
-    const double au = Hq * 128.0;
+    const double au = (double)Hq * h->hd;
     const double arow = 2.0 * (q + 2.0 * kv);
     LayerState& ls = h->layers[li];
     const bf16* x = h->layer_in[li];
@@ -984,10 +985,10 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       KScope ks(h, st, "rope_fwd", 0, 0, 0, 2.0 * (q + kv) * 2 + 512.0, 0, 0);
       if (sqkv)
         LK(rope_fwd(h->q_in[li], h->ld_q_in, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq,
-                    h->Hkv, qnw, knw, eps, st, h->k_in[li], h->ld_k_in));
+                    h->Hkv, h->hd, qnw, knw, eps, st, h->k_in[li], h->ld_k_in));
       else
         LK(rope_fwd(h->qkv_pre, W3, h->qk, q + kv, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
-                    h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+                    h->hd, h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     {
       KScope ks(h, st, "attn_fwd", 0, 2.0 * au, 0, arow + 4.0 * q + 4.0 * Hq, 0, 0);
@@ -1141,10 +1142,10 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       // the q/k-norm backward (Qwen3) reads the pre-norm q/k: saved or recomputed
       if (sqkv && h->qwen)
         LK(rope_bwd(h->gqkv, W3, h->q_in[li], h->ld_q_in, h->cosb, h->sinb, N, nd, h->Hq,
-                    h->Hkv, qnw, knw, eps, st, h->k_in[li], h->ld_k_in));
+                    h->Hkv, h->hd, qnw, knw, eps, st, h->k_in[li], h->ld_k_in));
       else
         LK(rope_bwd(h->gqkv, W3, h->qkv_pre, W3, h->cosb, h->sinb, N, nd, h->Hq, h->Hkv,
-                    h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
+                    h->hd, h->qwen ? qnw : nullptr, h->qwen ? knw : nullptr, eps, st));
     }
     int rest_qkv[3] = {0, 0, 0};
     if (hq) {
@@ -1411,7 +1412,8 @@ const char* dsb_last_error(const dsb_handle* h) {
 int dsb_create(const dsb_desc* d, dsb_handle** out) {
   if (!d || !out) return fail(nullptr, "dsb_create: null argument");
   if (d->abi_version != DSB_ABI_VERSION) return fail(nullptr, "dsb_create: ABI version mismatch");
-  if (d->head_dim != 128) return fail(nullptr, "dsb_create: head_dim must be 128");
+  if (d->head_dim != 128 && d->head_dim != 64)
+    return fail(nullptr, "dsb_create: head_dim must be 128 or 64");
   if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->n_heads % d->n_kv_heads)
     return fail(nullptr, "dsb_create: n_heads must be a positive multiple of n_kv_heads");
   if (d->lora_rank <= 0 || d->lora_rank % 8 || d->lora_rank > 64)
@@ -1429,7 +1431,8 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
   auto* h = new dsb_handle();
   h->d = *d;
   h->D = d->hidden; h->Hq = d->n_heads; h->Hkv = d->n_kv_heads;
-  h->q = h->Hq * 128; h->kv = h->Hkv * 128; h->W3 = h->q + 2 * h->kv;
+  h->hd = d->head_dim;
+  h->q = h->Hq * h->hd; h->kv = h->Hkv * h->hd; h->W3 = h->q + 2 * h->kv;
   h->I = d->intermediate; h->V = d->vocab; h->r = d->lora_rank; h->L = d->n_layers;
   h->N = d->s_max; h->s = d->lora_scaling; h->qwen = d->family == DSB_FAMILY_QWEN3;
   h->max_tiles = max_tiles_for(d->s_max, std::min(d->max_seqs, d->s_max));
@@ -1926,25 +1929,28 @@ int dsb_op_rope_table(const int32_t* pos, int n, const float* inv_freq, int half
 }
 
 int dsb_op_rope(const void* qkv_pre, int64_t ldin, void* qk_out, int64_t ldout, const float* cos_t,
-                const float* sin_t, int n, int Hq, int Hkv, const void* q_norm, const void* k_norm,
-                float eps, void* stream) {
+                const float* sin_t, int n, int Hq, int Hkv, int head_dim, const void* q_norm,
+                const void* k_norm, float eps, void* stream) {
   if (ldin % 8 || ldout % 8 || !aligned16(qkv_pre, qk_out, q_norm, k_norm, cos_t, sin_t))
     return fail(nullptr, "dsb_op_rope: row strides must be multiples of 8, pointers 16-byte aligned");
+  if (head_dim != 128 && head_dim != 64) return fail(nullptr, "dsb_op_rope: head_dim 128 or 64");
   hipStream_t s = (hipStream_t)stream;
   OPCK(rope_fwd((const bf16*)qkv_pre, ldin, (bf16*)qk_out, ldout, cos_t, sin_t, n, nullptr, Hq,
-                Hkv, (const bf16*)q_norm, (const bf16*)k_norm, eps, s));
+                Hkv, head_dim, (const bf16*)q_norm, (const bf16*)k_norm, eps, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
 }
 
 int dsb_op_rope_bwd(void* g, int64_t ldg, const void* qkv_pre, int64_t ldp, const float* cos_t,
-                    const float* sin_t, int n, int Hq, int Hkv, const void* q_norm,
+                    const float* sin_t, int n, int Hq, int Hkv, int head_dim, const void* q_norm,
                     const void* k_norm, float eps, void* stream) {
   if (ldg % 8 || ldp % 8 || !aligned16(g, qkv_pre, q_norm, k_norm, cos_t, sin_t))
     return fail(nullptr, "dsb_op_rope_bwd: row strides must be multiples of 8, pointers 16-byte aligned");
+  if (head_dim != 128 && head_dim != 64)
+    return fail(nullptr, "dsb_op_rope_bwd: head_dim 128 or 64");
   hipStream_t s = (hipStream_t)stream;
   OPCK(rope_bwd((bf16*)g, ldg, (const bf16*)qkv_pre, ldp, cos_t, sin_t, n, nullptr, Hq, Hkv,
-                (const bf16*)q_norm, (const bf16*)k_norm, eps, s));
+                head_dim, (const bf16*)q_norm, (const bf16*)k_norm, eps, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
 }
@@ -2000,8 +2006,10 @@ extern "C" {
 
 int dsb_op_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
                     int64_t ldv, void* ctx, int64_t ldc, float* o32, float* lse,
-                    const int32_t* seq_lens, int nseq, int Hq, int Hkv, void* stream) {
+                    const int32_t* seq_lens, int nseq, int Hq, int Hkv, int head_dim,
+                    void* stream) {
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(nullptr, "attn: bad head counts");
+  if (head_dim != 128 && head_dim != 64) return fail(nullptr, "attn: head_dim 128 or 64");
   hipStream_t s = (hipStream_t)stream;
   TmpDev tmp;
   AttnArgs a{};
@@ -2009,7 +2017,8 @@ int dsb_op_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
   if (attn_setup(seq_lens, nseq, tmp, a, &n)) return -1;
   a.q = (const bf16*)q; a.ldq = ldq; a.k = (const bf16*)k; a.ldk = ldk;
   a.v = (const bf16*)v; a.ldv = ldv; a.ctx = (bf16*)ctx; a.ldc = ldc;
-  a.o32 = o32; a.ldo32 = (long)Hq * 128; a.lse = lse; a.ld_stat = n; a.Hq = Hq; a.Hkv = Hkv;
+  a.o32 = o32; a.ldo32 = (long)Hq * head_dim; a.lse = lse; a.ld_stat = n; a.Hq = Hq; a.Hkv = Hkv;
+  a.hd = head_dim; a.scale = 1.f / std::sqrt((float)head_dim);
   OPCK(attn_fwd(a, s));
   OPCK(hipStreamSynchronize(s));
   return 0;
@@ -2019,8 +2028,9 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
                     int64_t ldv, const float* o32, const float* lse, const void* dout,
                     int64_t lddo, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
                     int64_t lddv, const int32_t* seq_lens, int nseq, int Hq, int Hkv,
-                    void* stream) {
+                    int head_dim, void* stream) {
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(nullptr, "attn: bad head counts");
+  if (head_dim != 128 && head_dim != 64) return fail(nullptr, "attn: head_dim 128 or 64");
   if (!o32 || !lse) return fail(nullptr, "attn: o32 and lse from the forward are required");
   if (ldq % 8 || ldk % 8 || ldv % 8 || lddo % 8 ||
       (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)o32) & 15))
@@ -2033,13 +2043,14 @@ int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, cons
   float* dsum = tmp.alloc<float>((size_t)Hq * (n + 1));
   if (!dsum) return fail(nullptr, "attn: hipMalloc failed");
   a.q = (const bf16*)q; a.ldq = ldq; a.k = (const bf16*)k; a.ldk = ldk;
-  a.v = (const bf16*)v; a.ldv = ldv; a.o32 = (float*)o32; a.ldo32 = (long)Hq * 128;
+  a.v = (const bf16*)v; a.ldv = ldv; a.o32 = (float*)o32; a.ldo32 = (long)Hq * head_dim;
+  a.hd = head_dim; a.scale = 1.f / std::sqrt((float)head_dim);
   a.lse = (float*)lse; a.dsum = dsum; a.ld_stat = n; a.dout = (const bf16*)dout; a.lddo = lddo;
   a.dq = (bf16*)dq; a.lddq = lddq; a.dk = (bf16*)dk; a.lddk = lddk; a.dv = (bf16*)dv;
   a.lddv = lddv; a.Hq = Hq; a.Hkv = Hkv;
   // the dK/dV head split the cycle takes for short token counts, partials in
   // a buffer allocated for the call
-  a.kv_part_elems = (long)(Hq / Hkv) * n * 2 * Hkv * 128;
+  a.kv_part_elems = (long)(Hq / Hkv) * n * 2 * Hkv * head_dim;
   if (attn_dkdv_head_split(a) > 1) {
     a.kv_part = tmp.alloc<float>((size_t)a.kv_part_elems);
     if (!a.kv_part) return fail(nullptr, "attn: hipMalloc failed");

@@ -20,26 +20,27 @@ hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_
                       int half, float* cosb, float* sinb, hipStream_t s);
 // q heads of a row at in / pre (row stride ldin / ldp); k heads at ink / prek
 // (stride ldk / ldpk), by default right after the q heads of the same row.
+// hd: head_dim, 128 or 64 (cos/sin rows of hd/2).
 hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
-                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv, int hd,
                     const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
                     const bf16* ink = nullptr, long ldk = 0);
 hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* cosb,
-                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv, int hd,
                     const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
                     const bf16* prek = nullptr, long ldpk = 0);
 hipError_t swiglu_h(const bf16* gu, long ldgu, bf16* h, long ldh, int n, const int* n_dev,
                     int I, hipStream_t s);
 
 // ---- attention.hip
-// Packed varlen causal GQA attention, head_dim 128. `tiles` holds one int4
+// Packed varlen causal GQA attention, head_dim 128 or 64. `tiles` holds one int4
 // (seq_start, seq_len, tile_start, 0) per 128-token tile of every sequence;
 // `ntiles_dev` is the live tile count (grid is sized for `max_tiles`).
 struct AttnArgs {
-  const bf16* q; long ldq;   // [n, Hq*128] (post-RoPE)
-  const bf16* k; long ldk;   // [n, Hkv*128] (post-RoPE)
-  const bf16* v; long ldv;   // [n, Hkv*128]
-  bf16* ctx; long ldc;       // fwd out [n, Hq*128]
+  const bf16* q; long ldq;   // [n, Hq*hd] (post-RoPE)
+  const bf16* k; long ldk;   // [n, Hkv*hd] (post-RoPE)
+  const bf16* v; long ldv;   // [n, Hkv*hd]
+  bf16* ctx; long ldc;       // fwd out [n, Hq*hd]
   float* o32;                // fwd out fp32 copy of ctx, ld = ldo32; null: none
   long ldo32;
   bf16* ores;                // fwd out bf16(O − bf16(O)), the rounding residual of
@@ -57,10 +58,12 @@ struct AttnArgs {
   const int* ntiles_dev;
   int max_tiles;
   int Hq, Hkv;
+  int hd = 128;                          // head_dim: 128 or 64
+  float scale = 0.08838834764831845f;    // 1/sqrt(hd)
   const int* n_dev;  // live token count (the dK/dV head-split sum reads it)
   int n;
   // fp32 workspace for the dK/dV pass's head split (null: none), at least
-  // (Hq / Hkv) · n · 2 · Hkv·128 floats when the split applies
+  // (Hq / Hkv) · n · 2 · Hkv·hd floats when the split applies
   float* kv_part = nullptr;
   long kv_part_elems = 0;
 };

@@ -199,58 +199,61 @@ __global__ void rope_table_kernel(const int* __restrict__ pos, int n, const int*
   sinb[idx] = s;
 }
 
-// Eight lanes per head (head_dim 128): lane i of a head's group owns the
-// rotate-half pairs (8i + e, 64 + 8i + e), e = 0..7, moved as 16-byte
-// vectors; one wave covers 8 heads of one token (q heads, then k heads), and
-// per-head sums reduce over the group's 8 lanes.
+// HD/16 lanes per head (8 at head_dim 128, 4 at 64): lane i of a head's
+// group owns the rotate-half pairs (8i + e, HD/2 + 8i + e), e = 0..7, moved as
+// 16-byte vectors; one wave covers 64/(HD/16) heads of one token (q heads,
+// then k heads), and per-head sums reduce over the group's lanes.
 //   in : the q heads of a row at in (stride ldin) and its k heads at ink
 //        (stride ldk): pre-norm, pre-RoPE projection outputs, either the
 //        [q | k | v] rows of the recompute or separate saved q / k buffers
 //   out: qk row [q | k] after (optional per-head RMSNorm, rounded to bf16) + RoPE
-DSB_DEV float group8_sum(float v) {
+template <int LPH>
+DSB_DEV float group_sum(float v) {
   v += __shfl_xor(v, 1, 64);
   v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
+  if constexpr (LPH == 8) v += __shfl_xor(v, 4, 64);
   return v;
 }
 
+template <int HD>
 __global__ __launch_bounds__(256) void rope_fwd_kernel(
     const bf16* __restrict__ in, long ldin, const bf16* __restrict__ ink, long ldk,
     bf16* __restrict__ out, long ldout,
     const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
     const int* n_dev, int Hq, int Hkv, const bf16* __restrict__ qn_w,
     const bf16* __restrict__ kn_w, float eps) {
+  constexpr int LPH = HD / 16, HPW = 64 / LPH, HALF = HD / 2;
   int N = n;
   if (n_dev) N = min(N, *n_dev);
-  const int H = Hq + Hkv, HG = (H + 7) / 8;
+  const int H = Hq + Hkv, HG = (H + HPW - 1) / HPW;
   const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= (long)N * HG) return;
-  const int t = (int)(item / HG), l = threadIdx.x & 63, i = l & 7;
-  const int hh = (int)(item % HG) * 8 + (l >> 3);
+  const int t = (int)(item / HG), l = threadIdx.x & 63, i = l % LPH;
+  const int hh = (int)(item % HG) * HPW + l / LPH;
   const bool live = hh < H;
   const int h = live ? hh : H - 1;
-  const bf16* src = h < Hq ? in + (long)t * ldin + h * 128 + 8 * i
-                            : ink + (long)t * ldk + (h - Hq) * 128 + 8 * i;
+  const bf16* src = h < Hq ? in + (long)t * ldin + h * HD + 8 * i
+                            : ink + (long)t * ldk + (h - Hq) * HD + 8 * i;
   float x1[8], x2[8];
   unpack8(ldg128(src), x1);
-  unpack8(ldg128(src + 64), x2);
+  unpack8(ldg128(src + HALF), x2);
   const bf16* nw = h < Hq ? qn_w : kn_w;
   if (nw) {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
-    const float inv = rsqrtf(group8_sum(ss) / 128.f + eps);
+    const float inv = rsqrtf(group_sum<LPH>(ss) / (float)HD + eps);
     float w1[8], w2[8];
     unpack8(ldg128(nw + 8 * i), w1);
-    unpack8(ldg128(nw + 64 + 8 * i), w2);
+    unpack8(ldg128(nw + HALF + 8 * i), w2);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       x1[e] = (float)(bf16)((x1[e] * inv) * w1[e]);
       x2[e] = (float)(bf16)((x2[e] * inv) * w2[e]);
     }
   }
-  const f32x4* cp = reinterpret_cast<const f32x4*>(cosb + (long)t * 64 + 8 * i);
-  const f32x4* sp = reinterpret_cast<const f32x4*>(sinb + (long)t * 64 + 8 * i);
+  const f32x4* cp = reinterpret_cast<const f32x4*>(cosb + (long)t * HALF + 8 * i);
+  const f32x4* sp = reinterpret_cast<const f32x4*>(sinb + (long)t * HALF + 8 * i);
   const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
   const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
@@ -261,36 +264,38 @@ __global__ __launch_bounds__(256) void rope_fwd_kernel(
     o2[e] = x2[e] * c[e] + x1[e] * sn[e];
   }
   if (live) {
-    bf16* dst = out + (long)t * ldout + h * 128 + 8 * i;
+    bf16* dst = out + (long)t * ldout + h * HD + 8 * i;
     stg128(dst, pack8(o1));
-    stg128(dst + 64, pack8(o2));
+    stg128(dst + HALF, pack8(o2));
   }
 }
 
-// In-place RoPE backward on g[:, :(Hq+Hkv)*128] (then the per-head RMSNorm
+// In-place RoPE backward on g[:, :(Hq+Hkv)*HD] (then the per-head RMSNorm
 // backward against the pre-norm projection output when norm weights are given);
 // same lane layout as the forward.
+template <int HD>
 __global__ __launch_bounds__(256) void rope_bwd_kernel(
     bf16* __restrict__ g, long ldg, const bf16* __restrict__ pre, long ldp,
     const bf16* __restrict__ prek, long ldpk,
     const float* __restrict__ cosb, const float* __restrict__ sinb, int n,
     const int* n_dev, int Hq, int Hkv, const bf16* __restrict__ qn_w,
     const bf16* __restrict__ kn_w, float eps) {
+  constexpr int LPH = HD / 16, HPW = 64 / LPH, HALF = HD / 2;
   int N = n;
   if (n_dev) N = min(N, *n_dev);
-  const int H = Hq + Hkv, HG = (H + 7) / 8;
+  const int H = Hq + Hkv, HG = (H + HPW - 1) / HPW;
   const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= (long)N * HG) return;
-  const int t = (int)(item / HG), l = threadIdx.x & 63, i = l & 7;
-  const int hh = (int)(item % HG) * 8 + (l >> 3);
+  const int t = (int)(item / HG), l = threadIdx.x & 63, i = l % LPH;
+  const int hh = (int)(item % HG) * HPW + l / LPH;
   const bool live = hh < H;
   const int h = live ? hh : H - 1;
-  bf16* gp = g + (long)t * ldg + h * 128 + 8 * i;
+  bf16* gp = g + (long)t * ldg + h * HD + 8 * i;
   float g1[8], g2[8];
   unpack8(ldg128(gp), g1);
-  unpack8(ldg128(gp + 64), g2);
-  const f32x4* cp = reinterpret_cast<const f32x4*>(cosb + (long)t * 64 + 8 * i);
-  const f32x4* sp = reinterpret_cast<const f32x4*>(sinb + (long)t * 64 + 8 * i);
+  unpack8(ldg128(gp + HALF), g2);
+  const f32x4* cp = reinterpret_cast<const f32x4*>(cosb + (long)t * HALF + 8 * i);
+  const f32x4* sp = reinterpret_cast<const f32x4*>(sinb + (long)t * HALF + 8 * i);
   const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
   const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
@@ -302,17 +307,17 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(
   }
   const bf16* nw = h < Hq ? qn_w : kn_w;
   if (nw) {
-    const bf16* xp = h < Hq ? pre + (long)t * ldp + h * 128 + 8 * i
-                            : prek + (long)t * ldpk + (h - Hq) * 128 + 8 * i;
+    const bf16* xp = h < Hq ? pre + (long)t * ldp + h * HD + 8 * i
+                            : prek + (long)t * ldpk + (h - Hq) * HD + 8 * i;
     float x1[8], x2[8], w1[8], w2[8];
     unpack8(ldg128(xp), x1);
-    unpack8(ldg128(xp + 64), x2);
+    unpack8(ldg128(xp + HALF), x2);
     unpack8(ldg128(nw + 8 * i), w1);
-    unpack8(ldg128(nw + 64 + 8 * i), w2);
+    unpack8(ldg128(nw + HALF + 8 * i), w2);
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
-    const float inv = rsqrtf(group8_sum(ss) / 128.f + eps);
+    const float inv = rsqrtf(group_sum<LPH>(ss) / (float)HD + eps);
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -320,7 +325,7 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(
       r2[e] *= w2[e];
       dot += r1[e] * (x1[e] * inv) + r2[e] * (x2[e] * inv);
     }
-    const float k = group8_sum(dot) / 128.f;
+    const float k = group_sum<LPH>(dot) / (float)HD;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       r1[e] = (r1[e] - (x1[e] * inv) * k) * inv;
@@ -329,7 +334,7 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(
   }
   if (live) {
     stg128(gp, pack8(r1));
-    stg128(gp + 64, pack8(r2));
+    stg128(gp + HALF, pack8(r2));
   }
 }
 
@@ -393,32 +398,46 @@ hipError_t rope_table(const int* pos, int n, const int* n_dev, const float* inv_
 }
 
 hipError_t rope_fwd(const bf16* in, long ldin, bf16* out, long ldout, const float* cosb,
-                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv, int hd,
                     const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
                     const bf16* ink, long ldk) {
-  const long items = (long)n * ((Hq + Hkv + 7) / 8);
+  if (hd != 128 && hd != 64) return hipErrorInvalidValue;
+  const int hpw = 64 / (hd / 16);
+  const long items = (long)n * ((Hq + Hkv + hpw - 1) / hpw);
   if (items <= 0) return hipSuccess;
   if (!ink) {
-    ink = in + (long)Hq * 128;
+    ink = in + (long)Hq * hd;
     ldk = ldin;
   }
-  hipLaunchKernelGGL(rope_fwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, in,
-                     ldin, ink, ldk, out, ldout, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+  const dim3 grid((unsigned)((items + 3) / 4));
+  if (hd == 128)
+    hipLaunchKernelGGL(rope_fwd_kernel<128>, grid, dim3(256), 0, s, in, ldin, ink, ldk, out,
+                       ldout, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+  else
+    hipLaunchKernelGGL(rope_fwd_kernel<64>, grid, dim3(256), 0, s, in, ldin, ink, ldk, out,
+                       ldout, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
   return hipGetLastError();
 }
 
 hipError_t rope_bwd(bf16* g, long ldg, const bf16* pre, long ldp, const float* cosb,
-                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv,
+                    const float* sinb, int n, const int* n_dev, int Hq, int Hkv, int hd,
                     const bf16* qn_w, const bf16* kn_w, float eps, hipStream_t s,
                     const bf16* prek, long ldpk) {
-  const long items = (long)n * ((Hq + Hkv + 7) / 8);
+  if (hd != 128 && hd != 64) return hipErrorInvalidValue;
+  const int hpw = 64 / (hd / 16);
+  const long items = (long)n * ((Hq + Hkv + hpw - 1) / hpw);
   if (items <= 0) return hipSuccess;
   if (!prek) {
-    prek = pre + (long)Hq * 128;
+    prek = pre + (long)Hq * hd;
     ldpk = ldp;
   }
-  hipLaunchKernelGGL(rope_bwd_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, g,
-                     ldg, pre, ldp, prek, ldpk, cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+  const dim3 grid((unsigned)((items + 3) / 4));
+  if (hd == 128)
+    hipLaunchKernelGGL(rope_bwd_kernel<128>, grid, dim3(256), 0, s, g, ldg, pre, ldp, prek, ldpk,
+                       cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
+  else
+    hipLaunchKernelGGL(rope_bwd_kernel<64>, grid, dim3(256), 0, s, g, ldg, pre, ldp, prek, ldpk,
+                       cosb, sinb, n, n_dev, Hq, Hkv, qn_w, kn_w, eps);
   return hipGetLastError();
 }
 

@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 # timing); the in-tree build is the default.
 LIB_PATH = os.environ.get("DSB_LIB") or os.path.join(LIB_DIR, "libdsb.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
 ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
@@ -124,17 +124,17 @@ _SIGS = {
     "dsb_op_rope_table": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p,
                                   c_void_p]),
     "dsb_op_rope": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int,
-                            c_int, c_int, c_void_p, c_void_p, c_float, c_void_p]),
+                            c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p]),
     "dsb_op_rope_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
-                                c_int, c_int, c_int, c_void_p, c_void_p, c_float,
+                                c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
                                 c_void_p]),
     "dsb_op_attn_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                 c_void_p, c_int64, c_void_p, c_void_p, POINTER(c_int32),
-                                c_int, c_int, c_int, c_void_p]),
+                                c_int, c_int, c_int, c_int, c_void_p]),
     "dsb_op_attn_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                 c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
                                 c_void_p, c_int64, c_void_p, c_int64, POINTER(c_int32),
-                                c_int, c_int, c_int, c_void_p]),
+                                c_int, c_int, c_int, c_int, c_void_p]),
     "dsb_op_head": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, POINTER(c_int32), c_int,
                             c_int, c_int, c_int, c_int, c_void_p, POINTER(c_float),
                             POINTER(c_int), c_void_p]),

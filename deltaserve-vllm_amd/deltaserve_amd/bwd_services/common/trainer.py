@@ -95,7 +95,8 @@ class LoraSftTrainerService(BackwardService):
         self.L = int(meta["num_hidden_layers"])
         self.Hq = int(meta["num_attention_heads"])
         self.Hkv = int(meta["num_key_value_heads"])
-        self.Hd = int(meta["head_dim"])
+        # head_dim as ft_meta.py:144-145 states it (hidden / heads when absent)
+        self.Hd = int(meta.get("head_dim") or self.D // self.Hq)
         self.q_size, self.kv_size = self.Hq * self.Hd, self.Hkv * self.Hd
         self.inter = int(meta["intermediate_size"])
         self.theta = float(meta["rope_theta"])

@@ -1,6 +1,9 @@
 """The BASELINE workload configurations and their seeded synthetic inputs.
 
-C1 is the reference's CPU-runnable case; C2–C5 run bf16 on one MI355X. The
+C1 is the reference's CPU-runnable case; C2–C5 run bf16 on one MI355X;
+llama32-1b is the model of the reference's end-to-end adapter test
+(tests/test_adapter_save_e2e.py: Llama-3.2-1B, max_lora_rank 8), the
+head_dim-64 case. Hd is the head_dim (128 when absent). The
 sequence-length rule: lengths uniform in [lo, hi] from a seeded generator;
 when a total is fixed, a deterministic ±1 round-robin walk within the bounds
 makes them sum to it.
@@ -35,6 +38,12 @@ CONFIGS = {
                total=16384, tie=False,
                rope_scaling={"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
                              "high_freq_factor": 4.0, "original_max_position_embeddings": 8192.0}),
+    "llama32-1b": dict(name="llama3.2-1b", family="llama3", L=16, D=2048, Hq=32, Hkv=8, Hd=64,
+                       I=8192, V=128256, r=8, alpha=16, theta=5e5, eps=1e-5, nseq=8, lo=64,
+                       hi=512, total=2048, tie=True,
+                       rope_scaling={"rope_type": "llama3", "factor": 32.0,
+                                     "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                     "original_max_position_embeddings": 8192.0}),
 }
 
 
@@ -61,12 +70,13 @@ def algorithmic_flops(cfg: dict, seq_lens) -> dict:
     projections (Z, gZ, gA, gB, gx, forward delta) and the LM head (logits +
     dH; the LSE-pass recompute is not counted)."""
     L, D, I, V, r = cfg["L"], cfg["D"], cfg["I"], cfg["V"], cfg["r"]
-    q, kv = cfg["Hq"] * 128, cfg["Hkv"] * 128
+    hd = cfg.get("Hd", 128)
+    q, kv = cfg["Hq"] * hd, cfg["Hkv"] * hd
     N = sum(seq_lens)
     M = sum(max(s - 1, 0) for s in seq_lens)
     S = sum(s * (s + 1) for s in seq_lens)
     dense = L * N * (4 * D * (q + 2 * kv) + 4 * D * q + 10 * D * I)
-    attn = L * 7 * cfg["Hq"] * 128 * S
+    attn = L * 7 * cfg["Hq"] * hd * S
     lora = L * N * 6 * r * (7 * D + 2 * q + 2 * kv + 3 * I)
     head = 4 * M * D * V
     return {"dense": dense, "attention": attn, "lora": lora, "head": head,

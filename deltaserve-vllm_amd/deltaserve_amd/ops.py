@@ -144,12 +144,13 @@ def rope_cos_sin(positions, inv_freq):
 
 
 def apply_rope(qkv_pre, Hq, Hkv, cos, sin, q_norm=None, k_norm=None, eps=1e-6):
-    """ops.py:68-73 (+ qwen3.py:96-107): rotated [q | k] of a [n, q+2kv] row block."""
+    """ops.py:68-73 (+ qwen3.py:96-107): rotated [q | k] of a [n, q+2kv] row block
+    (head_dim = 2·cos.shape[1]: 128 or 64)."""
     _dev(qkv_pre, cos, sin)
-    n = qkv_pre.shape[0]
-    out = torch.empty(n, (Hq + Hkv) * 128, dtype=BF16, device=qkv_pre.device)
+    n, hd = qkv_pre.shape[0], 2 * cos.shape[1]
+    out = torch.empty(n, (Hq + Hkv) * hd, dtype=BF16, device=qkv_pre.device)
     L.check(L.load().dsb_op_rope(_p(qkv_pre), _ld(qkv_pre), _p(out), _ld(out), _p(cos), _p(sin),
-                                 n, Hq, Hkv, _p(q_norm), _p(k_norm), float(eps), _stream()),
+                                 n, Hq, Hkv, hd, _p(q_norm), _p(k_norm), float(eps), _stream()),
             what="dsb_op_rope")
     return out
 
@@ -158,37 +159,42 @@ def rope_backward_(g, qkv_pre, Hq, Hkv, cos, sin, q_norm=None, k_norm=None, eps=
     """ops.py:76-81 (+ qwen3.py:133-144), in place on g's [q | k] columns."""
     _dev(g, qkv_pre, cos, sin)
     L.check(L.load().dsb_op_rope_bwd(_p(g), _ld(g), _p(qkv_pre), _ld(qkv_pre), _p(cos), _p(sin),
-                                     g.shape[0], Hq, Hkv, _p(q_norm), _p(k_norm), float(eps),
-                                     _stream()), what="dsb_op_rope_bwd")
+                                     g.shape[0], Hq, Hkv, 2 * cos.shape[1], _p(q_norm),
+                                     _p(k_norm), float(eps), _stream()), what="dsb_op_rope_bwd")
     return g
 
 
 # ---------------------------------------------------------------- attention
 
-def attn_forward(q, k, v, seq_lens, Hq, Hkv):
-    """attention.py:20-45 over packed rows: (ctx bf16, o32 fp32, lse [Hq, n] log2)."""
+def attn_forward(q, k, v, seq_lens, Hq, Hkv, head_dim=None):
+    """attention.py:20-45 over packed rows: (ctx bf16, o32 fp32, lse [Hq, n] log2);
+    head_dim (128 or 64) defaults to q's width over Hq."""
     _dev(q, k, v)
     n = q.shape[0]
-    ctx = torch.empty(n, Hq * 128, dtype=BF16, device=q.device)
-    o32 = torch.empty(n, Hq * 128, dtype=torch.float32, device=q.device)
+    hd = head_dim or q.shape[1] // Hq
+    ctx = torch.empty(n, Hq * hd, dtype=BF16, device=q.device)
+    o32 = torch.empty(n, Hq * hd, dtype=torch.float32, device=q.device)
     lse = torch.empty(Hq, max(n, 1), dtype=torch.float32, device=q.device)
     L.check(L.load().dsb_op_attn_fwd(_p(q), _ld(q), _p(k), _ld(k), _p(v), _ld(v), _p(ctx),
                                      _ld(ctx), _p(o32), _p(lse), L.i32_array(seq_lens),
-                                     len(seq_lens), Hq, Hkv, _stream()), what="dsb_op_attn_fwd")
+                                     len(seq_lens), Hq, Hkv, hd, _stream()),
+            what="dsb_op_attn_fwd")
     return ctx, o32, lse
 
 
-def attn_backward(q, k, v, o32, lse, dout, seq_lens, Hq, Hkv):
-    """attention.py:48-112: (dq, dk, dv) bf16 in [n, H*128]."""
+def attn_backward(q, k, v, o32, lse, dout, seq_lens, Hq, Hkv, head_dim=None):
+    """attention.py:48-112: (dq, dk, dv) bf16 in [n, H*head_dim]."""
     _dev(q, k, v, o32, lse, dout)
     n = q.shape[0]
-    dq = torch.empty(n, Hq * 128, dtype=BF16, device=q.device)
-    dk = torch.empty(n, Hkv * 128, dtype=BF16, device=q.device)
-    dv = torch.empty(n, Hkv * 128, dtype=BF16, device=q.device)
+    hd = head_dim or q.shape[1] // Hq
+    dq = torch.empty(n, Hq * hd, dtype=BF16, device=q.device)
+    dk = torch.empty(n, Hkv * hd, dtype=BF16, device=q.device)
+    dv = torch.empty(n, Hkv * hd, dtype=BF16, device=q.device)
     L.check(L.load().dsb_op_attn_bwd(_p(q), _ld(q), _p(k), _ld(k), _p(v), _ld(v), _p(o32),
                                      _p(lse), _p(dout), _ld(dout), _p(dq), _ld(dq), _p(dk),
                                      _ld(dk), _p(dv), _ld(dv), L.i32_array(seq_lens),
-                                     len(seq_lens), Hq, Hkv, _stream()), what="dsb_op_attn_bwd")
+                                     len(seq_lens), Hq, Hkv, hd, _stream()),
+            what="dsb_op_attn_bwd")
     return dq, dk, dv
 
 

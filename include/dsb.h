@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DSB_ABI_VERSION 4
+#define DSB_ABI_VERSION 5
 
 enum { DSB_FAMILY_LLAMA3 = 0, DSB_FAMILY_QWEN3 = 1 };
 enum { DSB_ROPE_DEFAULT = 0, DSB_ROPE_LINEAR = 1, DSB_ROPE_LLAMA3 = 2 };
@@ -39,7 +39,7 @@ typedef struct dsb_handle dsb_handle;
 
 /* Model and trainer constants: the backward `meta` dict of
  * deltaserve-plugin/deltaserve/ft_meta.py:131-213 plus the AdamW settings of
- * trainer.py:252-256. head_dim must be 128; lora_rank a multiple of 8 in
+ * trainer.py:252-256. head_dim 128 or 64; lora_rank a multiple of 8 in
  * [8, 64] (the rank-r kernels tile r in 16-row MFMA tiles and keep up to 4
  * of them per wave); hidden <= 8192. */
 typedef struct dsb_desc {
@@ -281,22 +281,24 @@ int dsb_op_rope_table(const int32_t* pos, int n, const float* inv_freq, int half
                       float* sin_out, void* stream);
 /* ops.py:68-73 (+ qwen3.py:96-107 when norm weights are given). */
 int dsb_op_rope(const void* qkv_pre, int64_t ldin, void* qk_out, int64_t ldout,
-                const float* cos_t, const float* sin_t, int n, int Hq, int Hkv,
+                const float* cos_t, const float* sin_t, int n, int Hq, int Hkv, int head_dim,
                 const void* q_norm, const void* k_norm, float eps, void* stream);
 /* ops.py:76-81 (+ qwen3.py:133-144), in place on g. */
 int dsb_op_rope_bwd(void* g, int64_t ldg, const void* qkv_pre, int64_t ldp, const float* cos_t,
-                    const float* sin_t, int n, int Hq, int Hkv, const void* q_norm,
+                    const float* sin_t, int n, int Hq, int Hkv, int head_dim, const void* q_norm,
                     const void* k_norm, float eps, void* stream);
-/* attention.py:20-45; o32 [n, Hq*128] fp32 and lse [Hq, n] (log2 domain) out. */
+/* attention.py:20-45; o32 [n, Hq*head_dim] fp32 and lse [Hq, n] (log2 domain)
+ * out; head_dim 128 or 64. */
 int dsb_op_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
                     int64_t ldv, void* ctx, int64_t ldc, float* o32, float* lse,
-                    const int32_t* seq_lens, int nseq, int Hq, int Hkv, void* stream);
+                    const int32_t* seq_lens, int nseq, int Hq, int Hkv, int head_dim,
+                    void* stream);
 /* attention.py:48-112 given the forward's o32/lse. */
 int dsb_op_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
                     int64_t ldv, const float* o32, const float* lse, const void* dout,
                     int64_t lddo, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
                     int64_t lddv, const int32_t* seq_lens, int nseq, int Hq, int Hkv,
-                    void* stream);
+                    int head_dim, void* stream);
 /* head.py:42-100 from the normed rows: loss, n_valid and dH [n, D] fp32
  * (grad wrt the normed rows; the final-norm backward is dsb_op_rmsnorm_bwd),
  * streaming the vocabulary in chunks of vocab_chunk columns (a multiple of

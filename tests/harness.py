@@ -25,11 +25,11 @@ LORA_KEY = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_
 
 def tiny_meta(family="llama3", L=2, D=256, Hq=2, Hkv=1, I=512, V=1000, r=8, theta=5e5,
               eps=1e-5, scaling=2.0, rope_scaling=None, lr=1e-4, s_max=512, tie=False,
-              vocab_chunk=0, gemm_tile=0):
+              vocab_chunk=0, gemm_tile=0, Hd=128):
     """Model dims + the backward meta keys the trainer reads; ``vocab_chunk``
     and ``gemm_tile`` are the libdsb tuning keys (0: defaults)."""
     m = dict(family=family, num_hidden_layers=L, hidden_size=D, num_attention_heads=Hq,
-             num_key_value_heads=Hkv, head_dim=128, intermediate_size=I, vocab_size=V,
+             num_key_value_heads=Hkv, head_dim=Hd, intermediate_size=I, vocab_size=V,
              lora_rank=r, rope_theta=theta, rms_norm_eps=eps, lora_scaling=scaling,
              rope_scaling=rope_scaling, learning_rate=lr, weight_decay=0.0, gamma=1.0,
              max_saved_finetuning_tokens=s_max, tie_word_embeddings=tie)
@@ -48,7 +48,7 @@ def config_meta(name, L=1, s_max=None):
     c = CONFIGS[name]
     lens = draw_lengths(c["nseq"], c["lo"], c["hi"], c["total"], seed=0)
     m = tiny_meta(family=c["family"], L=L, D=c["D"], Hq=c["Hq"], Hkv=c["Hkv"], I=c["I"],
-                  V=c["V"], r=c["r"], theta=c["theta"], eps=c["eps"],
+                  Hd=c.get("Hd", 128), V=c["V"], r=c["r"], theta=c["theta"], eps=c["eps"],
                   scaling=c["alpha"] / c["r"], rope_scaling=c["rope_scaling"],
                   s_max=s_max or sum(lens), tie=c["tie"])
     return m, lens
@@ -168,8 +168,9 @@ def max_rel(got, ref):
 
 
 def cosine(got, ref):
-    """Cosine similarity; -inf when either side holds a non-finite value."""
-    got, ref = got.detach().float().cpu().flatten(), ref.detach().float().cpu().flatten()
+    """Cosine similarity in float64 (fp32 sums over millions of elements drift
+    past 1); -inf when either side holds a non-finite value."""
+    got, ref = got.detach().double().cpu().flatten(), ref.detach().double().cpu().flatten()
     if not (torch.isfinite(got).all() and torch.isfinite(ref).all()):
         return float("-inf")
     return torch.nn.functional.cosine_similarity(got, ref, dim=0).item()

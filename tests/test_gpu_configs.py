@@ -70,6 +70,18 @@ def test_config_layer_and_head(name):
     assert worst["graph"]
 
 
+def test_llama32_1b_full_model():
+    """The reference's end-to-end adapter model, Llama-3.2-1B (head_dim 64,
+    32 q-heads over 8 kv heads, tied head, llama3 RoPE scaling, r = 8): all 16
+    layers at 2048 tokens in 8 sequences."""
+    meta, lens = config_meta("llama32-1b", L=16)
+    worst = cycle_parity(meta, lens, w_std=0.02, b_std=0.01, norm_jitter=0.0,
+                         ref_device="cuda")
+    _report("llama32-1b", worst)
+    assert_north_star(worst, direct_masters=False)
+    assert worst["graph"]
+
+
 def test_c4_spare_capacity_tail_split():
     """C4 widths with s_max = 9900 > n = 8192: the products' grids are sized
     for 39 row blocks, so qkv (1092 tiles) and o, gctx, gxn1, gxn2 and the

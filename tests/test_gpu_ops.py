@@ -205,20 +205,23 @@ def test_rope_table(scaling):
     assert (s.cpu() - rs).abs().max().item() < 2e-3
 
 
+@pytest.mark.parametrize("hd", [128, 64])
 @pytest.mark.parametrize("qk_norm", [False, True])
-def test_rope_fwd_bwd(qk_norm):
+def test_rope_fwd_bwd(qk_norm, hd):
+    """head_dim 64: four lanes per head, 16 heads per wave (6 heads: one
+    partly filled wave per token)."""
     from deltaserve_amd import ops
     n, Hq, Hkv = 50, 4, 2
-    q, kv = Hq * 128, Hkv * 128
+    q, kv = Hq * hd, Hkv * hd
     pre = _bf(_rnd(n, q + 2 * kv, seed=21))
     pos = torch.arange(n, dtype=torch.int32)
-    cos, sin = O.rope_cos_sin(pos, 128, 1e6)
-    qn = _bf(1 + _rnd(128, seed=22).abs() * 0.2) if qk_norm else None
-    kn = _bf(1 + _rnd(128, seed=23).abs() * 0.2) if qk_norm else None
+    cos, sin = O.rope_cos_sin(pos, hd, 1e6)
+    qn = _bf(1 + _rnd(hd, seed=22).abs() * 0.2) if qk_norm else None
+    kn = _bf(1 + _rnd(hd, seed=23).abs() * 0.2) if qk_norm else None
     out = ops.apply_rope(pre.to(DEV), Hq, Hkv, cos.to(DEV), sin.to(DEV),
                          None if qn is None else qn.to(DEV), None if kn is None else kn.to(DEV), 1e-6)
-    qp = pre.float()[:, :q].view(n, Hq, 128)
-    kp = pre.float()[:, q:q + kv].view(n, Hkv, 128)
+    qp = pre.float()[:, :q].view(n, Hq, hd)
+    kp = pre.float()[:, q:q + kv].view(n, Hkv, hd)
     if qk_norm:
         qp = O.rmsnorm(qp, qn.float(), 1e-6)
         kp = O.rmsnorm(kp, kn.float(), 1e-6)
@@ -228,11 +231,11 @@ def test_rope_fwd_bwd(qk_norm):
     gd = g.to(DEV).clone()
     ops.rope_backward_(gd, pre.to(DEV), Hq, Hkv, cos.to(DEV), sin.to(DEV),
                        None if qn is None else qn.to(DEV), None if kn is None else kn.to(DEV), 1e-6)
-    gq = O.rope_backward(g.float()[:, :q].view(n, Hq, 128), cos, sin)
-    gk = O.rope_backward(g.float()[:, q:q + kv].view(n, Hkv, 128), cos, sin)
+    gq = O.rope_backward(g.float()[:, :q].view(n, Hq, hd), cos, sin)
+    gk = O.rope_backward(g.float()[:, q:q + kv].view(n, Hkv, hd), cos, sin)
     if qk_norm:
-        gq = O.rmsnorm_backward(pre.float()[:, :q].view(n, Hq, 128), gq, qn.float(), 1e-6)
-        gk = O.rmsnorm_backward(pre.float()[:, q:q + kv].view(n, Hkv, 128), gk, kn.float(), 1e-6)
+        gq = O.rmsnorm_backward(pre.float()[:, :q].view(n, Hq, hd), gq, qn.float(), 1e-6)
+        gk = O.rmsnorm_backward(pre.float()[:, q:q + kv].view(n, Hkv, hd), gk, kn.float(), 1e-6)
     assert max_rel(gd[:, :q], gq.reshape(n, q)) < 1e-2
     assert max_rel(gd[:, q:q + kv], gk.reshape(n, kv)) < 1e-2
     assert torch.equal(gd[:, q + kv:].cpu(), g[:, q + kv:])  # v columns untouched
@@ -240,24 +243,29 @@ def test_rope_fwd_bwd(qk_norm):
 
 # group sizes Hq/Hkv 1..8: forward and dQ blocks take four (32-query subtile,
 # q-head) pairs of one kv head, so G = 3 and 5 mix subtiles within a block
-@pytest.mark.parametrize("seq_lens,Hq,Hkv", [([37, 128, 1, 200, 64], 4, 2), ([300], 8, 2),
-                                             ([5, 129, 256], 2, 1), ([1, 1, 2], 4, 4),
-                                             ([33, 95, 160, 1, 250], 10, 2), ([70, 31, 129], 6, 2),
-                                             ([200, 64], 8, 1)])
-def test_attention(seq_lens, Hq, Hkv):
+# head_dim 64 (last three cases): heads zero-padded to 128 inside the kernels
+@pytest.mark.parametrize("seq_lens,Hq,Hkv,hd", [([37, 128, 1, 200, 64], 4, 2, 128),
+                                                ([300], 8, 2, 128), ([5, 129, 256], 2, 1, 128),
+                                                ([1, 1, 2], 4, 4, 128),
+                                                ([33, 95, 160, 1, 250], 10, 2, 128),
+                                                ([70, 31, 129], 6, 2, 128), ([200, 64], 8, 1, 128),
+                                                ([37, 128, 1, 200, 64], 4, 2, 64),
+                                                ([300, 5], 8, 2, 64),
+                                                ([33, 95, 160, 1, 250], 10, 2, 64)])
+def test_attention(seq_lens, Hq, Hkv, hd):
     from deltaserve_amd import ops
     n = sum(seq_lens)
     b_start, *_ = O.pack(seq_lens)
-    qh = _bf(_rnd(n, Hq, 128, seed=31))
-    kh = _bf(_rnd(n, Hkv, 128, seed=32))
-    vh = _bf(_rnd(n, Hkv, 128, seed=33))
+    qh = _bf(_rnd(n, Hq, hd, seed=31))
+    kh = _bf(_rnd(n, Hkv, hd, seed=32))
+    vh = _bf(_rnd(n, Hkv, hd, seed=33))
     ctx, o32, lse = ops.attn_forward(qh.reshape(n, -1).to(DEV), kh.reshape(n, -1).to(DEV),
                                      vh.reshape(n, -1).to(DEV), seq_lens, Hq, Hkv)
     ref = O.attn_forward(qh.float(), kh.float(), vh.float(), seq_lens, b_start, Hq, Hkv)
     assert max_rel(o32, ref) < 1e-2
     assert cosine(o32, ref) > 0.9999
     assert max_rel(ctx, ref) < 1.5e-2
-    g = _bf(_rnd(n, Hq * 128, seed=34))
+    g = _bf(_rnd(n, Hq * hd, seed=34))
     dq, dk, dv = ops.attn_backward(qh.reshape(n, -1).to(DEV), kh.reshape(n, -1).to(DEV),
                                    vh.reshape(n, -1).to(DEV), o32, lse, g.to(DEV), seq_lens, Hq, Hkv)
     rq, rk, rv = O.attn_backward(qh.float(), kh.float(), vh.float(), g.float(), seq_lens, b_start,

@@ -34,6 +34,16 @@ def test_cycle_parity_7proj(family):
     assert_north_star(worst)
 
 
+@pytest.mark.parametrize("family", ["llama3", "qwen3"])
+def test_cycle_parity_head_dim_64(family):
+    """head_dim 64 (Llama-3.2-1B's): RoPE over 32-wide halves, the q/k norm
+    over 64 dims (Qwen3), attention on heads zero-padded to 128 with scale
+    1/8, and the qkv / o widths of 64-dim heads; GQA group of 4."""
+    meta = tiny_meta(family=family, L=2, D=512, Hq=8, Hkv=2, Hd=64, I=768)
+    worst = _run(meta, [37, 128, 1, 200, 64])
+    assert_north_star(worst)
+
+
 def test_cycle_parity_qkvo_only_llama3_rope_scaling():
     """The reference's own configuration: LoRA on q/k/v/o only, llama3 RoPE."""
     sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
