@@ -212,6 +212,10 @@ struct GraphSet {  // the cycle's graphs for one attention grid capacity
 struct dsb_handle {
   dsb_desc d{};
   int D, Hq, Hkv, hd, q, kv, W3, I, V, r, L, N, max_tiles, ntn, vchunk, nvc, ce_bn;
+  // the adapter's rank (rv) and the rank the kernels run at (r: rv rounded up
+  // to a multiple of 8; the padded rows of A and columns of B are zeros in the
+  // bf16 operands, so they add nothing, and their gradients are not stored)
+  int rv;
   int gemm_cfg = -1;  // forced dense-product tile (GEMM_*), -1 by shape
   int tile_cap = 0;   // attention grid capacity of the current cycle
   float s;
@@ -387,6 +391,7 @@ int finalize(dsb_handle* h) {
   if (!h->final_in || !h->ids || (int)h->layer_in.size() != h->L)
     return fail(h, "activations not bound");
   const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
+  const int rv = h->rv;
   const long NN = N + 1;
   CKR(dalloc(h, &h->xn1, NN * D));
   CKR(dalloc(h, &h->qkv_pre, NN * W3));
@@ -502,19 +507,19 @@ int finalize(dsb_handle* h) {
       for (int p = 0; p < 3; ++p) {
         if (!ls.has[p]) continue;
         const dsb_lora_tensors& t = ls.lora[p];
-        job(t.A, r, D, D, ls.Aqkv + (long)p * r * D, D, 0, 1.f);
-        job(t.B, outs[p], r, r, ls.B2qkv + (long)rowoff[p] * 3 * r + p * r, 3 * r, 0, s);
-        job(t.B, outs[p], r, r, bts[p], outs[p], 1, s);
+        job(t.A, rv, D, D, ls.Aqkv + (long)p * r * D, D, 0, 1.f);
+        job(t.B, outs[p], rv, rv, ls.B2qkv + (long)rowoff[p] * 3 * r + p * r, 3 * r, 0, s);
+        job(t.B, outs[p], rv, rv, bts[p], outs[p], 1, s);
       }
     }
     if (ls.has[DSB_PROJ_O]) {
-      CKR(dalloc(h, &ls.Ao, (long)r * q));
-      CKR(dalloc(h, &ls.Bo, (long)D * r));
-      CKR(dalloc(h, &ls.BTo, (long)r * D));
+      CKR(dalloc_zero(h, &ls.Ao, (long)r * q));
+      CKR(dalloc_zero(h, &ls.Bo, (long)D * r));
+      CKR(dalloc_zero(h, &ls.BTo, (long)r * D));
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_O];
-      job(t.A, r, q, q, ls.Ao, q, 0, 1.f);
-      job(t.B, D, r, r, ls.Bo, r, 0, s);
-      job(t.B, D, r, r, ls.BTo, D, 1, s);
+      job(t.A, rv, q, q, ls.Ao, q, 0, 1.f);
+      job(t.B, D, rv, rv, ls.Bo, r, 0, s);
+      job(t.B, D, rv, rv, ls.BTo, D, 1, s);
     }
     if (has_gu(ls)) {
       CKR(dalloc_zero(h, &ls.Agu, 2L * r * D));
@@ -523,25 +528,25 @@ int finalize(dsb_handle* h) {
       CKR(dalloc_zero(h, &ls.BTu, (long)r * I));
       if (ls.has[DSB_PROJ_GATE]) {
         const dsb_lora_tensors& tg = ls.lora[DSB_PROJ_GATE];
-        job(tg.A, r, D, D, ls.Agu, D, 0, 1.f);
-        job(tg.B, I, r, r, ls.B2gu, 2 * r, 0, s);
-        job(tg.B, I, r, r, ls.BTg, I, 1, s);
+        job(tg.A, rv, D, D, ls.Agu, D, 0, 1.f);
+        job(tg.B, I, rv, rv, ls.B2gu, 2 * r, 0, s);
+        job(tg.B, I, rv, rv, ls.BTg, I, 1, s);
       }
       if (ls.has[DSB_PROJ_UP]) {
         const dsb_lora_tensors& tu = ls.lora[DSB_PROJ_UP];
-        job(tu.A, r, D, D, ls.Agu + (long)r * D, D, 0, 1.f);
-        job(tu.B, I, r, r, ls.B2gu + (long)I * 2 * r + r, 2 * r, 0, s);
-        job(tu.B, I, r, r, ls.BTu, I, 1, s);
+        job(tu.A, rv, D, D, ls.Agu + (long)r * D, D, 0, 1.f);
+        job(tu.B, I, rv, rv, ls.B2gu + (long)I * 2 * r + r, 2 * r, 0, s);
+        job(tu.B, I, rv, rv, ls.BTu, I, 1, s);
       }
     }
     if (ls.has[DSB_PROJ_DOWN]) {
-      CKR(dalloc(h, &ls.Ad, (long)r * I));
-      CKR(dalloc(h, &ls.Bd, (long)D * r));
-      CKR(dalloc(h, &ls.BTd, (long)r * D));
+      CKR(dalloc_zero(h, &ls.Ad, (long)r * I));
+      CKR(dalloc_zero(h, &ls.Bd, (long)D * r));
+      CKR(dalloc_zero(h, &ls.BTd, (long)r * D));
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
-      job(t.A, r, I, I, ls.Ad, I, 0, 1.f);
-      job(t.B, D, r, r, ls.Bd, r, 0, s);
-      job(t.B, D, r, r, ls.BTd, D, 1, s);
+      job(t.A, rv, I, I, ls.Ad, I, 0, 1.f);
+      job(t.B, D, rv, rv, ls.Bd, r, 0, s);
+      job(t.B, D, rv, rv, ls.BTd, D, 1, s);
     }
     // optimizer tensors of this layer (A then B per bound projection, q..down)
     const int first_chunk = (int)opt_chunks.size();
@@ -549,7 +554,7 @@ int finalize(dsb_handle* h) {
     for (int p = 0; p < DSB_NUM_PROJ; ++p) {
       if (!ls.has[p]) continue;
       const dsb_lora_tensors& t = ls.lora[p];
-      const int na = r * ins[p], nb = outsz[p] * r;
+      const int na = rv * ins[p], nb = outsz[p] * rv;
       float *mA, *vA, *mB, *vB;
       CKR(dalloc_zero(h, &mA, na));
       CKR(dalloc_zero(h, &vA, na));
@@ -711,6 +716,7 @@ int tn(dsb_handle* h, const bf16* P, long ldp, const bf16* X, long ldx, int R, i
   a.n = h->N; a.n_dev = &h->d_hdr->n;
   a.outs[0] = o0; a.outs[1] = o1; a.outs[2] = o2;
   a.rg = rg; a.transpose_out = transpose; a.scale = scale;
+  a.rv = rg == h->r ? h->rv : 0;  // rank-structured outputs: the adapter's rows
   h->tn_pending.push_back(a);
   return 0;
 }
@@ -803,6 +809,7 @@ int dual(dsb_handle* h, const DualSpec* sp, int count, int r, hipStream_t s) {
     x.n = h->N; x.n_dev = &h->d_hdr->n; x.n_alloc = h->N; x.nsplit = ns;
     x.work = work; x.Y = sp[i].Y; x.ldy = sp[i].ldy; x.out = sp[i].out; x.scale = sp[i].scale;
     x.transpose_out = sp[i].transpose;
+    x.rv = h->rv;
     work += (long)((x.C + 511) / 512) * h->N * r + (long)ns * x.C * r;
     flops_n += 4.0 * r * x.C;
     bytes_n += 2.0 * x.C + 4.0 * r;
@@ -1246,7 +1253,7 @@ GraphSet& graph_set(dsb_handle* h) {
 // b_slot[:out, :r], both clamped to ±6.5e4 and cast to bf16, for every
 // projection with a bound served slot. Rebuilt whenever a slot is bound.
 int rebuild_publish(dsb_handle* h) {
-  const int D = h->D, q = h->q, kv = h->kv, I = h->I, r = h->r;
+  const int D = h->D, q = h->q, kv = h->kv, I = h->I, r = h->rv;
   const int ins[7] = {D, D, D, q, D, D, I}, outs[7] = {q, kv, kv, D, I, I, D};
   std::vector<CastJob> jobs;
   for (int i = 0; i < h->L; ++i)
@@ -1416,8 +1423,8 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
     return fail(nullptr, "dsb_create: head_dim must be 128 or 64");
   if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->n_heads % d->n_kv_heads)
     return fail(nullptr, "dsb_create: n_heads must be a positive multiple of n_kv_heads");
-  if (d->lora_rank <= 0 || d->lora_rank % 8 || d->lora_rank > 64)
-    return fail(nullptr, "dsb_create: lora_rank must be a multiple of 8 in [8, 64]");
+  if (d->lora_rank <= 0 || d->lora_rank > 64)
+    return fail(nullptr, "dsb_create: lora_rank must be in [1, 64]");
   if (d->hidden % 8 || d->hidden > 8192 || d->intermediate % 8 || d->vocab <= 0)
     return fail(nullptr, "dsb_create: hidden (<= 8192) and intermediate must be multiples of 8, vocab positive");
   if (d->s_max <= 0 || d->max_seqs <= 0 || d->n_layers <= 0)
@@ -1433,7 +1440,8 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
   h->D = d->hidden; h->Hq = d->n_heads; h->Hkv = d->n_kv_heads;
   h->hd = d->head_dim;
   h->q = h->Hq * h->hd; h->kv = h->Hkv * h->hd; h->W3 = h->q + 2 * h->kv;
-  h->I = d->intermediate; h->V = d->vocab; h->r = d->lora_rank; h->L = d->n_layers;
+  h->I = d->intermediate; h->V = d->vocab; h->L = d->n_layers;
+  h->rv = d->lora_rank; h->r = (d->lora_rank + 7) / 8 * 8;
   h->N = d->s_max; h->s = d->lora_scaling; h->qwen = d->family == DSB_FAMILY_QWEN3;
   h->max_tiles = max_tiles_for(d->s_max, std::min(d->max_seqs, d->s_max));
   // LM-head vocab chunk: one pause point per chunk in each pass, and the
@@ -1754,7 +1762,7 @@ int dsb_bind_served(dsb_handle* h, int layer, int proj, void* a_slot, int64_t ld
     return fail(h, "dsb_bind_served: layer/proj out of range");
   if (h->in_step) return fail(h, "dsb_bind_served: a segmented cycle is in progress");
   if (!h->layers[layer].has[proj]) return fail(h, "dsb_bind_served: projection has no LoRA bound");
-  const int D = h->D, q = h->q, r = h->r, I = h->I;
+  const int D = h->D, q = h->q, r = h->rv, I = h->I;
   const int ins[7] = {D, D, D, q, D, D, I};
   if ((a_slot == nullptr) != (b_slot == nullptr))
     return fail(h, "dsb_bind_served: bind both slots or neither");

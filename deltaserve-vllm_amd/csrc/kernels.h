@@ -116,6 +116,9 @@ struct TnArgs {
   int rg;
   int transpose_out;
   float scale;
+  // rows of each group that are stored (0: rg) and, transposed, the output
+  // row pitch: a rank padded to a multiple of 8 stores only the adapter's r
+  int rv = 0;
 };
 hipError_t lora_tn(const TnArgs& a, hipStream_t s);
 // Up to kTnBatch TN passes (each its own P, X, R, C, outputs and work region;
@@ -146,8 +149,9 @@ struct DualArgs {
   int nsplit;
   float* work;
   bf16* Y; long ldy;
-  float* out; float scale;  // out[c, j] (row pitch R1), or out[j, c] when !transpose_out
+  float* out; float scale;  // out[c, j] (row pitch rv), or out[j, c] when !transpose_out
   int transpose_out;
+  int rv = 0;               // rows j < rv are stored (0: R1)
 };
 // Up to 3 passes with the same R1, R2, n and nsplit in one launch (plus one
 // launch for all their reductions); each a[i].work is its own region.

@@ -368,11 +368,11 @@ __global__ __launch_bounds__(256) void lora_tn_reduce_kernel(TnBatch b) {
 #pragma unroll 8
   for (int sp = 0; sp < a.nsplit; ++sp) s += a.work[((long)sp * a.C + c) * a.R + j];
   s *= a.scale;
-  const int grp = j / a.rg, jj = j % a.rg;
+  const int grp = j / a.rg, jj = j % a.rg, rv = a.rv > 0 ? a.rv : a.rg;
   float* o = a.outs[grp];
-  if (o == nullptr) return;  // an untrained member of a LoRA group
+  if (o == nullptr || jj >= rv) return;  // an untrained member; a padded rank row
   if (a.transpose_out)
-    o[(long)c * a.rg + jj] = s;
+    o[(long)c * rv + jj] = s;
   else
     o[(long)jj * a.C + c] = s;
 }
@@ -666,10 +666,12 @@ __global__ __launch_bounds__(256) void lora_dual_reduce_kernel(DualBatch b) {
     for (int i = 0; i < 8; ++i)
       if (sp0 + i < a.nsplit) s += v[i];
   }
+  const int rv = a.rv > 0 ? a.rv : a.R1;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
+    if (j + e >= rv) continue;  // a padded rank row
     if (a.transpose_out)
-      a.out[(long)c * a.R1 + j + e] = s[e] * a.scale;
+      a.out[(long)c * rv + j + e] = s[e] * a.scale;
     else
       a.out[(long)(j + e) * a.C + c] = s[e] * a.scale;
   }

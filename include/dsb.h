@@ -39,9 +39,10 @@ typedef struct dsb_handle dsb_handle;
 
 /* Model and trainer constants: the backward `meta` dict of
  * deltaserve-plugin/deltaserve/ft_meta.py:131-213 plus the AdamW settings of
- * trainer.py:252-256. head_dim 128 or 64; lora_rank a multiple of 8 in
- * [8, 64] (the rank-r kernels tile r in 16-row MFMA tiles and keep up to 4
- * of them per wave); hidden <= 8192. */
+ * trainer.py:252-256. head_dim 128 or 64; lora_rank in [1, 64] (the rank-r
+ * kernels run at the rank rounded up to a multiple of 8, on zero-padded bf16
+ * copies of A and B, and store the adapter's own r rows of each gradient);
+ * hidden <= 8192. */
 typedef struct dsb_desc {
   int32_t abi_version;       /* DSB_ABI_VERSION */
   int32_t family;            /* DSB_FAMILY_* (Qwen3 adds per-head q/k RMSNorm) */

@@ -93,6 +93,21 @@ def test_cycle_parity_production_kernels(family, r):
     assert_north_star(worst)
 
 
+@pytest.mark.parametrize("family,r", [("llama3", 4), ("qwen3", 12), ("llama3", 20),
+                                      ("qwen3", 1)])
+def test_cycle_parity_rank_not_a_multiple_of_8(family, r):
+    """Ranks the reference takes that are not multiples of 8 (ops.py:115-146 is
+    rank-agnostic): the kernels run at r rounded up to 8 with zero rows in the
+    bf16 A operands and zero columns in B, so the padding adds nothing; the
+    gradients and the AdamW step cover the adapter's own r rows and columns
+    (12 runs at 16 on the fused grad_Z + grad_B passes; 20 runs at 24 and 4
+    and 1 at 8 on the separate skinny + TN kernels)."""
+    meta = tiny_meta(family=family, L=2, D=512, Hq=4, Hkv=2, I=768, V=1000, r=r,
+                     scaling=2.0, s_max=900)
+    worst = _run(meta, [37, 128, 1, 200, 64, 300])
+    assert_north_star(worst)
+
+
 @pytest.mark.parametrize("projs", [("q", "v"), ("k", "o", "up", "down"), ("gate",)])
 def test_cycle_parity_partial_lora_groups(projs):
     """Any subset of the seven projections may carry LoRA (the reference's

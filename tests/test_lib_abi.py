@@ -90,7 +90,7 @@ def test_create_rejects_bad_descriptors():
         return d
 
     h = ctypes.c_void_p()
-    for bad in (dict(abi_version=1), dict(head_dim=96), dict(head_dim=32), dict(lora_rank=12),
+    for bad in (dict(abi_version=1), dict(head_dim=96), dict(head_dim=32), dict(lora_rank=0),
                 dict(lora_rank=72),
                 dict(vocab_chunk=300), dict(vocab_chunk=-256), dict(gemm_tile=96),
                 dict(n_heads=3), dict(s_max=0)):
