@@ -66,6 +66,12 @@ DSB_DEV float block_sum(float v, float* red) {
 }
 
 DSB_DEV u32x4 ldg128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// A non-temporal 16-byte load: for data an epilogue reads once, so the
+// bursts of a whole round of tiles do not evict the operand panels the next
+// tiles read from L2 (the SwiGLU backward: 885 -> 815 µs per C3 launch).
+DSB_DEV u32x4 ldg128_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 DSB_DEV void stg128(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // σ(x) = 1/(1 + e^(−x)) with the hardware reciprocal (1 ulp) in place of an

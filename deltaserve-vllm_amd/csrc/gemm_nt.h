@@ -662,7 +662,7 @@ struct EpiBF16 {
     };
     for_each_row8_pf(
         acc, mw, nw, M, lane, wave, smem,
-        [&](int m, int n) { return whole(m, n) ? ldg128(R + (long)m * ldr + n) : u32x4{}; },
+        [&](int m, int n) { return whole(m, n) ? ldg128_nt(R + (long)m * ldr + n) : u32x4{}; },
         [&](int m, int n, float* v, const u32x4& r) {
           const int lim = N - n;
           if (lim <= 0) return;
@@ -750,7 +750,7 @@ struct EpiSwiGLUBwd {
   };
   DSB_DEV Chunk load(int m, int n) const {
     const bf16* p = GU + (long)m * ldgu + n;
-    return Chunk{ldg128(p), ldg128(p + I)};
+    return Chunk{ldg128_nt(p), ldg128_nt(p + I)};
   }
   DSB_DEV void finish(int m, int n, const float* v, const Chunk& c) const {
     float d[8], g[8], u[8], og[8], ou[8];
