@@ -255,7 +255,7 @@ struct dsb_handle {
   bf16* ores;  // bf16 rounding residual of the attention output: rowsum(dO∘O) from ctx + ores
   bf16 *normed, *dlog;
   float2* stats;
-  float *tgt_logit, *lse_h, *loss_row, *dH;
+  float *tgt_logit, *lse_h, *loss_row, *dH, *run_m, *run_l, *alpha;
   float* tn_work;
   long tn_work_elems;
   float* part = nullptr;  // split-K partials of the products with too few 256×256 tiles
@@ -428,6 +428,9 @@ int finalize(dsb_handle* h) {
   CKR(dalloc(h, &h->tgt_logit, NN));
   CKR(dalloc(h, &h->lse_h, NN));
   CKR(dalloc(h, &h->loss_row, NN));
+  CKR(dalloc(h, &h->run_m, NN));
+  CKR(dalloc(h, &h->run_l, NN));
+  CKR(dalloc(h, &h->alpha, NN));
   CKR(dalloc(h, &h->dlog, NN * h->vchunk));
   CKR(dalloc(h, &h->dH, NN * D));
   h->tn_work_elems = 32L << 20;
@@ -827,6 +830,7 @@ HeadArgs head_args(dsb_handle* h) {
   ha.n = h->N; ha.n_dev = &h->d_hdr->n; ha.D = h->D; ha.V = h->V; ha.stats = h->stats;
   ha.ntn = h->ntn; ha.ce_bn = h->ce_bn;
   ha.tgt_logit = h->tgt_logit; ha.lse = h->lse_h; ha.loss_row = h->loss_row;
+  ha.run_m = h->run_m; ha.run_l = h->run_l; ha.alpha = h->alpha;
   ha.loss_out = &h->d_hdr->loss; ha.inv_nvalid = &h->d_hdr->inv_nvalid;
   ha.dlog = h->dlog; ha.vchunk = h->vchunk; ha.dH = h->dH; ha.gemm_cfg = h->gemm_cfg;
   ha.part = h->part; ha.part_elems = h->part_elems; ha.ncu = h->ncu;
@@ -834,10 +838,11 @@ HeadArgs head_args(dsb_handle* h) {
 }
 
 // One segment of the cycle on stream st. With C vocab chunks: segments
-// 0 .. C-1 run the LM head's LSE pass one chunk each (segment 0 first builds
-// the RoPE table, the LoRA operand casts, the final norm and the labels; the
-// last reduces the statistics to the LSE and the loss); C .. 2C-1 its
-// gradient pass (the last ends with the final-norm backward); then one
+// 2c and 2c+1 run the LM head's chunk c — its logits product with the tile
+// statistics and probabilities, then the rescale to the row's running
+// softmax reference and the dH product (segment 0 first builds the RoPE
+// table, the LoRA operand casts, the final norm and the labels; segment 2C-1
+// ends with dH, the LSE and the loss and the final-norm backward); then one
 // segment per decoder layer, last layer first (forward recompute +
 // backward); the last segment runs the per-layer clip, AdamW and the publish
 // into the served LoRA slots. The cycle is the segments in order (captured
@@ -872,31 +877,24 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
         LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
       }
     }
-    const int c = seg < C ? seg : seg - C;
+    const int c = seg / 2;
     const int c0 = c * h->vchunk, Vc = std::min(h->vchunk, h->V - c0);
-    if (seg < C) {
+    if ((seg & 1) == 0) {
       {
         // 2·n·Vc·D of the head's algorithmic 4·M·D·V (the logits product)
-        KScope ks(h, st, h->ce_bn == 128 ? "gemm256x128_ce_stats" : "gemm256_ce_stats",
+        KScope ks(h, st, h->ce_bn == 128 ? "gemm256x128_ce_prob" : "gemm256_ce_prob",
                   2.0 * Vc * D, 0, 0, 2.0 * D + 8.0 * Vc / h->ce_bn, 0,
-                  2.0 * Vc * D);
-        LK(head_stats(ha, c0, st));
+                  2.0 * Vc * D + 2.0 * Vc);
+        LK(head_prob(ha, c0, st));
       }
-      if (seg == C - 1) {
-        KScope ks(h, st, "ce_reduce", 0, 0, 0, 8.0 * h->ntn + 16, 0, 0);
-        LK(head_reduce(ha, st));
+      {
+        KScope ks(h, st, "ce_rescale", 0, 0, 0, 8.0 * Vc / h->ce_bn + 4.0 * Vc + 12, 0, 0);
+        LK(head_rescale(ha, c0, st));
       }
       return 0;
     }
     {
-      // the logits of the chunk again (not algorithmic work: the price of
-      // not keeping them), with the dlogits in the epilogue
-      KScope ks(h, st, h->ce_bn == 128 ? "gemm256x128_ce_grad" : "gemm256_ce_grad",
-                2.0 * Vc * D, 0, 0, 2.0 * D + 2.0 * Vc, 0,
-                2.0 * Vc * D);
-      LK(head_chunk_grad(ha, c0, st));
-    }
-    {
+      // the other 2·n·Vc·D: dH = dH·α + P·W_chunk
       const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(N, D);
       const bool split = head_dh_split(ha, c0) > 1;
       int tail = 0;
@@ -907,6 +905,10 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       LK(head_chunk_dh(ha, c0, st));
     }
     if (c == C - 1) {
+      {
+        KScope ks(h, st, "ce_finalize", 0, 0, 0, 10.0 * D + 24, 0, 0);
+        LK(head_finalize(ha, st));
+      }
       KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 12.0 * D, 0, 2.0 * D);
       LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, h->g0, D,
                      N, nd, D, eps, st, nullptr, h->g32[0]));
@@ -2087,10 +2089,14 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   float* tl = tmp.alloc<float>(n + 1);
   float* lse = tmp.alloc<float>(n + 1);
   float* lr = tmp.alloc<float>(n + 1);
+  float* rm = tmp.alloc<float>(n + 1);
+  float* rl = tmp.alloc<float>(n + 1);
+  float* al = tmp.alloc<float>(n + 1);
   float* scal = tmp.alloc<float>(4);
   int* err = tmp.alloc<int>(1);
   bf16* dlog = tmp.alloc<bf16>((size_t)(n + 1) * vchunk);
-  if (!dpred || !labels || !stats || !tl || !lse || !lr || !scal || !err || !dlog)
+  if (!dpred || !labels || !stats || !tl || !lse || !lr || !rm || !rl || !al || !scal || !err ||
+      !dlog)
     return fail(nullptr, "dsb_op_head: hipMalloc failed");
   float hsc[4] = {nv > 0 ? 1.f / nv : 0.f, 0.f, 0.f, 0.f};
   OPCK(hipMemcpy(scal, hsc, sizeof(hsc), hipMemcpyHostToDevice));
@@ -2101,6 +2107,7 @@ int dsb_op_head(const void* normed, int64_t ldh, const void* lm_w, const int64_t
   a.normed = (const bf16*)normed; a.ldh = ldh; a.W = (const bf16*)lm_w;
   a.labels = labels; a.n = n; a.n_dev = nullptr; a.D = D; a.V = V; a.stats = stats; a.ntn = ntn;
   a.tgt_logit = tl; a.lse = lse; a.loss_row = lr; a.loss_out = scal + 1; a.inv_nvalid = scal;
+  a.run_m = rm; a.run_l = rl; a.alpha = al;
   a.dlog = dlog; a.vchunk = vchunk; a.dH = dH; a.gemm_cfg = -1;
   OPCK(head_fwd_bwd(a, s));
   OPCK(hipStreamSynchronize(s));

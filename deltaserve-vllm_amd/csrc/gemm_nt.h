@@ -791,10 +791,15 @@ struct EpiF32 {
   long ldc;
   int N;
   int accumulate;
+  // accumulate with a per-row factor on what C holds: C = C·rowscale[m] + acc
+  // (the LM head's dH across vocabulary chunks, rescaled to the row's running
+  // softmax reference); null: factor 1
+  const float* rowscale = nullptr;
   DSB_DEV void apply8(int m, int n, const float* v) const {
     const int lim = N - n;
     float* c = C + (long)m * ldc + n;
-    for (int i = 0; i < 8 && i < lim; ++i) c[i] = accumulate ? c[i] + v[i] : v[i];
+    const float sc = rowscale ? rowscale[m] : 1.f;
+    for (int i = 0; i < 8 && i < lim; ++i) c[i] = accumulate ? c[i] * sc + v[i] : v[i];
   }
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
@@ -831,11 +836,12 @@ struct EpiF32 {
           const int lim = N - n;
           if (lim <= 0) return;
           float* c = C + (long)m * ldc + n;
+          const float sc = rowscale ? rowscale[m] : 1.f;
           if (whole(m, n)) {
-            *reinterpret_cast<f32x4*>(c) = f32x4{v[0], v[1], v[2], v[3]} + x.a;
-            *reinterpret_cast<f32x4*>(c + 4) = f32x4{v[4], v[5], v[6], v[7]} + x.b;
+            *reinterpret_cast<f32x4*>(c) = f32x4{v[0], v[1], v[2], v[3]} + x.a * sc;
+            *reinterpret_cast<f32x4*>(c + 4) = f32x4{v[4], v[5], v[6], v[7]} + x.b * sc;
           } else {
-            for (int i = 0; i < 8 && i < lim; ++i) c[i] = c[i] + v[i];
+            for (int i = 0; i < 8 && i < lim; ++i) c[i] = c[i] * sc + v[i];
           }
         });
   }

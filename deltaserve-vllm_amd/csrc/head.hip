@@ -1,28 +1,30 @@
 // Final-norm output → LM head → shifted cross-entropy → dH, streaming the
 // vocabulary in chunks: no [rows, vocab] logits, probabilities or dlogits
-// ever exist in memory, only a bf16 [rows, chunk] dlogits tile per chunk.
+// ever exist in memory, only a bf16 [rows, chunk] probability tile per chunk.
 //
 // Semantics: deltaserve-plugin/deltaserve/bwd_services/common/head.py:42-100
 //   loss = sum_rows CE(logits, target) / n_valid, dlogits = (softmax - onehot)/n_valid,
 //   grad_rows = dlogits · W. Rows that predict nothing (the last token of each
 //   sequence) carry label -1 and contribute neither loss nor gradient.
 //
-// Pass 1 (LSE), one launch per vocab chunk: an MFMA GEMM logits tile whose
-//   epilogue reduces each 256-wide vocab tile to (max, sum exp) per row and
-//   picks out the target logit; nothing else is stored.
-// Reduce: combine the per-tile statistics into the row LSE and the row loss;
-//   a single-block deterministic sum gives the cycle loss.
-// Pass 2, per vocab chunk: the same GEMM recomputes the chunk's logits (bit
-//   for bit those of pass 1: same kernel, same K order) and its epilogue
-//   writes bf16 (exp(logit - lse) - onehot)/n_valid into the chunk's dlogits
-//   tile; then dH += dlogits_chunk · W_chunk with the transposed head copy
-//   (fp32 accumulate in the epilogue).
-// The recompute costs one more 2·M·D·V product than keeping the logits
-// (4.2 GB of fp32 at 8192 rows × 128256 vocab), which is what the reference
-// does (head.py:84-96); the chunk is the reference's VOCAB_CHUNK unit, so
-// the caller can pause between chunks in both passes (head.py:78-80, :92-94).
-// dlogits pass through bf16 (the MFMA operand type) where the reference keeps
-// them in fp32; the dH product accumulates in fp32.
+// Two vocabulary-wide products, with the softmax normalised online across
+// chunks as flash attention normalises across key tiles:
+//   per chunk c: logits = H·W_cᵀ (GEMM; its epilogue writes, per 256-column
+//     vocabulary tile t, the row max m_t and Σ exp(logit − m_t), the target
+//     logit where the tile holds it, and P = bf16(exp(logit − m_t)));
+//   ce_rescale: per row, the chunk max M_c = max_t m_t, the running max M and
+//     sum L updated (M' = max(M, M_c), L' = L·e^(M−M') + Σ_t s_t·e^(m_t−M')),
+//     α = e^(M−M'), and P scaled in place by e^(m_t − M') (P = exp(logit − M'));
+//   dH = dH·α + P·W_c (GEMM, fp32 accumulate with the per-row α);
+//   after the last chunk: dH = (dH/L − W[target]) / n_valid (the onehot term
+//   exactly, in fp32), LSE = M + ln L, loss_row = LSE − target logit, and a
+//   single-block deterministic sum gives the cycle loss.
+// Against the reference's 2 passes (logits for the LSE, then dlogits, both
+// chunked, head.py:78-80, :92-94) this keeps its 2·M·D·V of logits and
+// 2·M·D·V of dH and needs no third product. P passes through bf16 (the MFMA
+// operand type) where the reference keeps probabilities in fp32; dH
+// accumulates in fp32. The chunk is the reference's VOCAB_CHUNK unit; the
+// caller can pause between a chunk's two products and between chunks.
 #include "gemm_nt.h"
 #include "kernels.h"
 
@@ -31,19 +33,27 @@ namespace dsb {
 namespace {
 constexpr int CE_BN = 256;
 
-// Per 256-column vocab tile of chunk [c0, c0 + Vc): (max, sum exp) per row
-// into stats[m, c0/256 + tile] and the target logit where the tile holds it.
-struct EpiCEStats {
+// Per vocab tile (ce_bn columns) of chunk [c0, c0 + Vc): (max m_t, sum
+// exp(logit − m_t)) per row into stats[m, c0/ce_bn + tile], the target logit
+// where the tile holds it, and P[m, j] = bf16(exp(logit[m, c0 + j] − m_t)) for
+// the chunk's columns j < Vc; columns [Vc, Nc8) (Nc8 = round_up(Vc, 8)) are
+// written as zero so the dH product runs its K loop over whole 16-byte chunks.
+struct EpiCEProb {
   const int* labels;
   float2* stats;
   int ntn;
   float* tgt_logit;
-  int c0, Vc;
+  bf16* P;
+  long ldp;
+  int c0, Vc, Nc8;
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
     constexpr int TM = FM * 16, TN = FN * 16, BMl = WM * TM;
-    static_assert(WN * BMl * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2, "reduction scratch fits");
+    constexpr int PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG;
+    constexpr int STG = WM * WN * 32 * PITCH;  // for the staging rows of every wave
+    static_assert((STG + BMl + WN * BMl) * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2,
+                  "epilogue scratch fits the stages");
     const int wn = wave % WN, wm = wave / WN;
     const int n0 = nw - wn * TN;
     const int pn = c0 / (WN * TN) + n0 / (WN * TN);
@@ -51,8 +61,11 @@ struct EpiCEStats {
     // each 16-column block: a row's values of the wave tile sit in the four
     // lanes l%16 + 16q, combined with two shuffles
     const int l16 = lane & 15, lq = lane >> 4;
-    float* red = reinterpret_cast<float*>(smem);  // [WN][BMl]
-    float mx[FM];
+    float* fs = reinterpret_cast<float*>(smem);
+    float* red = fs;               // [WN][BMl] per-wave row maxima, before the staging rows
+    float* rowmax = fs + STG;      // [BMl] the tile's row maxima
+    float* rowsum = rowmax + BMl;  // [WN][BMl] per-wave row sums of exp(logit − max)
+    // 1) row maxima over the tile's live columns, and the target logit
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int m = mw + fm * 16 + l16;
@@ -68,36 +81,61 @@ struct EpiCEStats {
           if (n == t) tgt_logit[m] = x;
         }
       v = fmaxf(v, __shfl_xor(v, 16, 64));
-      mx[fm] = fmaxf(v, __shfl_xor(v, 32, 64));
+      v = fmaxf(v, __shfl_xor(v, 32, 64));
+      if (lq == 0) red[wn * BMl + wm * TM + fm * 16 + l16] = v;
     }
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-      if (lq == 0) red[wn * BMl + wm * TM + fm * 16 + l16] = mx[fm];
     __syncthreads();
-    float sm[FM];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int row = wm * TM + fm * 16 + l16;
       float b = red[row];
 #pragma unroll
       for (int j = 1; j < WN; ++j) b = fmaxf(b, red[j * BMl + row]);
-      mx[fm] = b;
-      float s = 0.f;
+      if (wn == 0 && lq == 0) rowmax[row] = b;
+    }
+    // the maxima are visible, and every wave is past its reads of `red`,
+    // before the staging rows overwrite it
+    __syncthreads();
+    // 2) P = bf16(exp(logit − max)) through the staging rows (one exp per
+    //    logit), each row's sum of the fp32 values reduced on the way: the
+    //    CG lanes of a staged row are consecutive
+    const int m0 = mw - wm * TM;
+    float* buf = fs + wave * 32 * PITCH;
+    const int rsub = lane / CG, cg = lane % CG;
+    const int n = nw + cg * 8;
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
+    for (int b = 0; b < FM / 2; ++b) {
+      if (mw + b * 32 >= M) break;  // uniform: the rest of the wave tile is past M
+      stage32<FM, FN, PITCH>(acc, b, buf, lane);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = nw + fn * 16 + 4 * lq + i;
-          if (n < Vc) s += __expf(acc[fm][fn][i] - b);
+      for (int it = 0; it < 32 / RPI; ++it) {
+        const int row = it * RPI + rsub, lrow = wm * TM + b * 32 + row, m = m0 + lrow;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
+        const float v[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+        const float bm = rowmax[lrow];
+        float e[8], part = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          e[i] = n + i < Vc ? __expf(v[i] - bm) : 0.f;
+          part += e[i];
         }
-      s += __shfl_xor(s, 16, 64);
-      sm[fm] = s + __shfl_xor(s, 32, 64);
+#pragma unroll
+        for (int o = 1; o < CG; o <<= 1) part += __shfl_xor(part, o, 64);
+        if (cg == 0) rowsum[wn * BMl + lrow] = part;
+        const int lim = Nc8 - n;
+        if (m < M && lim > 0) {
+          bf16* d = P + (long)m * ldp + n;
+          if (lim >= 8) {
+            stg128(d, pack8(e));
+          } else {
+            for (int i = 0; i < lim; ++i) d[i] = (bf16)e[i];
+          }
+        }
+      }
     }
     __syncthreads();
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-      if (lq == 0) red[wn * BMl + wm * TM + fm * 16 + l16] = sm[fm];
-    __syncthreads();
+    // 3) the tile's (max, sum) per row
     if (wn == 0 && lq == 0) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
@@ -105,74 +143,92 @@ struct EpiCEStats {
         const int m = mw + fm * 16 + l16;
         float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < WN; ++j) s += red[j * BMl + row];
-        if (m < M) stats[(long)m * ntn + pn] = make_float2(mx[fm], s);
+        for (int j = 0; j < WN; ++j) s += rowsum[j * BMl + row];
+        if (m < M) stats[(long)m * ntn + pn] = make_float2(rowmax[row], s);
       }
     }
   }
 };
 
-// dlog[m, j] = bf16((exp(logit[m, c0 + j] - lse[m]) - [c0 + j == t_m]) / n_valid)
-// for the chunk's columns j < Vc (0 for rows without a target); columns
-// [Vc, Nc8) (Nc8 = round_up(Vc, 8)) are written as zero so the dH product
-// runs its K loop over whole 16-byte chunks.
-struct EpiCEGrad {
-  const int* labels;
-  const float* lse;
-  const float* inv_nvalid;
-  bf16* D;
-  long ldd;
-  int c0, Vc, Nc8;
-  template <int FM, int FN, int WM, int WN>
-  DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
-                   void* smem) const {
-    const float sc = *inv_nvalid;
-    for_each_row8(acc, mw, nw, M, lane, wave, smem, [&](int m, int n, float* v) {
-      const int lim = Nc8 - n;
-      if (lim <= 0) return;
-      const int t = labels[m];
-      const float l = lse[m];
-      float p[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int j = n + i;
-        const float e = __expf(v[i] - l) - ((c0 + j) == t ? 1.f : 0.f);
-        p[i] = (t >= 0 && j < Vc) ? e * sc : 0.f;
-      }
-      bf16* d = D + (long)m * ldd + n;
-      if (lim >= 8) {
-        stg128(d, pack8(p));
-      } else {
-        for (int i = 0; i < lim; ++i) d[i] = (bf16)p[i];
-      }
-    });
-  }
-};
-
 }  // namespace
 
-// One wave per row: combine the per-tile (max, sumexp) pairs.
-__global__ __launch_bounds__(256) void ce_reduce_kernel(const float2* __restrict__ stats,
-                                                        int ntn, const int* __restrict__ labels,
-                                                        const float* __restrict__ tgt_logit,
-                                                        float* __restrict__ lse,
-                                                        float* __restrict__ loss_row, int n,
-                                                        const int* n_dev) {
-  int N = n;
-  if (n_dev) N = min(N, *n_dev);
+// Chunk [c0, c0 + Vc) after its logits product, one wave per live row: the
+// chunk max M_c of the tile maxima and its sum, the running max M and sum L
+// (first chunk: M = −inf, L = 0) moved to M' = max(M, M_c), α = e^(M − M')
+// for the dH accumulator, and P scaled in place by e^(m_t − M') per tile, so
+// P = bf16(exp(logit − M')). Rows without a target get P = 0.
+__global__ __launch_bounds__(256) void ce_rescale_kernel(HeadArgs a, int c0, int first) {
+  int N = a.n;
+  if (a.n_dev) N = min(N, *a.n_dev);
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
   if (m >= N) return;
-  const float2* st = stats + (long)m * ntn;
-  float mx = -INFINITY;
-  for (int j = l; j < ntn; j += 64) mx = fmaxf(mx, st[j].x);
-  mx = wave_max(mx);
-  float s = 0.f;
-  for (int j = l; j < ntn; j += 64) s += st[j].y * __expf(st[j].x - mx);
-  s = wave_sum(s);
+  const int bn = a.ce_bn, Vc = min(a.vchunk, a.V - c0), Nc8 = (Vc + 7) / 8 * 8;
+  const int nt = (Vc + bn - 1) / bn;
+  const float2* st = a.stats + (long)m * a.ntn + c0 / bn;
+  float mc = -INFINITY;
+  for (int j = l; j < nt; j += 64) mc = fmaxf(mc, st[j].x);
+  mc = wave_max(mc);
+  const float mo = first ? -INFINITY : a.run_m[m];
+  const float mn = fmaxf(mo, mc);
+  float sc = 0.f;
+  for (int j = l; j < nt; j += 64) sc += st[j].y * __expf(st[j].x - mn);
+  sc = wave_sum(sc);
   if (l == 0) {
-    const float v = mx + __logf(s);
-    lse[m] = v;
-    loss_row[m] = labels[m] >= 0 ? v - tgt_logit[m] : 0.f;
+    const float al = first ? 0.f : __expf(mo - mn);
+    a.run_m[m] = mn;
+    a.run_l[m] = (first ? 0.f : a.run_l[m] * al) + sc;
+    a.alpha[m] = al;
+  }
+  bf16* pr = a.dlog + (long)m * a.vchunk;
+  const bool live = a.labels[m] >= 0;
+#pragma unroll 4
+  for (int k = l; k < Nc8 / 8; k += 64) {
+    u32x4* q = reinterpret_cast<u32x4*>(pr + 8 * k);
+    if (!live) {
+      *q = u32x4{0u, 0u, 0u, 0u};
+      continue;
+    }
+    const float f = __expf(st[(8 * k) / bn].x - mn);
+    float v[8];
+    unpack8(*q, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] *= f;
+    *q = pack8(v);
+  }
+}
+
+// After the last chunk, one wave per live row: LSE = M + ln L, loss_row =
+// LSE − target logit, dH = (dH/L − W[target]) / n_valid; rows without a target
+// get dH = 0 and no loss.
+__global__ __launch_bounds__(256) void ce_finalize_kernel(HeadArgs a) {
+  int N = a.n;
+  if (a.n_dev) N = min(N, *a.n_dev);
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (m >= N) return;
+  const int t = a.labels[m];
+  float* dr = a.dH + (long)m * a.D;
+  if (t < 0) {
+    for (int k = l; k < a.D / 4; k += 64)
+      reinterpret_cast<f32x4*>(dr)[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (l == 0) a.loss_row[m] = 0.f;
+    return;
+  }
+  const float L = a.run_l[m], lse = a.run_m[m] + __logf(L);
+  if (l == 0) {
+    a.lse[m] = lse;
+    a.loss_row[m] = lse - a.tgt_logit[m];
+  }
+  const float inv = 1.f / L, sc = *a.inv_nvalid;
+  const bf16* w = a.W + (long)t * a.D;
+  for (int k = l; k < a.D / 8; k += 64) {
+    float wf[8];
+    unpack8(ldg128(w + 8 * k), wf);
+    f32x4* d = reinterpret_cast<f32x4*>(dr + 8 * k);
+    const f32x4 x0 = d[0], x1 = d[1];
+    d[0] = f32x4{(x0[0] * inv - wf[0]) * sc, (x0[1] * inv - wf[1]) * sc,
+                 (x0[2] * inv - wf[2]) * sc, (x0[3] * inv - wf[3]) * sc};
+    d[1] = f32x4{(x1[0] * inv - wf[4]) * sc, (x1[1] * inv - wf[5]) * sc,
+                 (x1[2] * inv - wf[6]) * sc, (x1[3] * inv - wf[7]) * sc};
   }
 }
 
@@ -198,31 +254,29 @@ static GemmProblem chunk_logits_problem(const HeadArgs& a, int c0) {
                      a.n, Vc, a.D, 0, a.n_dev};
 }
 
-hipError_t head_stats(const HeadArgs& a, int c0, hipStream_t s) {
+hipError_t head_prob(const HeadArgs& a, int c0, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  const int Vc = min(a.vchunk, a.V - c0);
-  EpiCEStats epi{a.labels, a.stats, a.ntn, a.tgt_logit, c0, Vc};
+  const int Vc = min(a.vchunk, a.V - c0), Nc8 = (Vc + 7) / 8 * 8;
+  EpiCEProb epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.dlog, (long)a.vchunk, c0, Vc, Nc8};
   if (a.ce_bn == 128) return launch_gemm_cfg<256, 128, 2, 2>(chunk_logits_problem(a, c0), epi, s);
   return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
 
-hipError_t head_reduce(const HeadArgs& a, hipStream_t s) {
+hipError_t head_rescale(const HeadArgs& a, int c0, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(ce_reduce_kernel, dim3((a.n + 3) / 4), dim3(256), 0, s, a.stats, a.ntn,
-                     a.labels, a.tgt_logit, a.lse, a.loss_row, a.n, a.n_dev);
+  hipLaunchKernelGGL(ce_rescale_kernel, dim3((a.n + 3) / 4), dim3(256), 0, s, a, c0,
+                     c0 == 0 ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t head_finalize(const HeadArgs& a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ce_finalize_kernel, dim3((a.n + 3) / 4), dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(ce_loss_kernel, dim3(1), dim3(1024), 0, s, a.loss_row, a.n, a.n_dev,
                      a.inv_nvalid, a.loss_out);
   return hipGetLastError();
-}
-
-hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s) {
-  if (a.n <= 0) return hipSuccess;
-  const int Vc = min(a.vchunk, a.V - c0), Nc8 = (Vc + 7) / 8 * 8;
-  EpiCEGrad epi{a.labels, a.lse, a.inv_nvalid, a.dlog, (long)a.vchunk, c0, Vc, Nc8};
-  if (a.ce_bn == 128) return launch_gemm_cfg<256, 128, 2, 2>(chunk_logits_problem(a, c0), epi, s);
-  return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
 
 int head_dh_split(const HeadArgs& a, int c0) {
@@ -242,13 +296,13 @@ int head_dh_tail(const HeadArgs& a, int c0, int* tail) {
 
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
   const int Nc8 = (min(a.vchunk, a.V - c0) + 7) / 8 * 8;
-  // dH += dlogits[:, chunk] · W[chunk, :]: the head read in place as the
+  // dH = dH·α + P[:, chunk] · W[chunk, :]: the head read in place as the
   // [K, N] operand, rows past the vocabulary loading as zeros
   GemmProblem q{a.dlog, (long)a.vchunk, a.W + (long)c0 * a.D, (long)a.D, nullptr, 0, nullptr, 0,
                 a.n, a.D, Nc8, 0, a.n_dev};
   q.b_kn = 1;
   q.kb_rows = min(a.vchunk, a.V - c0);
-  EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0};
+  EpiF32 ef{a.dH, (long)a.D, a.D, c0 > 0 ? 1 : 0, a.alpha};
   const int ks = head_dh_split(a, c0);
   if (ks > 1) {
     q.part = a.part;
@@ -263,14 +317,12 @@ hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s) {
 hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s) {
   hipError_t e;
   if (a.n <= 0) return hipSuccess;
-  for (int c0 = 0; c0 < a.V; c0 += a.vchunk)
-    if ((e = head_stats(a, c0, s)) != hipSuccess) return e;
-  if ((e = head_reduce(a, s)) != hipSuccess) return e;
   for (int c0 = 0; c0 < a.V; c0 += a.vchunk) {
-    if ((e = head_chunk_grad(a, c0, s)) != hipSuccess) return e;
+    if ((e = head_prob(a, c0, s)) != hipSuccess) return e;
+    if ((e = head_rescale(a, c0, s)) != hipSuccess) return e;
     if ((e = head_chunk_dh(a, c0, s)) != hipSuccess) return e;
   }
-  return hipSuccess;
+  return head_finalize(a, s);
 }
 
 }  // namespace dsb

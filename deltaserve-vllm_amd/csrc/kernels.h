@@ -165,29 +165,34 @@ struct HeadArgs {
   const int* labels;              // [n] target id or -1
   int n; const int* n_dev;
   int D, V;
-  float2* stats;                  // [n_cap, ntn]
+  float2* stats;                  // [n_cap, ntn] per vocab tile (max, sum exp)
   int ntn;                        // ceil(V / ce_bn)
   int ce_bn = 256;                // vocab tile width of the CE passes (256 or 128)
   float* tgt_logit;               // [n_cap]
-  float* lse;                     // [n_cap]
+  float* lse;                     // [n_cap] row LSE (natural log), after the last chunk
+  float* run_m;                   // [n_cap] running row max across chunks
+  float* run_l;                   // [n_cap] running Σ exp(logit − run_m)
+  float* alpha;                   // [n_cap] the dH accumulator's factor for the chunk
   float* loss_row;                // [n_cap]
   float* loss_out;                // scalar: sum(loss_row)/n_valid
   const float* inv_nvalid;        // device scalar 1/n_valid (0 when none)
-  bf16* dlog; int vchunk;         // [n_cap, vchunk] bf16 dlogits of one vocab chunk;
-                                  // vchunk a multiple of 256
+  bf16* dlog; int vchunk;         // [n_cap, vchunk] bf16 probabilities of one vocab
+                                  // chunk; vchunk a multiple of 256
   float* dH;                      // [n, D] fp32
   int gemm_cfg;                   // tile of the dH product (-1: by shape)
   float* part = nullptr;          // split-K partials for the dH product (null: no split)
   long part_elems = 0;
   int ncu = 0;                    // compute units (tail split of the dH product; 0: none)
 };
-// Chunk c0 (a multiple of vchunk) of pass 1 / pass 2; head_reduce between the passes.
+// Chunk c0 (a multiple of vchunk): head_prob (logits, tile statistics and
+// probabilities), head_rescale (online-softmax reference), head_chunk_dh
+// (dH·α + P·W); head_finalize after the last chunk (dH, LSE, loss).
 int head_num_chunks(const HeadArgs& a);
 hipError_t head_fwd_bwd(const HeadArgs& a, hipStream_t s);
-hipError_t head_stats(const HeadArgs& a, int c0, hipStream_t s);
-hipError_t head_reduce(const HeadArgs& a, hipStream_t s);
-hipError_t head_chunk_grad(const HeadArgs& a, int c0, hipStream_t s);
+hipError_t head_prob(const HeadArgs& a, int c0, hipStream_t s);
+hipError_t head_rescale(const HeadArgs& a, int c0, hipStream_t s);
 hipError_t head_chunk_dh(const HeadArgs& a, int c0, hipStream_t s);
+hipError_t head_finalize(const HeadArgs& a, hipStream_t s);
 // K splits head_chunk_dh uses for chunk c0 (1: none), over the whole product
 // or (head_dh_tail) over the tiles of its partly filled last round
 int head_dh_split(const HeadArgs& a, int c0);
