@@ -388,6 +388,13 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   load_row_frags(a.q, a.ldq, st + qpos, h * hd, qok, lh, hd, qf);
   load_row_frags(a.dout, a.lddo, st + qpos, h * hd, qok, lh, hd, df_);
   const float lse2 = qok ? a.lse[(long)h * a.ld_stat + st + qpos] : 0.f;
+  // the first K/V tile is requested before the dsum prologue waits on its own
+  // loads, so the two latencies overlap
+  const FragOffs fo(lane);
+  const SeqTiles tk(a.k, a.ldk, st, L, w, lane, hd), tv(a.v, a.ldv, st, L, w, lane, hd);
+  const unsigned lds0 = lds_addr(smem);
+  tk.load(0, kvh * hd, lds0, w);
+  tv.load(0, kvh * hd, lds0 + TILE * 2, w);
   // dsum = rowsum(dO∘O) of the wave's rows: the lane's 64 dims of dO (df_)
   // against the same dims of O (ctx + its rounding residual, or the fp32 copy,
   // when the forward wrote one, else the bf16 ctx), the two halves of a row
@@ -434,11 +441,6 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   const float sl2 = a.scale * kLog2e;
   const int nt = qb.nt;
 
-  const FragOffs fo(lane);
-  const SeqTiles tk(a.k, a.ldk, st, L, w, lane, hd), tv(a.v, a.ldv, st, L, w, lane, hd);
-  const unsigned lds0 = lds_addr(smem);
-  tk.load(0, kvh * hd, lds0, w);
-  tv.load(0, kvh * hd, lds0 + TILE * 2, w);
   // The wave computes the tiles with a key at or before its last query
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
