@@ -52,7 +52,7 @@ struct EpiCEProb {
     constexpr int TM = FM * 16, TN = FN * 16, BMl = WM * TM;
     constexpr int PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG;
     constexpr int STG = WM * WN * 32 * PITCH;  // for the staging rows of every wave
-    static_assert((STG + BMl + WN * BMl) * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2,
+    static_assert((STG + 2 * BMl + WN * BMl) * 4 <= 2 * (WM * TM + WN * TN) * 64 * 2,
                   "epilogue scratch fits the stages");
     const int wn = wave % WN, wm = wave / WN;
     const int n0 = nw - wn * TN;
@@ -65,33 +65,44 @@ struct EpiCEProb {
     float* red = fs;               // [WN][BMl] per-wave row maxima, before the staging rows
     float* rowmax = fs + STG;      // [BMl] the tile's row maxima
     float* rowsum = rowmax + BMl;  // [WN][BMl] per-wave row sums of exp(logit − max)
-    // 1) row maxima over the tile's live columns, and the target logit
+    int* tcol = reinterpret_cast<int*>(rowsum + WN * BMl);  // [BMl] target column in the chunk, or -1
+    // 1) row maxima over the tile's live columns (every column of the wave
+    //    tile is live except in the chunk's last tile: one wave-uniform test)
+    const bool whole = nw + TN <= Vc;
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      const int m = mw + fm * 16 + l16;
-      const int t = (m < M) ? labels[m] - c0 : -1;
       float v = -INFINITY;
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int n = nw + fn * 16 + 4 * lq + i;
           const float x = acc[fm][fn][i];
-          if (n < Vc) v = fmaxf(v, x);
-          if (n == t) tgt_logit[m] = x;
+          v = (whole || nw + fn * 16 + 4 * lq + i < Vc) ? fmaxf(v, x) : v;
         }
       v = fmaxf(v, __shfl_xor(v, 16, 64));
       v = fmaxf(v, __shfl_xor(v, 32, 64));
       if (lq == 0) red[wn * BMl + wm * TM + fm * 16 + l16] = v;
     }
+    // The accumulators' copies read above die here: the empty asm claims to
+    // rewrite each one in its AGPRs, so phase 2 reads them from there again
+    // instead of the compiler keeping VGPR copies across the barriers.
+    auto& accw = const_cast<f32x4 (&)[FM][FN]>(acc);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) asm volatile("" : "+a"(accw[fm][fn]));
     __syncthreads();
+    if (wn == 0 && lq == 0) {
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const int row = wm * TM + fm * 16 + l16;
-      float b = red[row];
+      for (int fm = 0; fm < FM; ++fm) {
+        const int row = wm * TM + fm * 16 + l16, m = mw + fm * 16 + l16;
+        float b = red[row];
 #pragma unroll
-      for (int j = 1; j < WN; ++j) b = fmaxf(b, red[j * BMl + row]);
-      if (wn == 0 && lq == 0) rowmax[row] = b;
+        for (int j = 1; j < WN; ++j) b = fmaxf(b, red[j * BMl + row]);
+        rowmax[row] = b;
+        const int t = m < M ? labels[m] - c0 : -1;
+        tcol[row] = t >= 0 && t < Vc ? t : -1;
+      }
     }
     // the maxima are visible, and every wave is past its reads of `red`,
     // before the staging rows overwrite it
@@ -114,10 +125,18 @@ struct EpiCEProb {
         const f32x4 y = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
         const float v[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
         const float bm = rowmax[lrow];
+        // the target logit, where the row's target column is one of these 8
+        const int tj = tcol[lrow] - n;
+        if (m < M && (unsigned)tj < 8u) {
+          float x = v[0];
+#pragma unroll
+          for (int i = 1; i < 8; ++i) x = tj == i ? v[i] : x;
+          tgt_logit[m] = x;
+        }
         float e[8], part = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          e[i] = n + i < Vc ? __expf(v[i] - bm) : 0.f;
+          e[i] = (whole || n + i < Vc) ? __expf(v[i] - bm) : 0.f;
           part += e[i];
         }
 #pragma unroll
