@@ -1,11 +1,11 @@
 // Packed varlen causal GQA attention on gfx950 MFMA, head_dim 128 or 64:
 // forward recompute (ctx, optional fp32 ctx copy, row log-sum-exp) and the
-// FA2-style backward split into a dQ pass (forward and dQ blocks: 4 waves of
-// 32 queries sharing one kv head, see q_block), which also forms
-// dsum = rowsum(dO∘O) for its rows, and a dK/dV pass that runs after it (one
-// block per 128 keys of one kv head, summing its q-head group in registers, no
-// atomics). Softmax statistics, P and dS stay fp32 in registers; P and dS are
-// rounded to bf16 only as MFMA operands.
+// FA2-style backward: a dsum = rowsum(dO∘O) pass, then two passes that do
+// not depend on each other (the cycle runs them concurrently): dQ (forward
+// and dQ blocks: 4 waves of 32 queries sharing one kv head, see q_block) and
+// dK/dV (one block per 128 keys of one kv head, summing its q-head group in
+// registers, no atomics). Softmax statistics, P and dS stay fp32 in
+// registers; P and dS are rounded to bf16 only as MFMA operands.
 //
 // head_dim 64 runs the head_dim-128 kernels on heads zero-padded to 128 inside
 // the loads (dims past a.hd load as zeros, so they add nothing to Q·Kᵀ, dO·Vᵀ
@@ -370,6 +370,63 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- dsum
+// dsum[h, row] = rowsum(dO∘O) over head h's dims, for every live row and
+// q-head: O is ctx + its rounding residual (or the fp32 copy when the forward
+// wrote one, else the bf16 ctx). A thread takes 8 dims of two rows (its six
+// 16-byte loads issued before any use); the hd/8 threads of a (row, head) are
+// consecutive lanes and reduce by shuffles. The dQ and dK/dV passes read it,
+// so they do not depend on each other.
+constexpr int kDsumRows = 2;
+__global__ __launch_bounds__(256) void attn_dsum_kernel(AttnArgs a) {
+  const int n = a.n_dev ? min(a.n, *a.n_dev) : a.n;
+  const int per_row = a.Hq * a.hd / 8, gw = a.hd / 8;
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  const long m0 = g / per_row * kDsumRows;
+  // a (row, head) group's lanes share m0, so groups leave whole
+  if (m0 >= n) return;
+  const int d0 = (int)(g % per_row) * 8;
+  float acc[kDsumRows];
+  if (a.o32) {
+#pragma unroll
+    for (int i = 0; i < kDsumRows; ++i) {
+      const long m = min(m0 + i, (long)n - 1);
+      float dv[8];
+      unpack8(ldg128(a.dout + m * a.lddo + d0), dv);
+      const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.o32 + m * a.ldo32 + d0);
+      const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.o32 + m * a.ldo32 + d0 + 4);
+      acc[i] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i] += dv[e] * o0[e] + dv[4 + e] * o1[e];
+    }
+  } else {
+    u32x4 xd[kDsumRows], xc[kDsumRows], xr[kDsumRows];
+#pragma unroll
+    for (int i = 0; i < kDsumRows; ++i) {
+      const long m = min(m0 + i, (long)n - 1);  // a last odd row repeats, unstored
+      xd[i] = ldg128(a.dout + m * a.lddo + d0);
+      xc[i] = ldg128(a.ctx + m * a.ldc + d0);
+      xr[i] = a.ores ? ldg128(a.ores + m * a.ldc + d0) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < kDsumRows; ++i) {
+      float dv[8], ov[8], rv[8];
+      unpack8(xd[i], dv);
+      unpack8(xc[i], ov);
+      unpack8(xr[i], rv);
+      acc[i] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[i] += dv[e] * (ov[e] + rv[e]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kDsumRows; ++i) {
+    float v = acc[i];
+    for (int o = 1; o < gw; o <<= 1) v += __shfl_xor(v, o, 64);
+    if (d0 % a.hd == 0 && m0 + i < n) a.dsum[(long)(d0 / a.hd) * a.ld_stat + m0 + i] = v;
+  }
+}
+
 // ---------------------------------------------------------------- dQ
 // Block: 4 waves × 32 queries (q_block layout) of one kv head's q-heads;
 // streams the kv head's K/V tiles. dQ = scale · dS·K.
@@ -388,50 +445,12 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   load_row_frags(a.q, a.ldq, st + qpos, h * hd, qok, lh, hd, qf);
   load_row_frags(a.dout, a.lddo, st + qpos, h * hd, qok, lh, hd, df_);
   const float lse2 = qok ? a.lse[(long)h * a.ld_stat + st + qpos] : 0.f;
-  // the first K/V tile is requested before the dsum prologue waits on its own
-  // loads, so the two latencies overlap
+  const float dsum = qok ? a.dsum[(long)h * a.ld_stat + st + qpos] : 0.f;
   const FragOffs fo(lane);
   const SeqTiles tk(a.k, a.ldk, st, L, w, lane, hd), tv(a.v, a.ldv, st, L, w, lane, hd);
   const unsigned lds0 = lds_addr(smem);
   tk.load(0, kvh * hd, lds0, w);
   tv.load(0, kvh * hd, lds0 + TILE * 2, w);
-  // dsum = rowsum(dO∘O) of the wave's rows: the lane's 64 dims of dO (df_)
-  // against the same dims of O (ctx + its rounding residual, or the fp32 copy,
-  // when the forward wrote one, else the bf16 ctx), the two halves of a row
-  // joined across lanes l and l^32; the dK/dV pass that runs next reads it
-  // from a.dsum.
-  float dsum = 0.f;
-  {
-    const long orow = (long)(st + (qok ? qpos : 0));
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      if (kk * 16 >= hd) break;
-      const int d0 = h * hd + kk * 16 + lh * 8;
-      float ov[8];
-      if (a.ores) {
-        float rv[8];
-        unpack8(ldg128(a.ctx + orow * a.ldc + d0), ov);
-        unpack8(ldg128(a.ores + orow * a.ldc + d0), rv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ov[e] += rv[e];
-      } else if (a.o32) {
-        const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.o32 + orow * a.ldo32 + d0);
-        const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.o32 + orow * a.ldo32 + d0 + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ov[e] = o0[e];
-          ov[4 + e] = o1[e];
-        }
-      } else {
-        unpack8(ldg128(a.ctx + orow * a.ldc + d0), ov);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dsum += (float)df_[kk][e] * ov[e];
-    }
-    dsum += __shfl_xor(dsum, 32, 64);
-    if (!qok) dsum = 0.f;
-    if (qok && lh == 0) a.dsum[(long)h * a.ld_stat + st + qpos] = dsum;
-  }
 
   f32x16 dq[4];
 #pragma unroll
@@ -582,12 +601,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     to.load(q0, hq * hd, d + TILE * 2, w);
   };
   if (nit > 0) {
+    // the first pair's tiles are requested before the wait on its lse/dsum
+    // rows, so the K/V rows, those rows and the tiles arrive in one latency
     load_ld(0);
+    stage(0, 0);
     if (tid < TR) {
       sLD[0][0][tid] = nl;
       sLD[0][1][tid] = nd;
     }
-    stage(0, 0);
   }
   for (int it = 0; it < nit; ++it) {
     const int sidx = it & 1;
@@ -848,9 +869,18 @@ hipError_t attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// dQ first: it computes dsum, which the dK/dV pass reads.
+hipError_t attn_dsum(const AttnArgs& a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  const long threads = (long)(a.n + kDsumRows - 1) / kDsumRows * (a.Hq * a.hd / 8);
+  hipLaunchKernelGGL(attn_dsum_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                     a);
+  return hipGetLastError();
+}
+
+// dsum first (both passes read it); the dQ and dK/dV passes are independent.
 hipError_t attn_bwd(const AttnArgs& a, hipStream_t s) {
   hipError_t e;
+  if ((e = attn_dsum(a, s)) != hipSuccess) return e;
   if ((e = attn_bwd_dq(a, s)) != hipSuccess) return e;
   return attn_bwd_dkdv(a, s);
 }

@@ -222,6 +222,10 @@ struct dsb_handle {
   bool qwen = false;
   hipStream_t hs = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr, ev_t0 = nullptr, ev_t1 = nullptr;
+  // second stream (default priority) for the attention backward's dK/dV pass,
+  // forked from and joined back into the cycle's stream by these events
+  hipStream_t hs2 = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   std::vector<LayerState> layers;
   const bf16* lm_w = nullptr;
   const bf16* norm_w = nullptr;
@@ -1138,13 +1142,33 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       if (dual_o) CKR(tn(h, h->Zo_b, r, h->grm, D, r, D, t.gB, nullptr, nullptr, r, 1, h->s, st));
     }
     {
-      // dQ first: it also forms dsum = rowsum(dO∘O) (reads ctx and its residual)
-      KScope ks(h, st, "attn_dq", 0, au, 0, arow + 2.0 * q + 2.0 * q + 4.0 * q + 4.0 * Hq, 0, 0);
-      LK(attn_bwd_dq(at, st));
+      // dsum = rowsum(dO∘O) (reads dO, ctx and its residual) for both passes
+      KScope ks(h, st, "attn_dsum", 0, 0, 0, 6.0 * q + 4.0 * Hq, 0, 0);
+      LK(attn_dsum(at, st));
     }
     {
-      KScope ks(h, st, "attn_dkdv", 0, 4.0 * au, 0, arow + 2.0 * q + 4.0 * kv, 0, 0);
-      LK(attn_bwd_dkdv(at, st));
+      // The dQ and dK/dV passes share only inputs: dK/dV runs on the second
+      // stream, concurrently with dQ, so each pass's blocks fill the CUs the
+      // other leaves idle (short sequences leave both latency-bound). Under
+      // per-kernel timing they run in order, each timed alone.
+      const bool fork = !h->ktiming;
+      hipStream_t sk = fork ? h->hs2 : st;
+      if (fork) {
+        CK(hipEventRecord(h->ev_fork, st));
+        CK(hipStreamWaitEvent(h->hs2, h->ev_fork, 0));
+      }
+      {
+        KScope ks(h, sk, "attn_dkdv", 0, 4.0 * au, 0, arow + 2.0 * q + 4.0 * kv, 0, 0);
+        LK(attn_bwd_dkdv(at, sk));
+      }
+      {
+        KScope ks(h, st, "attn_dq", 0, au, 0, arow + 2.0 * q + 2.0 * q + 8.0 * Hq, 0, 0);
+        LK(attn_bwd_dq(at, st));
+      }
+      if (fork) {
+        CK(hipEventRecord(h->ev_join, h->hs2));
+        CK(hipStreamWaitEvent(st, h->ev_join, 0));
+      }
     }
     {
       KScope ks(h, st, "rope_bwd", 0, 0, 0, 4.0 * (q + kv) + 512.0, 0, 0);
@@ -1462,6 +1486,9 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
   h->layers.resize(h->L);
   h->ktiming = (d->flags & DSB_FLAG_KTIMING) != 0;
   hipError_t e = hipStreamCreateWithFlags(&h->hs, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&h->hs2, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_fork, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_in, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_out, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreate(&h->ev_t0);
@@ -1478,6 +1505,7 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
 void dsb_destroy(dsb_handle* h) {
   if (!h) return;
   if (h->hs) (void)hipStreamSynchronize(h->hs);
+  if (h->hs2) (void)hipStreamSynchronize(h->hs2);
   drop_graphs(h);
   for (hipEvent_t e : h->ring) (void)hipEventDestroy(e);
   if (h->d_pub_jobs) (void)hipFree(h->d_pub_jobs);
@@ -1492,6 +1520,9 @@ void dsb_destroy(dsb_handle* h) {
   if (h->ev_out) (void)hipEventDestroy(h->ev_out);
   if (h->ev_t0) (void)hipEventDestroy(h->ev_t0);
   if (h->ev_t1) (void)hipEventDestroy(h->ev_t1);
+  if (h->ev_fork) (void)hipEventDestroy(h->ev_fork);
+  if (h->ev_join) (void)hipEventDestroy(h->ev_join);
+  if (h->hs2) (void)hipStreamDestroy(h->hs2);
   if (h->hs) (void)hipStreamDestroy(h->hs);
   delete h;
 }

@@ -47,7 +47,7 @@ struct AttnArgs {
                              // ctx (ld = ldc); dsum then takes O = ctx + ores.
                              // With neither copy dsum takes O from the bf16 ctx.
   float* lse;                // [Hq, ld_stat] log2-domain row log-sum-exp
-  float* dsum;               // [Hq, ld_stat] rowsum(dO ∘ O), written by the dQ pass
+  float* dsum;               // [Hq, ld_stat] rowsum(dO ∘ O), written by attn_dsum
   long ld_stat;
   const bf16* dout; long lddo;  // bwd in: grad of ctx
   bf16* dq; long lddq;       // bwd out
@@ -68,7 +68,9 @@ struct AttnArgs {
   long kv_part_elems = 0;
 };
 hipError_t attn_fwd(const AttnArgs& a, hipStream_t s);
-hipError_t attn_bwd(const AttnArgs& a, hipStream_t s);
+hipError_t attn_bwd(const AttnArgs& a, hipStream_t s);  // attn_dsum, dQ, dK/dV in order
+// dsum for every live row and q-head; the dQ and dK/dV passes read it
+hipError_t attn_dsum(const AttnArgs& a, hipStream_t s);
 hipError_t attn_bwd_dkdv(const AttnArgs& a, hipStream_t s);
 // q-head slices the dK/dV pass splits into (1: none) when kv_part_elems
 // holds the partials; attn_bwd_dkdv takes the split when kv_part is set
