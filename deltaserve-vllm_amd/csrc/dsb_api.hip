@@ -1061,9 +1061,29 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
       EpiSwiGLUBwd e{gu, ldgu, h->Ggu, 2L * I, I};
       CKR(gemm(h, "dswiglu", p, e, st, 8.0, 0.0));
     }
+    // gate, up and down adapters all present and the three passes (each over
+    // I columns) fit one fused launch: one launch and one reduction for all
+    // three instead of three of each (C3: 84 column blocks × 3 token splits)
+    bool mlp3 = false;
+    if (hd && hdual && ls.has[DSB_PROJ_GATE] && ls.has[DSB_PROJ_UP]) {
+      const int C3c[3] = {I, I, I};
+      mlp3 = dual_splits(h, C3c, 3, r) > 0;
+    }
+    if (mlp3) {
+      const DualSpec d[3] = {
+          {h->hb, I, I, h->gZd_b, r, ls.Ad, h->Zd_b, r, ls.lora[DSB_PROJ_DOWN].gA, 1.f, 0},
+          {h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, h->gZgu_b, 2L * r,
+           grad_b(h, ls, DSB_PROJ_GATE), h->s, 1},
+          {h->Ggu + I, 2L * I, I, h->Zgu_b + r, 2L * r, ls.BTu, h->gZgu_b + r, 2L * r,
+           grad_b(h, ls, DSB_PROJ_UP), h->s, 1}};
+      const int rc = dual(h, d, 3, r, st);
+      if (rc != 0) return -1;
+    }
     if (hd) {
       const dsb_lora_tensors& t = ls.lora[DSB_PROJ_DOWN];
-      if (hdual) {
+      if (mlp3) {
+        // Z_d and grad_A_d came from the three-pass launch above
+      } else if (hdual) {
         // Z_d = bf16(h·A_dᵀ) and grad_A_d = grad_Z_dᵀ·h [r, I] in one pass over h
         const DualSpec d{h->hb, I, I, h->gZd_b, r, ls.Ad, h->Zd_b, r, t.gA, 1.f, 0};
         const int rc = dual(h, &d, 1, r, st);
@@ -1075,7 +1095,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     }
     // 1: the member's grad_Z / grad_B still need the separate kernels
     int rest_g = 0, rest_u = 0;
-    if (hg) {
+    if (hg && !mlp3) {
       const bool tg = ls.has[DSB_PROJ_GATE], tu = ls.has[DSB_PROJ_UP];
       const DualSpec d[2] = {
           {h->Ggu, 2L * I, I, h->Zgu_b, 2L * r, ls.BTg, h->gZgu_b, 2L * r,
