@@ -10,11 +10,14 @@
 // Two vocabulary-wide products, with the softmax normalised online across
 // chunks as flash attention normalises across key tiles:
 //   per chunk c: logits = H·W_cᵀ (GEMM; its epilogue writes, per 256-column
-//     vocabulary tile t, the row max m_t and Σ exp(logit − m_t), the target
+//     vocabulary tile t, the reference m_t = max(the tile's row max, the
+//     running max M of the earlier chunks) and Σ exp(logit − m_t), the target
 //     logit where the tile holds it, and P = bf16(exp(logit − m_t)));
 //   ce_rescale: per row, the chunk max M_c = max_t m_t, the running max M and
 //     sum L updated (M' = max(M, M_c), L' = L·e^(M−M') + Σ_t s_t·e^(m_t−M')),
-//     α = e^(M−M'), and P scaled in place by e^(m_t − M') (P = exp(logit − M'));
+//     α = e^(M−M'), and P scaled in place by e^(m_t − M') (P = exp(logit − M'))
+//     on the rows where some m_t differs from M' (every row of the first
+//     chunk; later, only the rows whose maximum lies in the chunk);
 //   dH = dH·α + P·W_c (GEMM, fp32 accumulate with the per-row α);
 //   after the last chunk: dH = (dH/L − W[target]) / n_valid (the onehot term
 //   exactly, in fp32), LSE = M + ln L, loss_row = LSE − target logit, and a
@@ -33,8 +36,10 @@ namespace dsb {
 namespace {
 constexpr int CE_BN = 256;
 
-// Per vocab tile (ce_bn columns) of chunk [c0, c0 + Vc): (max m_t, sum
-// exp(logit − m_t)) per row into stats[m, c0/ce_bn + tile], the target logit
+// Per vocab tile (ce_bn columns) of chunk [c0, c0 + Vc): (reference m_t, sum
+// exp(logit − m_t)) per row into stats[m, c0/ce_bn + tile], m_t being the
+// tile's row max or, from the second chunk on, the running max when that is
+// larger; the target logit
 // where the tile holds it, and P[m, j] = bf16(exp(logit[m, c0 + j] − m_t)) for
 // the chunk's columns j < Vc; columns [Vc, Nc8) (Nc8 = round_up(Vc, 8)) are
 // written as zero so the dH product runs its K loop over whole 16-byte chunks.
@@ -46,6 +51,10 @@ struct EpiCEProb {
   bf16* P;
   long ldp;
   int c0, Vc, Nc8;
+  // the running max over the earlier chunks (null for the first chunk): each
+  // tile's reference is max(tile max, running max), so a row whose maximum is
+  // not in this chunk has one reference for all its tiles and needs no rescale
+  const float* run_m;
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
@@ -99,6 +108,7 @@ struct EpiCEProb {
         float b = red[row];
 #pragma unroll
         for (int j = 1; j < WN; ++j) b = fmaxf(b, red[j * BMl + row]);
+        if (run_m && m < M) b = fmaxf(b, run_m[m]);
         rowmax[row] = b;
         const int t = m < M ? labels[m] - c0 : -1;
         tcol[row] = t >= 0 && t < Vc ? t : -1;
@@ -172,10 +182,13 @@ struct EpiCEProb {
 }  // namespace
 
 // Chunk [c0, c0 + Vc) after its logits product, one wave per live row: the
-// chunk max M_c of the tile maxima and its sum, the running max M and sum L
-// (first chunk: M = −inf, L = 0) moved to M' = max(M, M_c), α = e^(M − M')
+// chunk max M_c of the tile references m_t and its sum, the running max M and
+// sum L (first chunk: M = −inf, L = 0) moved to M' = max(M, M_c), α = e^(M − M')
 // for the dH accumulator, and P scaled in place by e^(m_t − M') per tile, so
-// P = bf16(exp(logit − M')). Rows without a target get P = 0.
+// P = bf16(exp(logit − M')). After the first chunk every m_t is at least M, so
+// a row whose maximum is not in this chunk has m_t = M = M' for every tile and
+// its P is left as it is; so are the rows without a target, whose dH the
+// finalize sets to zero whatever the product accumulated (P <= 1: finite).
 __global__ __launch_bounds__(256) void ce_rescale_kernel(HeadArgs a, int c0, int first) {
   int N = a.n;
   if (a.n_dev) N = min(N, *a.n_dev);
@@ -198,15 +211,14 @@ __global__ __launch_bounds__(256) void ce_rescale_kernel(HeadArgs a, int c0, int
     a.run_l[m] = (first ? 0.f : a.run_l[m] * al) + sc;
     a.alpha[m] = al;
   }
+  if (a.labels[m] < 0) return;
+  bool scaled = false;
+  for (int j = l; j < nt; j += 64) scaled |= st[j].x != mn;
+  if (!__any(scaled)) return;
   bf16* pr = a.dlog + (long)m * a.vchunk;
-  const bool live = a.labels[m] >= 0;
 #pragma unroll 4
   for (int k = l; k < Nc8 / 8; k += 64) {
     u32x4* q = reinterpret_cast<u32x4*>(pr + 8 * k);
-    if (!live) {
-      *q = u32x4{0u, 0u, 0u, 0u};
-      continue;
-    }
     const float f = __expf(st[(8 * k) / bn].x - mn);
     float v[8];
     unpack8(*q, v);
@@ -276,7 +288,8 @@ static GemmProblem chunk_logits_problem(const HeadArgs& a, int c0) {
 hipError_t head_prob(const HeadArgs& a, int c0, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const int Vc = min(a.vchunk, a.V - c0), Nc8 = (Vc + 7) / 8 * 8;
-  EpiCEProb epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.dlog, (long)a.vchunk, c0, Vc, Nc8};
+  EpiCEProb epi{a.labels, a.stats, a.ntn, a.tgt_logit, a.dlog, (long)a.vchunk, c0, Vc, Nc8,
+                c0 > 0 ? a.run_m : nullptr};
   if (a.ce_bn == 128) return launch_gemm_cfg<256, 128, 2, 2>(chunk_logits_problem(a, c0), epi, s);
   return launch_gemm_cfg<256, CE_BN, 2, 2>(chunk_logits_problem(a, c0), epi, s);
 }
