@@ -126,9 +126,24 @@ struct QBlock {
   int nt_w;    // key tiles the wave attends (0 if it has no query)
   bool empty;  // no wave of the block has a query (block-uniform)
 };
+// Workgroups go to the 8 XCDs round robin by linear id. The kernels take
+// their (tile index, kv head) from the linear id with the kv head varying
+// fastest (grid.y = Hkv): with 8 kv heads every XCD, and its L2, serves one
+// kv head, whose streamed tiles (K/V in the forward and dQ passes, its
+// q-heads' Q/dO in the dK/dV pass) its blocks share, and consecutive tile
+// indices (the heaviest-first order) still start first.
+struct XcdPos {
+  int x, kvh;
+};
+DSB_DEV XcdPos xcd_pos(int hkv) {
+  const int lin = (int)(blockIdx.x + gridDim.x * blockIdx.y);
+  return XcdPos{lin / hkv, lin % hkv};
+}
+
 DSB_DEV QBlock q_block(const AttnArgs& a, int w) {
   const int G = a.Hq / a.Hkv;
-  const int tile = blockIdx.x / G, b = blockIdx.x - tile * G;
+  const XcdPos xp = xcd_pos(a.Hkv);
+  const int tile = xp.x / G, b = xp.x - tile * G;
   QBlock r{};
   r.empty = tile >= *a.ntiles_dev;
   if (r.empty) return r;
@@ -137,7 +152,7 @@ DSB_DEV QBlock q_block(const AttnArgs& a, int w) {
   r.L = tl.y;
   const int p = 4 * b + w;
   r.q0 = tl.z + 32 * (3 - p / G);
-  r.h = blockIdx.y * G + p % G;
+  r.h = xp.kvh * G + p % G;
   r.empty = tl.z + 32 * (3 - (4 * b + 3) / G) >= r.L;  // the block's lightest subtile
   const int q_end = min(r.L, tl.z + 32 * (4 - (4 * b) / G));
   r.nt = (q_end + TR - 1) / TR;
@@ -210,7 +225,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const QBlock qb = q_block(a, w);
   if (qb.empty) return;
-  const int kvh = blockIdx.y, h = qb.h, st = qb.st, L = qb.L;
+  const int kvh = qb.h / (a.Hq / a.Hkv), h = qb.h, st = qb.st, L = qb.L;
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
   const int qpos = qb.q0 + lr;
   const bool qok = qpos < L;
@@ -435,7 +450,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const QBlock qb = q_block(a, w);
   if (qb.empty) return;
-  const int kvh = blockIdx.y, h = qb.h, st = qb.st, L = qb.L;
+  const int kvh = qb.h / (a.Hq / a.Hkv), h = qb.h, st = qb.st, L = qb.L;
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
   const int qpos = qb.q0 + lr;
   const bool qok = qpos < L;
@@ -546,9 +561,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
 // q head of the group over the queries at or after the block's first key.
 // LDS: 2 stages × (Q tile + dO tile + lse/dsum rows) ≈ 65 KB.
 __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
-  const int tile = blockIdx.x;
+  const XcdPos xp = xcd_pos(a.Hkv);
+  const int tile = xp.x;
   if (tile >= *a.ntiles_dev) return;
-  const int kvh = blockIdx.y, G = a.Hq / a.Hkv;
+  const int kvh = xp.kvh, G = a.Hq / a.Hkv;
   const int4 tl = a.tiles_k[tile];
   const int st = tl.x, L = tl.y, k0 = tl.z;
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TILE];
