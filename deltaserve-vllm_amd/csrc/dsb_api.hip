@@ -892,10 +892,12 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
         LK(head_prob(ha, c0, st));
       }
       {
-        // bytes: the tile statistics and running state of every row; the P
-        // pass over a row (4·Vc bytes) runs only where the row's maximum lies
-        // in the chunk (every row of the first chunk), so it is not counted
-        KScope ks(h, st, "ce_rescale", 0, 0, 0, 8.0 * Vc / h->ce_bn + 12, 0, 0);
+        // bytes: the tile statistics and running state of every row, and the
+        // P pass over every row (4·Vc bytes) in the first chunk; later chunks
+        // scale only the rows whose maximum lies in them, which the count
+        // leaves out (a lower bound)
+        KScope ks(h, st, "ce_rescale", 0, 0, 0, 8.0 * Vc / h->ce_bn + 12 + (c0 == 0 ? 4.0 * Vc : 0.0),
+                  0, 0);
         LK(head_rescale(ha, c0, st));
       }
       return 0;
