@@ -146,10 +146,12 @@ def fp32_reference_mode():
     torch.set_float32_matmul_precision("highest")
 
 
-def build_service(model: O.Model, family="llama3", device="cuda"):
+def build_service(model: O.Model, family="llama3", device="cuda", meta_extra=None):
     from deltaserve_amd.bwd_services.registry import get_service
 
     base, ft, meta = shared_from_model(model, device)
+    if meta_extra:
+        meta = dict(meta, **meta_extra)
     svc = get_service(family)(0)
     svc.shared = {"base": base, "ft": ft, "meta": meta}
     err = svc._on_weights_shared()

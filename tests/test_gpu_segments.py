@@ -6,6 +6,10 @@
   :92-94, base.py:148-208) computes exactly what the single-graph cycle
   computes: same kernels in the same order, so loss, gradients and updated
   masters agree bit for bit, for any run-ahead bound.
+* The attention backward's dK/dV pass runs on a second stream beside the
+  dQ pass (parallel graph branches, or two streams in an eager cycle); the
+  per-kernel timing mode runs them in order. All three give the same loss,
+  gradients and masters bit for bit (the passes share only inputs).
 * A cleared GPU grant holds the cycle at a boundary until it is set again.
 * Every cycle ends by writing clamp(A) and clamp(s·B) (bf16) into the bound
   rows of vLLM's stacked LoRA buffers (trainer.py:760-802) and nothing else.
@@ -67,6 +71,33 @@ def test_segmented_cycle_equals_single_graph(family, run_ahead, vchunk):
     finally:
         one.close()
         seg.close()
+
+
+@pytest.mark.parametrize("family", ["llama3", "qwen3"])
+def test_concurrent_attention_backward_equals_in_order(family):
+    meta, model, gacts = _setup(family)
+    n = sum(SEQ)
+    graph = build_service(model, family)
+    eager = build_service(model, family, meta_extra={"backward_hip_graph": False})
+    timed = build_service(model, family)
+    timed.set_kernel_timing(True)
+    svcs = [graph, eager, timed]
+    try:
+        for _ in range(2):
+            out = [s.process_backward(gacts, SEQ, n, epoch=0) for s in svcs]
+            assert graph.last_cycle_info["graph"]
+            assert not eager.last_cycle_info["graph"] and not timed.last_cycle_info["graph"]
+            for o in out[1:]:
+                assert o == out[0], (o, out[0])
+            ref = _state(graph)
+            for s in svcs[1:]:
+                st = _state(s)
+                for k in ref:
+                    assert torch.equal(ref[k][0], st[k][0]), ("master", k)
+                    assert torch.equal(ref[k][1], st[k][1]), ("grad", k)
+    finally:
+        for s in svcs:
+            s.close()
 
 
 def test_pause_points_per_vocab_chunk_and_layer():
