@@ -296,8 +296,12 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   static_assert(IA >= 1 && IB >= 1 && BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "loader split");
   static_assert(NW % 2 == 0, "row-block parity is the wave's");
   static_assert(IAB < 64, "vmcnt range");
-  constexpr int SA = BM * BK, SE = (BM + BN) * BK;  // elements
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * SE];
+  // LDS: two A slots, then three B slots (elements). A K tile is loaded one
+  // step ahead of its use, the B tile two: B is the operand every XCD fetches
+  // (A's row panels are the XCD's own), so its loads miss L2 more often and
+  // get the longer lead.
+  constexpr int SA = BM * BK, SB = BN * BK;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * SA + 3 * SB];
 
   int M = p.M;
   if (p.M_dev) M = min(M, *p.M_dev);
@@ -398,53 +402,67 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   // issue_one(j) so they can be spread over a run of MFMAs. Tiles past the
   // end (kt >= nk) fall past K of the second segment and fill the slot with
   // zeros without touching memory.
+  // A fill of K tile ktA into A slot sa and of K tile ktB into B slot sb;
+  // dstB is biased by −SA elements, so B row offsets keep the SA of the
+  // fragment-read layout (brow, btr).
   struct Fill {
     u32x4 dA, dB;
     int voA, voB, stA;
-    bool s1;
-    unsigned dst;
+    bool s1B;
+    unsigned dstA, dstB;
   };
-  auto make_fill = [&](int kt, int slot) {
+  auto a_slot = [&](int sa) { return lds0 + (unsigned)(sa * SA * 2) + (unsigned)(8 * wave * BK * 2); };
+  auto b_slot = [&](int sb) {
+    return lds0 + (unsigned)((SA + sb * SB) * 2) + (unsigned)(8 * wave * BK * 2);
+  };
+  auto make_fill = [&](int ktA, int sa, int ktB, int sb) {
     Fill f;
-    const bool s1 = kt < nk1;
-    const int k0 = s1 ? kt * BK : (kt - nk1) * BK;
-    const int K = s1 ? p.K1 : K2;
-    const int kb = (k0 * 2) | ((k0 + lch * 8 < K) ? 0 : OOB);
-    f.dA = s1 ? dA1 : dA2;
-    if constexpr (KN)
-      f.dB = kn_rsrc(s1, k0);
-    else
-      f.dB = s1 ? dB1 : dB2;
-    f.voA = (s1 ? voA1 : voA2) + kb;
-    f.voB = (s1 ? voB1 : voB2) + kb;
-    f.stA = s1 ? stA1 : stA2;
-    f.s1 = s1;
-    f.dst = lds0 + (unsigned)(slot * SE * 2) + (unsigned)(8 * wave * BK * 2);
+    {
+      const bool s1 = ktA < nk1;
+      const int k0 = s1 ? ktA * BK : (ktA - nk1) * BK;
+      const int kb = (k0 * 2) | ((k0 + lch * 8 < (s1 ? p.K1 : K2)) ? 0 : OOB);
+      f.dA = s1 ? dA1 : dA2;
+      f.voA = (s1 ? voA1 : voA2) + kb;
+      f.stA = s1 ? stA1 : stA2;
+    }
+    {
+      const bool s1 = ktB < nk1;
+      const int k0 = s1 ? ktB * BK : (ktB - nk1) * BK;
+      const int kb = (k0 * 2) | ((k0 + lch * 8 < (s1 ? p.K1 : K2)) ? 0 : OOB);
+      if constexpr (KN)
+        f.dB = kn_rsrc(s1, k0);
+      else
+        f.dB = s1 ? dB1 : dB2;
+      f.voB = (s1 ? voB1 : voB2) + kb;
+      f.s1B = s1;
+    }
+    f.dstA = a_slot(sa);
+    f.dstB = b_slot(sb);
     return f;
   };
   auto issue_one = [&](const Fill& f, int j) {
     if (j < IA) {
-      lds_dma16_m0(f.dA, f.voA + j * f.stA, f.dst + j * 8 * NW * BK * 2);
+      lds_dma16_m0(f.dA, f.voA + j * f.stA, f.dstA + j * 8 * NW * BK * 2);
     } else if constexpr (KN) {
-      set_m0(f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+      set_m0(f.dstB + (SA + (j - IA) * 8 * NW * BK) * 2);
       asm volatile("s_nop 0" ::: "memory");
-      dma16_m0(f.dB, f.s1 ? vkn1[j - IA] : vkn2[j - IA]);
+      dma16_m0(f.dB, f.s1B ? vkn1[j - IA] : vkn2[j - IA]);
     } else {
-      lds_dma16_m0(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]),
-                   f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+      lds_dma16_m0(f.dB, f.voB + (f.s1B ? boff1[j - IA] : boff2[j - IA]),
+                   f.dstB + (SA + (j - IA) * 8 * NW * BK) * 2);
     }
   };
   // the same load split around an MFMA: M0 before it, the load after it
   auto pre_one = [&](const Fill& f, int j) {
-    set_m0(j < IA ? f.dst + j * 8 * NW * BK * 2 : f.dst + (SA + (j - IA) * 8 * NW * BK) * 2);
+    set_m0(j < IA ? f.dstA + j * 8 * NW * BK * 2 : f.dstB + (SA + (j - IA) * 8 * NW * BK) * 2);
   };
   auto go_one = [&](const Fill& f, int j) {
     if (j < IA)
       dma16_m0(f.dA, f.voA + j * f.stA);
     else if constexpr (KN)
-      dma16_m0(f.dB, f.s1 ? vkn1[j - IA] : vkn2[j - IA]);
+      dma16_m0(f.dB, f.s1B ? vkn1[j - IA] : vkn2[j - IA]);
     else
-      dma16_m0(f.dB, f.voB + (f.s1 ? boff1[j - IA] : boff2[j - IA]));
+      dma16_m0(f.dB, f.voB + (f.s1B ? boff1[j - IA] : boff2[j - IA]));
   };
 
   f32x4 acc[FM][FN];
@@ -482,18 +500,22 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   // fragment i - FM, or with a [K, N] B half (i - FM) % 2 of B fragment
   // (i - FM) / 2 (one LDS instruction per read, so a read fits between two
   // MFMAs).
-  auto read_one = [&](const bf16* b, int s, int buf, int i) {
+  // ba: the A slot; bb: the B slot's base less SA elements (brow and btr
+  // include SA)
+  auto read_one = [&](const bf16* ba, const bf16* bb, int s, int buf, int i) {
     const int ch = ((4 * s + lq) ^ g) << 3;
     if (i < FM) {
-      af[buf][i] = *reinterpret_cast<const bf16x8*>(b + arow + ch + i * 16 * BK);
+      af[buf][i] = *reinterpret_cast<const bf16x8*>(ba + arow + ch + i * 16 * BK);
     } else if constexpr (KN) {
       const int fn = (i - FM) >> 1, h = (i - FM) & 1;
-      const char* t = reinterpret_cast<const char*>(b) + btr[fn] + 32 * s * BN * 2 + h * 4 * BN * 2;
+      const char* t = reinterpret_cast<const char*>(bb) + btr[fn] + 32 * s * BN * 2 + h * 4 * BN * 2;
       bkn[buf][fn][h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)t);
     } else {
-      bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(b + brow + ch + (i - FM) * 16 * BK);
+      bfr[buf][i - FM] = *reinterpret_cast<const bf16x8*>(bb + brow + ch + (i - FM) * 16 * BK);
     }
   };
+  auto a_base = [&](int sa) { return (const bf16*)smem + sa * SA; };
+  auto b_base = [&](int sb) { return (const bf16*)smem + SA + sb * SB; };
   constexpr int NM = FM * FN, NR = FM + (KN ? 2 : 1) * FN, H1 = IAB / 2;
   auto bfrag = [&](int buf, int fn) {
     if constexpr (KN)
@@ -508,8 +530,8 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
   // MFMA). A wave issues at most one instruction every few cycles, so a burst
   // of other instructions between MFMAs would leave the matrix pipe idle
   // (loads after every MFMA, or every other one, measured slower).
-  auto mma = [&](int buf, int t0, int t1, const bf16* nb, int ns, int nbuf, int nr,
-                 const Fill& f, int j0, int nj) {
+  auto mma = [&](int buf, int t0, int t1, const bf16* nba, const bf16* nbb, int ns, int nbuf,
+                 int nr, const Fill& f, int j0, int nj) {
     int r = 0, j = 0;
 #pragma unroll
     for (int t = t0; t < t1; ++t) {
@@ -523,7 +545,7 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
       mfma16_acc(acc[fm][fn], bfrag(buf, fn), af[buf][fm]);
       if (r < nr) {
         __builtin_amdgcn_sched_barrier(0);
-        read_one(nb, ns, nbuf, r++);
+        read_one(nba, nbb, ns, nbuf, r++);
         __builtin_amdgcn_sched_barrier(0);
       } else if (ld) {
         __builtin_amdgcn_sched_barrier(0);
@@ -533,69 +555,77 @@ __attribute__((amdgpu_waves_per_eu(WM* WN / 4, WM* WN / 4))) void gemm_nt_kernel
     }
 #pragma unroll
     for (int rr = 0; rr < NR; ++rr)
-      if (rr >= r && rr < nr) read_one(nb, ns, nbuf, rr);
+      if (rr >= r && rr < nr) read_one(nba, nbb, ns, nbuf, rr);
 #pragma unroll
     for (int jj = 0; jj < IAB; ++jj)
       if (jj >= j && jj < nj) issue_one(f, j0 + jj);
   };
-  // Loads of K tile kt (< nk1, first segment) into slot `slot`: the
-  // descriptors and row offsets are the loop-invariant ones of segment 1.
-  auto make_fill1 = [&](int kt, int slot) {
+  // Loads of K tiles ktA, ktB (both < nk1, first segment): the descriptors
+  // and row offsets are the loop-invariant ones of segment 1.
+  auto make_fill1 = [&](int ktA, int sa, int ktB, int sb) {
     Fill f;
-    const int k0 = kt * BK;
-    const int kb = (k0 * 2) | ((k0 + lch * 8 < p.K1) ? 0 : OOB);
+    const int k0a = ktA * BK, k0b = ktB * BK;
     f.dA = dA1;
     if constexpr (KN)
-      f.dB = kn_rsrc(true, k0);
+      f.dB = kn_rsrc(true, k0b);
     else
       f.dB = dB1;
-    f.voA = voA1 + kb;
-    f.voB = voB1 + kb;
+    f.voA = voA1 + ((k0a * 2) | ((k0a + lch * 8 < p.K1) ? 0 : OOB));
+    f.voB = voB1 + ((k0b * 2) | ((k0b + lch * 8 < p.K1) ? 0 : OOB));
     f.stA = stA1;
-    f.s1 = true;
-    f.dst = lds0 + (unsigned)(slot * SE * 2) + (unsigned)(8 * wave * BK * 2);
+    f.s1B = true;
+    f.dstA = a_slot(sa);
+    f.dstB = b_slot(sb);
     return f;
   };
 
-  // Prologue: stage kt0 loaded and published, slice 0 of it read, and the
-  // loads of stage kt0+1 in flight.
+  // Prologue: tile kt0 loaded and published, slice 0 of it read, and in
+  // flight, in this order: A and B of tile kt0+1, then B of tile kt0+2.
   {
-    const Fill f = make_fill(kt0, 0);
+    const Fill f = make_fill(kt0, 0, kt0, 0);
 #pragma unroll
     for (int j = 0; j < IAB; ++j) issue_one(f, j);
   }
   wait_vm<0>();
   lds_barrier();
 #pragma unroll
-  for (int i = 0; i < NR; ++i) read_one(smem, 0, 0, i);
+  for (int i = 0; i < NR; ++i) read_one(a_base(0), b_base(0), 0, 0, i);
   {
-    const Fill f = make_fill(kt0 + 1, 1);
+    const Fill f = make_fill(kt0 + 1, 1, kt0 + 1, 1);
 #pragma unroll
     for (int j = 0; j < IAB; ++j) issue_one(f, j);
+    const Fill fb = make_fill(kt0 + 1, 1, kt0 + 2, 2);
+#pragma unroll
+    for (int j = IA; j < IAB; ++j) issue_one(fb, j);
   }
 
-  // Step kt computes on slot kt&1 (fragments of slice 0 already in buffer 0).
+  // Step kt computes on A slot (kt−kt0)&1 and B slot (kt−kt0)%3 (fragments of
+  // slice 0 already in buffer 0). Its mid-step wait leaves in flight only the
+  // B loads of tile kt+2 (issued last, in the step before): A and B of tile
+  // kt+1 have landed. After that barrier its slots are free, and it issues A
+  // of tile kt+2 and then B of tile kt+3 into them.
   auto step = [&](int kt, auto&& mk) {
-    const int cur = (kt - kt0) & 1;
-    const bf16* b = smem + cur * SE;
-    const Fill next2 = mk(kt + 2, cur);  // stage kt+2 refills this step's slot
+    const int ca = (kt - kt0) & 1, cb = (kt - kt0) % 3;
+    const bf16* ba = a_base(ca);
+    const bf16* bb = b_base(cb);
+    const Fill next = mk(kt + 2, ca, kt + 3, cb);
     __builtin_amdgcn_sched_barrier(0);
-    mma(0, 0, NM / 2, b, 1, 1, NR, next2, 0, 0);
+    mma(0, 0, NM / 2, ba, bb, 1, 1, NR, next, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm0();
-    wait_vm<0>();
+    wait_vm<IB>();
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    mma(0, NM / 2, NM, b, 1, 1, 0, next2, 0, H1);
+    mma(0, NM / 2, NM, ba, bb, 1, 1, 0, next, 0, H1);
     __builtin_amdgcn_sched_barrier(0);
-    mma(1, 0, NM, smem + (cur ^ 1) * SE, 0, 0, NR, next2, H1, IAB - H1);
+    mma(1, 0, NM, a_base(ca ^ 1), b_base(cb == 2 ? 0 : cb + 1), 0, 0, NR, next, H1, IAB - H1);
     __builtin_amdgcn_sched_barrier(0);
   };
-  // Steps whose prefetch (tile kt+2) stays in segment 1 use the invariant
-  // segment-1 fill; the last few steps select the segment per tile.
-  // (tiles past this block's range that the last steps prefetch are other
-  // blocks' tiles or zero fills past K: loaded, never multiplied)
-  const int nfast = max(kt0, min(kt1, nk1 - 2));
+  // Steps whose prefetches (A tile kt+2, B tile kt+3) stay in segment 1 use
+  // the invariant segment-1 fill; the last few steps select the segment per
+  // tile. (Tiles past this block's range that the last steps prefetch are
+  // other blocks' tiles or zero fills past K: loaded, never multiplied.)
+  const int nfast = max(kt0, min(kt1, nk1 - 3));
   int kt = kt0;
   for (; kt < nfast; ++kt) step(kt, make_fill1);
   for (; kt < kt1; ++kt) step(kt, make_fill);
