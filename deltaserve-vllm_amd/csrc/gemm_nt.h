@@ -229,6 +229,47 @@ DSB_DEV void for_each_row8_pf(const f32x4 (&acc)[FM][FN], int mw, int nw, int M,
   }
 }
 
+// for_each_row8_pf for a wave tile whose rows are all below M and whose
+// columns the caller has checked: no per-row or per-block tests, so the
+// code between the loads and their use is straight-line and the compiler's
+// memory-counter waits count exactly how many loads and stores were issued
+// after the one a chunk needs. (With the tests, each row's loads and stores
+// sit behind an exec-mask branch and the compiler, unable to count across
+// them, waits for every outstanding access before each row of the first two
+// blocks, the previous row's stores included.)
+template <int FM, int FN, class L, class F>
+DSB_DEV void for_each_row8_pf_full(const f32x4 (&acc)[FM][FN], int mw, int nw, int lane,
+                                   int wave, void* smem, L&& load, F&& f) {
+  constexpr int TN = FN * 16, PITCH = TN + 4, CG = TN / 8, RPI = 64 / CG, IT = 32 / RPI;
+  static_assert(64 % CG == 0 && FM % 2 == 0, "row groups");
+  using T = decltype(load(0, 0));
+  float* buf = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
+  const int rsub = lane / CG, cg = lane % CG, n = nw + cg * 8;
+  constexpr int PD = 2;
+  T pf[PD + 1][IT];
+#pragma unroll
+  for (int b = 0; b < PD && b < FM / 2; ++b)
+#pragma unroll
+    for (int it = 0; it < IT; ++it) pf[b][it] = load(mw + b * 32 + it * RPI + rsub, n);
+#pragma unroll
+  for (int b = 0; b < FM / 2; ++b) {
+    if (b + PD < FM / 2) {
+#pragma unroll
+      for (int it = 0; it < IT; ++it)
+        pf[(b + PD) % (PD + 1)][it] = load(mw + (b + PD) * 32 + it * RPI + rsub, n);
+    }
+    stage32<FM, FN, PITCH>(acc, b, buf, lane);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int row = it * RPI + rsub;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(buf + row * PITCH + cg * 8 + 4);
+      float v[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+      f(mw + b * 32 + row, n, v, pf[b % (PD + 1)][it]);
+    }
+  }
+}
+
 // 8 values to bf16 at p[0 .. min(8, lim)); 16-byte store when whole and aligned.
 // The 16-byte store is non-temporal: the outputs of a whole wave of tiles land
 // at once, and streaming them keeps them from evicting the A/B panels the
@@ -686,6 +727,21 @@ struct EpiBF16 {
       });
       return;
     }
+    if (mw + FM * 16 <= M && nw + FN * 16 <= N && ldr % 8 == 0 && ldc % 8 == 0 &&
+        ((((unsigned long)R) | ((unsigned long)C)) & 15) == 0) {
+      // every chunk whole and aligned
+      for_each_row8_pf_full(
+          acc, mw, nw, lane, wave, smem,
+          [&](int m, int n) { return ldg128_nt(R + (long)m * ldr + n); },
+          [&](int m, int n, float* v, const u32x4& r) {
+            float rf[8];
+            unpack8(r, rf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] += rf[i];
+            __builtin_nontemporal_store(pack8(v), reinterpret_cast<u32x4*>(C + (long)m * ldc + n));
+          });
+      return;
+    }
     // residual rows read ahead (whole aligned chunks; others read in place)
     auto whole = [&](int m, int n) {
       return N - n >= 8 && (((unsigned long)(R + (long)m * ldr + n)) & 15) == 0;
@@ -806,6 +862,12 @@ struct EpiSwiGLUBwd {
   template <int FM, int FN, int WM, int WN>
   DSB_DEV void run(const f32x4 (&acc)[FM][FN], int mw, int nw, int M, int lane, int wave,
                    void* smem) const {
+    if (mw + FM * 16 <= M && nw + FN * 16 <= I) {
+      for_each_row8_pf_full(
+          acc, mw, nw, lane, wave, smem, [&](int m, int n) { return load(m, n); },
+          [&](int m, int n, float* v, const Chunk& c) { finish(m, n, v, c); });
+      return;
+    }
     for_each_row8_pf(
         acc, mw, nw, M, lane, wave, smem,
         [&](int m, int n) { return n < I ? load(m, n) : Chunk{}; },
@@ -855,6 +917,35 @@ struct EpiF32 {
     struct F8 {
       f32x4 a, b;
     };
+    if (mw + FM * 16 <= M && nw + FN * 16 <= N && ldc % 4 == 0 &&
+        (((unsigned long)C) & 15) == 0) {
+      // every chunk whole and aligned; the row factor read with the chunk
+      // (the pointer test outside the walk keeps its body branch-free)
+      struct F8s {
+        f32x4 a, b;
+        float s;
+      };
+      auto walk = [&](auto scaled) {
+        for_each_row8_pf_full(
+            acc, mw, nw, lane, wave, smem,
+            [&](int m, int n) {
+              const float* c = C + (long)m * ldc + n;
+              return F8s{*reinterpret_cast<const f32x4*>(c),
+                         *reinterpret_cast<const f32x4*>(c + 4),
+                         decltype(scaled)::value ? rowscale[m] : 1.f};
+            },
+            [&](int m, int n, float* v, const F8s& x) {
+              float* c = C + (long)m * ldc + n;
+              *reinterpret_cast<f32x4*>(c) = f32x4{v[0], v[1], v[2], v[3]} + x.a * x.s;
+              *reinterpret_cast<f32x4*>(c + 4) = f32x4{v[4], v[5], v[6], v[7]} + x.b * x.s;
+            });
+      };
+      if (rowscale)
+        walk(std::true_type{});
+      else
+        walk(std::false_type{});
+      return;
+    }
     for_each_row8_pf(
         acc, mw, nw, M, lane, wave, smem,
         [&](int m, int n) {
