@@ -102,15 +102,29 @@ struct EpiCEProb {
       for (int fn = 0; fn < FN; ++fn) asm volatile("" : "+a"(accw[fm][fn]));
     __syncthreads();
     if (wn == 0 && lq == 0) {
+      // the rows' labels and running maxima, all loaded before the first is
+      // used (rows past M read row M − 1 and are not used): loads behind a
+      // per-row test would each wait for the one before
+      int lab[FM];
+      float rmx[FM];
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) lab[fm] = labels[min(mw + fm * 16 + l16, M - 1)];
+      if (run_m) {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) rmx[fm] = run_m[min(mw + fm * 16 + l16, M - 1)];
+      } else {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) rmx[fm] = -INFINITY;
+      }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         const int row = wm * TM + fm * 16 + l16, m = mw + fm * 16 + l16;
         float b = red[row];
 #pragma unroll
         for (int j = 1; j < WN; ++j) b = fmaxf(b, red[j * BMl + row]);
-        if (run_m && m < M) b = fmaxf(b, run_m[m]);
+        if (run_m) b = fmaxf(b, rmx[fm]);
         rowmax[row] = b;
-        const int t = m < M ? labels[m] - c0 : -1;
+        const int t = m < M ? lab[fm] - c0 : -1;
         tcol[row] = t >= 0 && t < Vc ? t : -1;
       }
     }
