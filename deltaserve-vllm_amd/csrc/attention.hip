@@ -87,6 +87,22 @@ struct SeqTiles {
   }
 };
 
+// Ring prologue of the K/V stream (forward and dQ passes): key tiles 0 and 1
+// (when there are two) go to the two stages at once, so the second tile's
+// latency runs beside the first's instead of after it. The loop then issues
+// tile t+1 at step t from t = 1 on, into the stage tile t−1 has freed. At the
+// short sequences of a packed cycle most blocks stream only a few tiles, so
+// the prologue's exposed latency is a large share of a block.
+DSB_DEV void load_first_two(const SeqTiles& tk, const SeqTiles& tv, int nt, int col0,
+                            unsigned lds0, int wave) {
+  tk.load(0, col0, lds0, wave);
+  tv.load(0, col0, lds0 + TILE * 2, wave);
+  if (nt > 1) {
+    tk.load(TR, col0, lds0 + 2 * TILE * 2, wave);
+    tv.load(TR, col0, lds0 + 3 * TILE * 2, wave);
+  }
+}
+
 // Row fragments of one global row (lane's row, 8 × 16 columns) straight to
 // registers; columns from hd on (and rows that are not ok) are zeros.
 DSB_DEV void load_row_frags(const bf16* base, long ld, long row, int col0, bool ok, int lh,
@@ -246,8 +262,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const FragOffs fo(lane);
   const SeqTiles tk(a.k, a.ldk, st, L, w, lane, hd), tv(a.v, a.ldv, st, L, w, lane, hd);
   const unsigned lds0 = lds_addr(smem);
-  tk.load(0, kvh * hd, lds0, w);
-  tv.load(0, kvh * hd, lds0 + TILE * 2, w);
+  load_first_two(tk, tv, qb.nt, kvh * hd, lds0, w);
   // The wave computes the tiles with a key at or before its last query
   // (t < nt_w); after those it only takes part in the block's loads and
   // barriers. Two loops, so the compute loop has no skip path (a skip path
@@ -256,7 +271,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   auto advance = [&](int t) {
     wait_vm<0>();
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
-    if (t + 1 < nt) {
+    if (t >= 1 && t + 1 < nt) {  // tiles 0 and 1 came with the prologue
       const unsigned nxt = lds0 + (unsigned)(((t + 1) & 1) * 2 * TILE * 2);
       tk.load((t + 1) * TR, kvh * hd, nxt, w);
       tv.load((t + 1) * TR, kvh * hd, nxt + TILE * 2, w);
@@ -464,8 +479,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   const FragOffs fo(lane);
   const SeqTiles tk(a.k, a.ldk, st, L, w, lane, hd), tv(a.v, a.ldv, st, L, w, lane, hd);
   const unsigned lds0 = lds_addr(smem);
-  tk.load(0, kvh * hd, lds0, w);
-  tv.load(0, kvh * hd, lds0 + TILE * 2, w);
+  load_first_two(tk, tv, qb.nt, kvh * hd, lds0, w);
 
   f32x16 dq[4];
 #pragma unroll
@@ -483,7 +497,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttnArgs a) {
   auto advance = [&](int t) {
     wait_vm<0>();
     lds_barrier();  // tile t landed for every wave; stage (t+1)&1 is free
-    if (t + 1 < nt) {
+    if (t >= 1 && t + 1 < nt) {  // tiles 0 and 1 came with the prologue
       const unsigned nxt = lds0 + (unsigned)(((t + 1) & 1) * 2 * TILE * 2);
       tk.load((t + 1) * TR, kvh * hd, nxt, w);
       tv.load((t + 1) * TR, kvh * hd, nxt + TILE * 2, w);
@@ -617,13 +631,20 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     to.load(q0, hq * hd, d + TILE * 2, w);
   };
   if (nit > 0) {
-    // the first pair's tiles are requested before the wait on its lse/dsum
-    // rows, so the K/V rows, those rows and the tiles arrive in one latency
+    // the first two pairs' tiles (and the second pair's lse/dsum rows, kept
+    // in nl/nd for the end of pair 0) are requested before the wait on the
+    // first pair's lse/dsum rows, so the K/V rows, those rows and both pairs'
+    // tiles arrive in one latency; the loop issues pair it+1 from it = 1 on
     load_ld(0);
+    const float nl0 = nl, nd0 = nd;
     stage(0, 0);
+    if (nit > 1) {
+      load_ld(1);
+      stage(1, 1);
+    }
     if (tid < TR) {
-      sLD[0][0][tid] = nl;
-      sLD[0][1][tid] = nd;
+      sLD[0][0][tid] = nl0;
+      sLD[0][1][tid] = nd0;
     }
   }
   for (int it = 0; it < nit; ++it) {
@@ -633,7 +654,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(AttnArgs a) {
     const bf16* sO = sQ + TILE;
     wait_vm<0>();
     __syncthreads();  // pair `it` (tiles and lse/dsum rows) visible; the other stage is free
-    if (it + 1 < nit) {
+    if (it >= 1 && it + 1 < nit) {
       load_ld(it + 1);
       stage(it + 1, sidx ^ 1);
     }
