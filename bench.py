@@ -302,6 +302,10 @@ def main():
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the saved-gate_up variant timing")
     ap.add_argument("--classes-out", default=os.path.join(ROOT, "gpurun_out", "kernel_classes.json"))
+    ap.add_argument("--serial-layers", action="store_true",
+                    help="each layer's recompute right before its backward on one stream "
+                         "(meta backward_serial_layers), instead of beside the previous "
+                         "layer's backward")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of 2 GiB (3 times) and exit: the "
                          "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -327,6 +331,8 @@ def main():
     base, ft, meta = build_synthetic(cfg, dev)
     meta["max_saved_finetuning_tokens"] = n
     meta["backward_max_seqs"] = len(seq_lens)
+    if args.serial_layers:
+        meta["backward_serial_layers"] = True
     svc = get_service(cfg["family"])(0)
     svc.shared = {"base": base, "ft": ft, "meta": meta}
     err = svc._on_weights_shared()

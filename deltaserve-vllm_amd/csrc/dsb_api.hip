@@ -226,6 +226,22 @@ struct dsb_handle {
   // forked from and joined back into the cycle's stream by these events
   hipStream_t hs2 = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  // Layer overlap: layer li's recompute writes buffer set li & 1, so the
+  // recompute of the layer processed next (li − 1) runs on a third stream
+  // beside layer li's backward, forked and joined inside layer li's segment.
+  // The side stream's products take their own split-K and skinny-slice
+  // scratch (part2, tn_work2). Off under per-kernel timing, with
+  // DSB_FLAG_SERIAL_LAYERS, with one layer, or for large cycles (see
+  // dsb_create); set 1 then aliases set 0.
+  struct RecSet {
+    bf16 *xn1, *qkv_pre, *qk, *ctx, *ores, *resid, *xn2, *gu, *hb, *Zqkv_b, *Zo_b, *Zgu_b, *Zd_b;
+    float* lse;
+  };
+  RecSet rset[2] = {};
+  bool overlap = false;
+  hipStream_t hs3 = nullptr;
+  hipEvent_t ev_fork3 = nullptr, ev_join3 = nullptr;
+  float *part2 = nullptr, *tn_work2 = nullptr;
   std::vector<LayerState> layers;
   const bf16* lm_w = nullptr;
   const bf16* norm_w = nullptr;
@@ -464,6 +480,31 @@ int finalize(dsb_handle* h) {
     }
     h->part_elems = need;
     if (need > 0) CKR(dalloc(h, &h->part, need));
+  }
+  {
+    dsb_handle::RecSet& s0 = h->rset[0];
+    s0 = {h->xn1, h->qkv_pre, h->qk, h->ctx, h->ores, h->resid, h->xn2, h->gu, h->hb,
+          h->Zqkv_b, h->Zo_b, h->Zgu_b, h->Zd_b, h->lse};
+    h->rset[1] = s0;
+    if (h->overlap) {
+      dsb_handle::RecSet& s1 = h->rset[1];
+      CKR(dalloc(h, &s1.xn1, NN * D));
+      CKR(dalloc(h, &s1.qkv_pre, NN * W3));
+      CKR(dalloc(h, &s1.qk, NN * (q + kv)));
+      CKR(dalloc(h, &s1.ctx, NN * q));
+      CKR(dalloc(h, &s1.ores, NN * q));
+      CKR(dalloc(h, &s1.resid, NN * D));
+      CKR(dalloc(h, &s1.xn2, NN * D));
+      CKR(dalloc(h, &s1.gu, NN * 2 * I));
+      CKR(dalloc(h, &s1.hb, NN * I));
+      CKR(dalloc(h, &s1.Zqkv_b, NN * 3 * r));
+      CKR(dalloc(h, &s1.Zo_b, NN * r));
+      CKR(dalloc(h, &s1.Zgu_b, NN * 2 * r));
+      CKR(dalloc(h, &s1.Zd_b, NN * r));
+      CKR(dalloc(h, &s1.lse, (long)h->Hq * NN));
+      CKR(dalloc(h, &h->tn_work2, h->tn_work_elems));
+      if (h->part_elems > 0) CKR(dalloc(h, &h->part2, h->part_elems));
+    }
   }
   CKR(dalloc(h, &h->cosb, NN * (h->hd / 2)));
   CKR(dalloc(h, &h->sinb, NN * (h->hd / 2)));
@@ -853,81 +894,16 @@ HeadArgs head_args(dsb_handle* h) {
 // as one graph); the pause-point path (reference base.py:148-208,
 // _maybe_pause per vocab chunk and per layer) launches them one graph per
 // segment.
-int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
+// One decoder layer of the cycle: its forward recompute (rec) into the
+// current buffer set and/or its backward (bwd) from it. lo counts the layers
+// processed before this one (the incoming gradient buffers alternate by it).
+int enqueue_layer(dsb_handle* h, int li, int lo, hipStream_t st, bool rec, bool bwd) {
   const int N = h->N, D = h->D, q = h->q, kv = h->kv, W3 = h->W3, I = h->I, r = h->r;
   const int* nd = &h->d_hdr->n;
   const float eps = h->d.rms_eps;
   const double Hq = h->Hq;
-  const int C = h->nvc;
-  if (seg < 2 * C) {
-    // ---- head: loss and grad wrt final_in (head.py:42-100)
-    const HeadArgs ha = head_args(h);
-    if (seg == 0) {
-      h->kpos = 0;  // kernel-timing records restart with every cycle
-      {
-        KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
-        LK(rope_table(h->d_pos, N, nd, h->inv_freq, h->hd / 2, h->cosb, h->sinb, st));
-      }
-      {
-        KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
-        LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
-      }
-      {
-        KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
-        LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
-      }
-      {
-        KScope ks(h, st, "labels", 0, 0, 0, 16, 0, 0);
-        LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
-      }
-    }
-    const int c = seg / 2;
-    const int c0 = c * h->vchunk, Vc = std::min(h->vchunk, h->V - c0);
-    if ((seg & 1) == 0) {
-      {
-        // 2·n·Vc·D of the head's algorithmic 4·M·D·V (the logits product)
-        KScope ks(h, st, h->ce_bn == 128 ? "gemm256x128_ce_prob" : "gemm256_ce_prob",
-                  2.0 * Vc * D, 0, 0, 2.0 * D + 8.0 * Vc / h->ce_bn, 0,
-                  2.0 * Vc * D + 2.0 * Vc);
-        LK(head_prob(ha, c0, st));
-      }
-      {
-        // bytes: the tile statistics and running state of every row, and the
-        // P pass over every row (4·Vc bytes) in the first chunk; later chunks
-        // scale only the rows whose maximum lies in them, which the count
-        // leaves out (a lower bound)
-        KScope ks(h, st, "ce_rescale", 0, 0, 0, 8.0 * Vc / h->ce_bn + 12 + (c0 == 0 ? 4.0 * Vc : 0.0),
-                  0, 0);
-        LK(head_rescale(ha, c0, st));
-      }
-      return 0;
-    }
-    {
-      // the other 2·n·Vc·D: dH = dH·α + P·W_chunk
-      const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(N, D);
-      const bool split = head_dh_split(ha, c0) > 1;
-      int tail = 0;
-      const bool tsplit = head_dh_tail(ha, c0, &tail) > 1;
-      KScope ks(h, st,
-                std::string(split ? "gemm256sk" : tsplit ? "gemm256t" : cfg_name(cfg)) + "_f32",
-                2.0 * Vc * D, 0, 0, 2.0 * Vc + 8.0 * D, 0, 2.0 * Vc * D);
-      LK(head_chunk_dh(ha, c0, st));
-    }
-    if (c == C - 1) {
-      {
-        KScope ks(h, st, "ce_finalize", 0, 0, 0, 10.0 * D + 24, 0, 0);
-        LK(head_finalize(ha, st));
-      }
-      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 12.0 * D, 0, 2.0 * D);
-      LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, h->g0, D,
-                     N, nd, D, eps, st, nullptr, h->g32[0]));
-    }
-    return 0;
-  }
-  if (seg < 2 * C + h->L) {
-    const int lo = seg - 2 * C;  // layers done before this one in the cycle
-    h->tn_pending.clear();
-    const int li = h->L - 1 - lo;
+  {
+    if (bwd) h->tn_pending.clear();
     // the incoming gradient alternates between the two g buffers layer by layer
     bf16* g = (lo & 1) ? h->g1 : h->g0;
     bf16* gnext = (lo & 1) ? h->g0 : h->g1;
@@ -987,7 +963,10 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     const bf16* rs = srm ? h->rm_in[li] : h->resid;
     const long ldrs = srm ? h->ld_rm_in : (long)D;
 
+    const bool hdual = hd && dual_splits(h, &I, 1, r) > 0;
+
     // ================= forward recompute (llama3.py:62-146, qwen3.py:68-130)
+    if (rec) {
     {
       KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
       LK(rmsnorm_fwd(x, ldx, (const bf16*)ls.w.in_ln, h->xn1, D, N, nd, D, eps, st));
@@ -1051,8 +1030,9 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
     // Z_d = h·A_dᵀ feeds only grad_B of down (the down product itself is not
     // recomputed): when the fused kernel fits, it is computed in the backward
     // together with grad_A_d from one pass over h
-    const bool hdual = hd && dual_splits(h, &I, 1, r) > 0;
     if (hd && !hdual) CKR(skinny(h, h->hb, I, ls.Ad, r, I, h->Zd_b, r, st));
+    }  // rec
+    if (!bwd) return 0;
 
     // ================= backward (llama3.py:149-219, qwen3.py:147-204, ffn.py:29-48)
     if (hd) CKR(skinny(h, g, D, ls.BTd, r, D, h->gZd_b, r, st));
@@ -1253,6 +1233,115 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
                      N, nd, D, eps, st, h->grm32, gnext32));
     }
     CKR(tn_flush(h, st));
+    return 0;
+  }
+  return 0;
+}
+
+void use_set(dsb_handle* h, int k) {
+  const dsb_handle::RecSet& s = h->rset[k];
+  h->xn1 = s.xn1; h->qkv_pre = s.qkv_pre; h->qk = s.qk; h->ctx = s.ctx; h->ores = s.ores;
+  h->resid = s.resid; h->xn2 = s.xn2; h->gu = s.gu; h->hb = s.hb; h->Zqkv_b = s.Zqkv_b;
+  h->Zo_b = s.Zo_b; h->Zgu_b = s.Zgu_b; h->Zd_b = s.Zd_b; h->lse = s.lse;
+}
+
+int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
+  const int N = h->N, D = h->D;
+  const int* nd = &h->d_hdr->n;
+  const float eps = h->d.rms_eps;
+  const int C = h->nvc;
+  if (seg < 2 * C) {
+    // ---- head: loss and grad wrt final_in (head.py:42-100)
+    const HeadArgs ha = head_args(h);
+    if (seg == 0) {
+      h->kpos = 0;  // kernel-timing records restart with every cycle
+      {
+        KScope ks(h, st, "rope_table", 0, 0, 0, 4.0 + 64 * 8.0, 0, 0);
+        LK(rope_table(h->d_pos, N, nd, h->inv_freq, h->hd / 2, h->cosb, h->sinb, st));
+      }
+      {
+        KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
+        LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
+      }
+      {
+        KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
+        LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
+      }
+      {
+        KScope ks(h, st, "labels", 0, 0, 0, 16, 0, 0);
+        LK(build_labels(h->ids, h->d_pred, h->labels, N, nd, h->V, &h->d_hdr->err, st));
+      }
+    }
+    const int c = seg / 2;
+    const int c0 = c * h->vchunk, Vc = std::min(h->vchunk, h->V - c0);
+    if ((seg & 1) == 0) {
+      {
+        // 2·n·Vc·D of the head's algorithmic 4·M·D·V (the logits product)
+        KScope ks(h, st, h->ce_bn == 128 ? "gemm256x128_ce_prob" : "gemm256_ce_prob",
+                  2.0 * Vc * D, 0, 0, 2.0 * D + 8.0 * Vc / h->ce_bn, 0,
+                  2.0 * Vc * D + 2.0 * Vc);
+        LK(head_prob(ha, c0, st));
+      }
+      {
+        // bytes: the tile statistics and running state of every row, and the
+        // P pass over every row (4·Vc bytes) in the first chunk; later chunks
+        // scale only the rows whose maximum lies in them, which the count
+        // leaves out (a lower bound)
+        KScope ks(h, st, "ce_rescale", 0, 0, 0, 8.0 * Vc / h->ce_bn + 12 + (c0 == 0 ? 4.0 * Vc : 0.0),
+                  0, 0);
+        LK(head_rescale(ha, c0, st));
+      }
+      return 0;
+    }
+    {
+      // the other 2·n·Vc·D: dH = dH·α + P·W_chunk
+      const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : pick_gemm_cfg(N, D);
+      const bool split = head_dh_split(ha, c0) > 1;
+      int tail = 0;
+      const bool tsplit = head_dh_tail(ha, c0, &tail) > 1;
+      KScope ks(h, st,
+                std::string(split ? "gemm256sk" : tsplit ? "gemm256t" : cfg_name(cfg)) + "_f32",
+                2.0 * Vc * D, 0, 0, 2.0 * Vc + 8.0 * D, 0, 2.0 * Vc * D);
+      LK(head_chunk_dh(ha, c0, st));
+    }
+    if (c == C - 1) {
+      {
+        KScope ks(h, st, "ce_finalize", 0, 0, 0, 10.0 * D + 24, 0, 0);
+        LK(head_finalize(ha, st));
+      }
+      KScope ks(h, st, "rmsnorm_bwd", 0, 0, 0, 12.0 * D, 0, 2.0 * D);
+      LK(rmsnorm_bwd(h->final_in, h->act_ld, h->dH, true, D, h->norm_w, nullptr, 0, h->g0, D,
+                     N, nd, D, eps, st, nullptr, h->g32[0]));
+    }
+    return 0;
+  }
+  if (seg < 2 * C + h->L) {
+    const int lo = seg - 2 * C;  // layers done before this one in the cycle
+    const int li = h->L - 1 - lo;
+    const bool ov = h->overlap && !h->ktiming;
+    if (lo == 0 || !ov) {
+      use_set(h, li & 1);
+      CKR(enqueue_layer(h, li, lo, st, true, false));
+    }
+    // the next layer's recompute (into the other set) beside this backward
+    const bool fork = ov && li >= 1;
+    if (fork) {
+      CK(hipEventRecord(h->ev_fork3, st));
+      CK(hipStreamWaitEvent(h->hs3, h->ev_fork3, 0));
+      use_set(h, (li - 1) & 1);
+      std::swap(h->part, h->part2);
+      std::swap(h->tn_work, h->tn_work2);
+      const int rc = enqueue_layer(h, li - 1, lo + 1, h->hs3, true, false);
+      std::swap(h->part, h->part2);
+      std::swap(h->tn_work, h->tn_work2);
+      if (rc != 0) return rc;
+    }
+    use_set(h, li & 1);
+    CKR(enqueue_layer(h, li, lo, st, false, true));
+    if (fork) {
+      CK(hipEventRecord(h->ev_join3, h->hs3));
+      CK(hipStreamWaitEvent(st, h->ev_join3, 0));
+    }
     return 0;
   }
   // ---- per-layer clip + AdamW (trainer.py:624-636, :668)
@@ -1510,8 +1599,18 @@ int dsb_create(const dsb_desc* d, dsb_handle** out) {
               : d->gemm_tile == 64  ? GEMM_SKINNY : -1;
   h->layers.resize(h->L);
   h->ktiming = (d->flags & DSB_FLAG_KTIMING) != 0;
+  // Layer overlap pays where the products leave CUs idle: 256-token to
+  // 4.7 K-token cycles at 1–5 K hidden (C1, C2, the 256-token Qwen3-14B
+  // cycle: 9–24 % shorter) but not at 8192 tokens × 4096 (C3: 0.1–0.3 %
+  // longer), whose products fill every CU for several rounds; it is on up to
+  // s_max · hidden = 2^24.
+  h->overlap = !(d->flags & DSB_FLAG_SERIAL_LAYERS) && h->L > 1 &&
+               (long)d->s_max * d->hidden <= (16L << 20);
   hipError_t e = hipStreamCreateWithFlags(&h->hs, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&h->hs2, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&h->hs3, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_fork3, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_join3, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_fork, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ev_in, hipEventDisableTiming);
@@ -1531,6 +1630,7 @@ void dsb_destroy(dsb_handle* h) {
   if (!h) return;
   if (h->hs) (void)hipStreamSynchronize(h->hs);
   if (h->hs2) (void)hipStreamSynchronize(h->hs2);
+  if (h->hs3) (void)hipStreamSynchronize(h->hs3);
   drop_graphs(h);
   for (hipEvent_t e : h->ring) (void)hipEventDestroy(e);
   if (h->d_pub_jobs) (void)hipFree(h->d_pub_jobs);
@@ -1548,6 +1648,9 @@ void dsb_destroy(dsb_handle* h) {
   if (h->ev_fork) (void)hipEventDestroy(h->ev_fork);
   if (h->ev_join) (void)hipEventDestroy(h->ev_join);
   if (h->hs2) (void)hipStreamDestroy(h->hs2);
+  if (h->ev_fork3) (void)hipEventDestroy(h->ev_fork3);
+  if (h->ev_join3) (void)hipEventDestroy(h->ev_join3);
+  if (h->hs3) (void)hipStreamDestroy(h->hs3);
   if (h->hs) (void)hipStreamDestroy(h->hs);
   delete h;
 }

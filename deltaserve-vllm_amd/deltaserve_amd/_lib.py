@@ -23,7 +23,7 @@ FAMILY_LLAMA3, FAMILY_QWEN3 = 0, 1
 ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
 PROJ_INDEX = {p: i for i, p in enumerate(PROJS)}
-FLAG_GRAPH, FLAG_NO_CLIP, FLAG_KTIMING = 1, 2, 4
+FLAG_GRAPH, FLAG_NO_CLIP, FLAG_KTIMING, FLAG_SERIAL_LAYERS = 1, 2, 4, 8
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 
 

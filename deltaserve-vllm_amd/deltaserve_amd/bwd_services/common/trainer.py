@@ -201,6 +201,8 @@ class LoraSftTrainerService(BackwardService):
         d.beta1, d.beta2, d.adam_eps = 0.9, 0.999, 1e-8
         d.weight_decay, d.max_grad_norm = self.weight_decay, 1.0
         d.flags = L.FLAG_GRAPH if _graph_enabled(meta) else 0
+        if meta.get("backward_serial_layers"):
+            d.flags |= L.FLAG_SERIAL_LAYERS
         d.vocab_chunk = int(meta.get("backward_vocab_chunk") or 0)
         d.gemm_tile = int(meta.get("backward_gemm_tile") or 0)
         h = c_void_p()

@@ -33,7 +33,12 @@ enum {
 /* element types of the capture entry points */
 enum { DSB_DT_BF16 = 0, DSB_DT_F16 = 1, DSB_DT_F32 = 2 };
 /* dsb_desc.flags */
-enum { DSB_FLAG_GRAPH = 1u, DSB_FLAG_NO_CLIP = 2u, DSB_FLAG_KTIMING = 4u };
+/* DSB_FLAG_SERIAL_LAYERS: run each layer's recompute right before its
+   backward on the cycle's stream, instead of beside the previous layer's
+   backward on a second stream (the default for models of more than one layer
+   whose s_max · hidden is at most 2^24; results are the same either way). */
+enum { DSB_FLAG_GRAPH = 1u, DSB_FLAG_NO_CLIP = 2u, DSB_FLAG_KTIMING = 4u,
+       DSB_FLAG_SERIAL_LAYERS = 8u };
 
 typedef struct dsb_handle dsb_handle;
 

@@ -10,6 +10,10 @@
   dQ pass (parallel graph branches, or two streams in an eager cycle); the
   per-kernel timing mode runs them in order. All three give the same loss,
   gradients and masters bit for bit (the passes share only inputs).
+* Each layer's recompute runs on a third stream beside the backward of the
+  layer before it in the cycle, into the other of two buffer sets; with
+  ``backward_serial_layers`` it runs right before its own backward. Both
+  orders give the same loss, gradients and masters bit for bit.
 * A cleared GPU grant holds the cycle at a boundary until it is set again.
 * Every cycle ends by writing clamp(A) and clamp(s·B) (bf16) into the bound
   rows of vLLM's stacked LoRA buffers (trainer.py:760-802) and nothing else.
@@ -21,7 +25,7 @@ import time
 import pytest
 import torch
 
-from harness import O, bf16_round_acts, build_service, gpu_activations, tiny_meta
+from harness import O, bf16_round_acts, build_service, config_meta, gpu_activations, tiny_meta
 
 pytestmark = pytest.mark.gpu
 
@@ -211,3 +215,37 @@ def test_cycle_publishes_into_the_served_slot(segmented):
         _check_published(svc, bufs)
     finally:
         svc.close()
+
+
+@pytest.mark.parametrize("case", ["llama3", "qwen3", "c4s"])
+def test_layer_overlap_equals_serial(case):
+    """Three layers, two cycles. The c4s case (256 tokens at Qwen3-14B widths)
+    takes the split-K products and the skinny kernel's K split in the
+    recompute, whose scratch the side stream has its own copy of."""
+    if case == "c4s":
+        meta, seq = config_meta("c4s", L=3)
+        dev = "cuda"
+    else:
+        meta, seq, dev = tiny_meta(family=case, L=3), SEQ, "cpu"
+    model = O.make_model(meta, seed=3, w_std=0.02, b_std=0.01, device=dev)
+    n = sum(seq)
+    ids = torch.randint(0, meta["vocab_size"], (n,), generator=torch.Generator().manual_seed(3))
+    acts = bf16_round_acts(O.forward_capture(model, ids.to(dev), seq))
+    gacts = gpu_activations(acts, meta["max_saved_finetuning_tokens"])
+    del acts
+    family = meta["family"]
+    over = build_service(model, family)
+    serial = build_service(model, family, meta_extra={"backward_serial_layers": True})
+    try:
+        for _ in range(2):
+            l1, n1 = over.process_backward(gacts, seq, n, epoch=0)
+            l2, n2 = serial.process_backward(gacts, seq, n, epoch=0)
+            assert over.last_cycle_info["graph"] and serial.last_cycle_info["graph"]
+            assert n1 == n2 and l1 == l2, (l1, l2)
+            s1, s2 = _state(over), _state(serial)
+            for k in s1:
+                assert torch.equal(s1[k][0], s2[k][0]), ("master", k)
+                assert torch.equal(s1[k][1], s2[k][1]), ("grad", k)
+    finally:
+        over.close()
+        serial.close()
