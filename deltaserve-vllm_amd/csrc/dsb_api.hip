@@ -1245,6 +1245,26 @@ void use_set(dsb_handle* h, int k) {
   h->Zo_b = s.Zo_b; h->Zgu_b = s.Zgu_b; h->Zd_b = s.Zd_b; h->lse = s.lse;
 }
 
+// Layer li's recompute on the third stream (into set li & 1, with the side
+// scratch), forked from st; the caller joins it back before its segment ends.
+int fork_recompute(dsb_handle* h, int li, hipStream_t st) {
+  CK(hipEventRecord(h->ev_fork3, st));
+  CK(hipStreamWaitEvent(h->hs3, h->ev_fork3, 0));
+  use_set(h, li & 1);
+  std::swap(h->part, h->part2);
+  std::swap(h->tn_work, h->tn_work2);
+  const int rc = enqueue_layer(h, li, h->L - 1 - li, h->hs3, true, false);
+  std::swap(h->part, h->part2);
+  std::swap(h->tn_work, h->tn_work2);
+  return rc;
+}
+
+int join_recompute(dsb_handle* h, hipStream_t st) {
+  CK(hipEventRecord(h->ev_join3, h->hs3));
+  CK(hipStreamWaitEvent(st, h->ev_join3, 0));
+  return 0;
+}
+
 int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
   const int N = h->N, D = h->D;
   const int* nd = &h->d_hdr->n;
@@ -1263,6 +1283,11 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
         KScope ks(h, st, "lora_cast", 0, 0, 0, 0, 0, (double)h->cast_elems * 6.0);
         LK(lora_cast(h->d_jobs, h->d_cast_chunks, h->ncast_chunks, st));
       }
+      // with the layer overlap, the last layer's recompute (which needs the
+      // RoPE tables and the bf16 LoRA operands just written) runs beside the
+      // rest of this segment: the final norm, the labels and the first
+      // vocabulary chunk's logits
+      if (h->overlap && !h->ktiming) CKR(fork_recompute(h, h->L - 1, st));
       {
         KScope ks(h, st, "rmsnorm_fwd", 0, 0, 0, 4.0 * D, 0, 2.0 * D);
         LK(rmsnorm_fwd(h->final_in, h->act_ld, h->norm_w, h->normed, D, N, nd, D, eps, st));
@@ -1291,6 +1316,7 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
                   0, 0);
         LK(head_rescale(ha, c0, st));
       }
+      if (seg == 0 && h->overlap && !h->ktiming) CKR(join_recompute(h, st));
       return 0;
     }
     {
@@ -1318,30 +1344,19 @@ int enqueue_segment(dsb_handle* h, int seg, hipStream_t st) {
   if (seg < 2 * C + h->L) {
     const int lo = seg - 2 * C;  // layers done before this one in the cycle
     const int li = h->L - 1 - lo;
+    // with the overlap, this layer's recompute ran in the previous segment
+    // (the first layer's beside the head's first chunk)
     const bool ov = h->overlap && !h->ktiming;
-    if (lo == 0 || !ov) {
+    if (!ov) {
       use_set(h, li & 1);
       CKR(enqueue_layer(h, li, lo, st, true, false));
     }
     // the next layer's recompute (into the other set) beside this backward
     const bool fork = ov && li >= 1;
-    if (fork) {
-      CK(hipEventRecord(h->ev_fork3, st));
-      CK(hipStreamWaitEvent(h->hs3, h->ev_fork3, 0));
-      use_set(h, (li - 1) & 1);
-      std::swap(h->part, h->part2);
-      std::swap(h->tn_work, h->tn_work2);
-      const int rc = enqueue_layer(h, li - 1, lo + 1, h->hs3, true, false);
-      std::swap(h->part, h->part2);
-      std::swap(h->tn_work, h->tn_work2);
-      if (rc != 0) return rc;
-    }
+    if (fork) CKR(fork_recompute(h, li - 1, st));
     use_set(h, li & 1);
     CKR(enqueue_layer(h, li, lo, st, false, true));
-    if (fork) {
-      CK(hipEventRecord(h->ev_join3, h->hs3));
-      CK(hipStreamWaitEvent(st, h->ev_join3, 0));
-    }
+    if (fork) CKR(join_recompute(h, st));
     return 0;
   }
   // ---- per-layer clip + AdamW (trainer.py:624-636, :668)
